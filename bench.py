@@ -1,0 +1,328 @@
+"""Benchmark of the MI355X quantized-matmul / MoE hot path.
+
+Headline (BASELINE.json metric "MoE FP4 decode HBM GB/s (% of peak); FP8
+block GEMM TFLOP/s at M=128"):
+  value  = FP4 routed-MoE decode throughput, M=1 token, 384 experts, top-8,
+           hidden 4096, expert intermediate 2048, as
+           algorithmic HBM bytes per step / step time. A step is one token:
+           sigmoid routing from fp32 logits + bias, FP8 quantisation of x,
+           fused gate/up SwiGLU re-quantised to FP8, down projection and the
+           ascending-expert-id sum. Each step uses a different token, so the
+           eight experts it streams change from step to step (the 5.1 GB of
+           expert weights do not fit the 256 MB Infinity Cache).
+  fp8_gemm = M=128, K=4096, N in {4096, 12288, 2048} block-scaled FP8 GEMM
+           both scale formats, TFLOP/s per kernel launch,
+           weights rotated over > 256 MB of copies (cold).
+
+Timing: the steps are captured once into a HIP graph (one node per kernel,
+no allocation, no memset) and replayed; wall time between two device
+synchronisations brackets exactly `--steps` steps. Per-kernel durations for
+the roofline come from HIP events recorded on the launch stream around
+individual launches.
+
+    python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+E, DIM, INTER, TOPK = 384, 4096, 2048, 8
+PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5000.0
+FP4_MAT = INTER * DIM // 2          # packed bytes of one w1/w3/w2 matrix
+FP4_SC = INTER * DIM // 32          # UE8M0 bytes of one matrix
+EXPERT_BYTES = 3 * (FP4_MAT + FP4_SC)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_experts(L, torch, gen, dev):
+    """384 experts x (w1, w3, w2): N(0, 0.02) f32 generated on the device and
+    encoded by ws_weight_quant_fp4 (packed e2m1 + UE8M0 per 1x32)."""
+    w1 = torch.empty((E * INTER, DIM // 2), dtype=torch.uint8, device=dev)
+    s1 = torch.empty((E * INTER, DIM // 32), dtype=torch.uint8, device=dev)
+    w3 = torch.empty_like(w1)
+    s3 = torch.empty_like(s1)
+    w2 = torch.empty((E * DIM, INTER // 2), dtype=torch.uint8, device=dev)
+    s2 = torch.empty((E * DIM, INTER // 32), dtype=torch.uint8, device=dev)
+    buf = torch.empty((INTER, DIM), dtype=torch.float32, device=dev)
+    for e in range(E):
+        for w, s, rows, cols in ((w1, s1, INTER, DIM), (w3, s3, INTER, DIM),
+                                 (w2, s2, DIM, INTER)):
+            b = buf.view(rows, cols)
+            b.normal_(0.0, 0.02, generator=gen)
+            L.weight_quant_fp4(b, w[e * rows:(e + 1) * rows], s[e * rows:(e + 1) * rows],
+                               rows, cols)
+    torch.cuda.synchronize()
+    return w1, s1, w3, s3, w2, s2
+
+
+def bench_moe(L, torch, dev, steps, warmup, n_tokens, cpu_seconds):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    t0 = time.time()
+    slabs = make_experts(L, torch, gen, dev)
+    log("experts generated in %.1fs" % (time.time() - t0))
+    logits = torch.randn((n_tokens, E), device=dev, generator=gen)
+    bias = torch.randn((E,), device=dev, generator=gen) * 0.1
+    x = torch.randn((n_tokens, DIM), device=dev, generator=gen)
+    idx = torch.empty((n_tokens, TOPK), dtype=torch.int32, device=dev)
+    wts = torch.empty((n_tokens, TOPK), dtype=torch.float32, device=dev)
+    y = torch.empty((n_tokens, DIM), dtype=torch.float32, device=dev)
+    ws = torch.empty(L.moe_decode_workspace_size(DIM, INTER, TOPK), dtype=torch.uint8, device=dev)
+
+    def step(t, stream):
+        L.moe_topk(logits[t], bias, None, idx[t], wts[t], 1, E, TOPK, L.SCORE_SIGMOID, 1.0, True,
+                   1.0, stream=stream)
+        L.moe_decode(x[t], idx[t], wts[t], *slabs, y[t], DIM, INTER, E, TOPK, ws, stream=stream)
+
+    # eager pass: results for the parity check and the per-kernel timing inputs
+    s = torch.cuda.current_stream()
+    for t in range(n_tokens):
+        step(t, s)
+    torch.cuda.synchronize()
+    y_eager = y.clone()
+
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(g, stream=cs):
+            for t in range(n_tokens):
+                step(t, cs)
+    torch.cuda.synchronize()
+    reps_w = max(1, math.ceil(warmup / n_tokens))
+    for _ in range(reps_w):
+        g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(y, y_eager):
+        raise RuntimeError("graph replay differs from the eager pass")
+    reps = max(1, math.ceil(steps / n_tokens))
+    done = reps * n_tokens
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / done
+    step_bytes = TOPK * EXPERT_BYTES + 2 * E * 4 + 2 * DIM * 4
+    gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # per-kernel durations with events on the launch stream
+    w1, s1, w3, s3, w2, s2 = slabs
+    xq = torch.empty((n_tokens, DIM), dtype=torch.uint8, device=dev)
+    xs = torch.empty((n_tokens, DIM // 32), dtype=torch.uint8, device=dev)
+    hq = torch.empty((n_tokens, TOPK, INTER), dtype=torch.uint8, device=dev)
+    hs = torch.empty((n_tokens, TOPK, INTER // 32), dtype=torch.uint8, device=dev)
+    for t in range(n_tokens):
+        L.emit8(x[t], xq[t], xs[t], DIM, stream=s)
+    torch.cuda.synchronize()
+
+    def timed(fn, reps_k):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps_k)]
+        for i in range(reps_k):
+            t = i % n_tokens
+            ev[i][0].record(s)
+            fn(t)
+            ev[i][1].record(s)
+        torch.cuda.synchronize()
+        ms = [a.elapsed_time(b) for a, b in ev]
+        ms.sort()
+        return sum(ms) / len(ms), ms[len(ms) // 2]
+
+    glu = lambda t: L.expert_glu_quant(xq[t], xs[t], idx[t], wts[t], w1, s1, w3, s3, hq[t], hs[t],
+                                       INTER, DIM, E, TOPK, stream=s)
+    red = lambda t: L.expert_reduce(hq[t], hs[t], w2, s2, idx[t], y[t], DIM, INTER, E, TOPK,
+                                    stream=s)
+    for t in range(n_tokens):
+        glu(t)
+    reps_k = max(200, n_tokens)
+    glu_avg, glu_med = timed(glu, reps_k)
+    red_avg, red_med = timed(red, reps_k)
+    glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + DIM + DIM // 32 + TOPK * (INTER + INTER // 32)
+    red_bytes = TOPK * (FP4_MAT + FP4_SC) + TOPK * (INTER + INTER // 32) + DIM * 4
+    kern = {
+        "expert_glu_quant_kernel": {"avg_us": glu_avg * 1e3, "median_us": glu_med * 1e3,
+                                    "bytes": glu_bytes,
+                                    "GB/s": glu_bytes / (glu_avg * 1e-3) / 1e9},
+        "expert_reduce_kernel": {"avg_us": red_avg * 1e3, "median_us": red_med * 1e3,
+                                 "bytes": red_bytes,
+                                 "GB/s": red_bytes / (red_avg * 1e-3) / 1e9},
+    }
+    torch.cuda.synchronize()
+    return dict(ms_per_step=ms_per_step, gbs=gbs, step_bytes=step_bytes, kernels=kern,
+                slabs=slabs, logits=logits, bias=bias, x=x, idx=idx, wts=wts, y=y_eager,
+                steps=done)
+
+
+def cpu_baseline_moe(res, seconds):
+    """The C oracle's routed MoE (restatement of weightstream-ref moe.rs,
+    single thread) on the same tokens, timed over about `seconds` of CPU
+    work. Returns (GB/s-equivalent, tokens, max rel err of the GPU steps
+    checked on the way)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    shapes = [(INTER, DIM // 2), (INTER, DIM // 32), (INTER, DIM // 2), (INTER, DIM // 32),
+              (DIM, INTER // 2), (DIM, INTER // 32)]
+    views = [t.view(E, *shp) for t, shp in zip(res["slabs"], shapes)]
+    host = [np.zeros((E,) + shp, np.uint8) for shp in shapes]
+    logits = res["logits"].cpu().numpy()
+    bias = res["bias"].cpu().numpy()
+    xs = res["x"].cpu().numpy()
+    gidx, gw, gy = res["idx"].cpu().numpy(), res["wts"].cpu().numpy(), res["y"].cpu().numpy()
+    spent, n, worst, route_ok = 0.0, 0, 0.0, True
+    while spent < seconds and n < len(xs):
+        t = n
+        for e in gidx[t]:
+            for h, v in zip(host, views):
+                h[e] = v[e].cpu().numpy()
+        c0 = time.perf_counter()
+        ri, rw = O.route(O.score(logits[t], O.SCORE_SIGMOID), bias, TOPK)
+        yref = O.moe_routed(*host, DIM, INTER, xs[t], ri, rw)
+        spent += time.perf_counter() - c0
+        route_ok &= bool(np.array_equal(ri, gidx[t]) and
+                         np.array_equal(rw.view(np.uint32), gw[t].view(np.uint32)))
+        err = np.abs(gy[t] - yref).max() / max(np.abs(yref).max(), 1e-30)
+        worst = max(worst, float(err))
+        n += 1
+    step_bytes = res["step_bytes"]
+    return step_bytes * n / spent / 1e9, n, spent, worst, route_ok
+
+
+def bench_gemm(L, torch, dev, reps):
+    """Config 2: M=128, K=4096 FP8 block-scaled GEMM (act quant + GEMM per
+    step), cold weights (rotated over > 256 MB of copies)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    M, K = 128, 4096
+    out = {}
+    x = torch.randn((M, K), device=dev, generator=gen)
+    x = torch.where(torch.rand((M, K), device=dev, generator=gen) < 0.01, x * 20, x)
+    aq8 = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    aqf = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    as8 = torch.empty((M, K // 32), dtype=torch.uint8, device=dev)
+    asf = torch.empty((M, K // 128), dtype=torch.float32, device=dev)
+    L.emit8(x, aq8, as8, M * K)
+    L.act_quant_f32s(x, aqf, asf, M, K)
+    s = torch.cuda.current_stream()
+    for N in (4096, 12288, 2048):
+        copies = max(2, math.ceil(400e6 / (N * K)))
+        w = torch.randn((N, K), device=dev, generator=gen) * 0.02
+        wq = torch.empty((copies, N, K), dtype=torch.uint8, device=dev)
+        ws8 = torch.empty((copies, N // 32, K // 32), dtype=torch.uint8, device=dev)
+        wsf = torch.empty((copies, N // 128, K // 128), dtype=torch.float32, device=dev)
+        for c in range(copies):
+            L.weight_quant_fp8(w, wq[c], ws8[c], N, K)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        flops = 2.0 * M * N * K
+        res = {}
+        for fmt in ("ue8m0_32", "f32_128"):
+            if fmt == "f32_128":
+                # f32 block scales for the same codes (timing only)
+                wsf.fill_(0.02 / 448)
+            def run(c):
+                if fmt == "ue8m0_32":
+                    L.fp8_gemm_bf16(aq8, as8, wq[c], ws8[c], y, M, N, K, stream=s)
+                else:
+                    L.fp8_gemm_f32s(aqf, asf, wq[c], wsf[c], y, M, N, K, out_bf16=True, stream=s)
+            for c in range(copies):
+                run(c)
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(reps)]
+            for i in range(reps):
+                ev[i][0].record(s)
+                run(i % copies)
+                ev[i][1].record(s)
+            torch.cuda.synchronize()
+            ms = sorted(a.elapsed_time(b) for a, b in ev)
+            avg = sum(ms) / len(ms)
+            bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 2
+            res[fmt] = {"avg_us": avg * 1e3, "median_us": ms[len(ms) // 2] * 1e3,
+                        "TFLOP/s": flops / (avg * 1e-3) / 1e12,
+                        "frac_fp8_peak": flops / (avg * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
+                        "GB/s": bytes_ / (avg * 1e-3) / 1e9,
+                        "frac_hbm_peak": bytes_ / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS}
+        out[str(N)] = res
+        del wq, ws8, wsf
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--tokens", type=int, default=64, help="distinct tokens cycled by the steps")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the hot path is built and measured on a single "
+              "MI355X (expert-parallel sharding across GPUs is not part of this build); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from weightstream_amd import launch as L
+    L.Hip.global_()
+    dev = "cuda:0"
+    log("device:", torch.cuda.get_device_name(0))
+
+    res = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, args.cpu_seconds)
+    k = res["kernels"]["expert_glu_quant_kernel"]
+    roof = {"kernel": "expert_glu_quant_kernel", "bound": "hbm", "achieved": k["GB/s"],
+            "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["GB/s"] / PEAK_HBM_GBS,
+            "traffic": None}
+    cpu = None
+    if not args.no_cpu:
+        import multiprocessing
+        gbs, n, spent, worst, route_ok = cpu_baseline_moe(res, args.cpu_seconds)
+        cpu = {"value": gbs, "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": "%d tokens of the same workload (%.1f s of CPU), C oracle "
+                         "restating weightstream-ref moe.rs/actquant.rs, 1 thread; host has "
+                         "%d CPUs" % (n, spent, multiprocessing.cpu_count()),
+               "tokens_per_s": n / spent}
+        log("parity on %d tokens: routing bit-exact=%s, max rel err %.2e" % (n, route_ok, worst))
+        if not route_ok or worst > 1e-3:
+            raise RuntimeError("GPU results differ from the oracle")
+    gemm = None if args.no_gemm else bench_gemm(L, torch, dev, 200)
+
+    line = {
+        "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
+        "value": res["gbs"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": res["steps"],
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp4xfp8",
+        "data": "synthetic: N(0,0.02) weights encoded e2m1+UE8M0 1x32, N(0,1) tokens, "
+                "N(0,1) logits + N(0,0.1) bias, seed 0",
+        "config": {"workload": "fp4_moe_decode_m1", "experts": E, "top_k": TOPK, "hidden": DIM,
+                   "inter": INTER, "score": "sigmoid", "swiglu_limit": 10.0,
+                   "bytes_per_step": res["step_bytes"], "frac_hbm_peak":
+                   res["gbs"] / PEAK_HBM_GBS, "tokens_per_s": 1e3 / res["ms_per_step"]},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": res["kernels"],
+        "fp8_gemm_m128": gemm,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,189 @@
+/* weightstream-hip: C ABI of the MI355X (gfx950) quantized-matmul / MoE hot
+ * path. Drop-in replacement for the kernel launches that weightstream-gpu's
+ * launch.rs issues on weightstream-cuda today.
+ *
+ * Conventions (those of launch.rs, weightstream-gpu/src/launch.rs:1-33):
+ *  - every pointer is a device pointer the caller owns; kernels never allocate
+ *    (the fused MoE drivers take a caller workspace, sized by *_workspace_size);
+ *  - every call is stream-ordered and asynchronous on `stream` (NULL = the
+ *    default stream), like the `*_on` variants of launch.rs;
+ *  - outputs are written in full, never accumulated into;
+ *  - the return value is 0 on success, a hipError_t (1..999) if the launch
+ *    failed, or one of the WS_ERR_* codes below if the arguments are rejected
+ *    before anything is launched. launch.rs panics (`.unwrap()`) on failure;
+ *    the host mirrors (include/ws_hip.hpp, weightstream_amd/launch.py) throw.
+ *
+ * Formats (weightstream-core/src/quant.rs:1-215): e4m3fn bytes; packed e2m1,
+ * low nibble = even K; UE8M0 scale bytes 2^(b-127). Activations carry one
+ * UE8M0 scale per 1x32 K block ([M, K/32]); FP8 weights one per 32x32 block
+ * ([ceil(N/32), K/32]); FP4 weights one per row per 32 K ([N, K/32]).
+ * Shapes: K must be a multiple of 128 and N a multiple of 16.
+ */
+#ifndef WS_HIP_H
+#define WS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *ws_stream_t;
+
+#define WS_OK 0
+#define WS_ERR_INVALID_ARG 1001   /* null pointer or non-positive size */
+#define WS_ERR_SHAPE 1002         /* shape outside what the kernels support */
+#define WS_ERR_NO_DEVICE 1003     /* no gfx950 device */
+
+/* Score functions of weightstream-ref moe.rs:29-42. */
+#define WS_SCORE_SOFTMAX 0
+#define WS_SCORE_SIGMOID 1
+#define WS_SCORE_SQRTSOFTPLUS 2
+
+/* ---------------------------------------------------------------------
+ * Runtime. Replaces weightstream_cuda::gpu::Cuda::global() (gpu.rs:42-187):
+ * code objects are linked in, so init only validates the device.
+ * ------------------------------------------------------------------- */
+/* Checks that the current device is gfx950. lib.rs:11-13 built_with_cuda(). */
+int ws_init(void);
+int ws_built_with_hip(void);
+const char *ws_error_string(int code);
+/* Device ws_expf over the 32-bit patterns [lo, lo+n): out[i] = bits(expf(x)).
+ * Test hook for the exhaustive host/device expf agreement check. */
+int ws_expf_probe(uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Activation quantisation (weightstream-cuda/kernels/actquant.cu).
+ * ------------------------------------------------------------------- */
+/* launch.rs:296-301 snap8 -> act_quant_ue8m0_snap: in-place FP8 snap of
+ * f32 x[n], n % 32 == 0 (weightstream-ref actquant.rs:21 fp8_snap). */
+int ws_snap8(float *x, int64_t n, ws_stream_t stream);
+/* launch.rs:303-308 emit8 -> act_quant_fp8_emit: x[n] -> q[n] e4m3 and
+ * s[n/32] UE8M0. Bit-exact with weightstream-ref's fp8 act quant. */
+int ws_emit8(const float *x, uint8_t *q, uint8_t *s, int64_t n, ws_stream_t stream);
+/* launch.rs:310-318 emit8_packed: as emit8, and also writes the scales again
+ * at s + round_up(n/32, 16) (the packed-scale tail of the reference). */
+int ws_emit8_packed(const float *x, uint8_t *q, uint8_t *s, int64_t n, ws_stream_t stream);
+/* launch.rs:320-326 pack_scales -> pack_scale_words: four UE8M0 bytes per
+ * little-endian u32 word, n/128 words. */
+int ws_pack_scales(const uint8_t *src, uint32_t *dst, int64_t n, ws_stream_t stream);
+
+/* Weight encoders (weightstream-ref store.rs:357-422, with the amax taken
+ * over the whole block): f32 w[rows, cols] ->
+ *  fp4: packed e2m1 q[rows, cols/2] + UE8M0 s[rows, cols/32] (amax floor
+ *       6*2^-126, scale 2^log2_ceil(amax/6), clamp +-6);
+ *  fp8: e4m3 q[rows, cols] + UE8M0 s[ceil(rows/32), cols/32] per 32x32 block
+ *       (amax floor 1e-4, scale 2^log2_ceil(amax/448), clamp +-448). */
+int ws_weight_quant_fp4(const float *w, uint8_t *q, uint8_t *s, int64_t rows, int64_t cols,
+                        ws_stream_t stream);
+int ws_weight_quant_fp8(const float *w, uint8_t *q, uint8_t *s, int64_t rows, int64_t cols,
+                        ws_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Block-scaled GEMM: C[M,N] = A[M,K] . B[N,K]^T, f32 accumulate.
+ * One MFMA kernel family covers the reference's fp8_gemm (M=1 decode),
+ * fp8_gemm_tile (M-batch) and the TileLang gemm_mxfp8 kernels.
+ * ------------------------------------------------------------------- */
+/* launch.rs:717-742 fp8_gemm(_on) (fp8_gemm.cu:9): A e4m3 + sa[M,K/32],
+ * B e4m3 + sb[ceil(N/32),K/32], C f32 [M,N]. */
+int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* launch.rs:744-767 fp8_gemm_tile (fp8_gemm_tile.cu:28): same contract. */
+int ws_fp8_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* launch.rs:344-377 fp8_gemm_tl(_on) takes packed u32 scale words and a
+ * shape enum; this entry takes the raw UE8M0 bytes of fp8_gemm and any
+ * (N,K), and writes bf16 (RNE, quant.rs:95-101) instead of f32. */
+int ws_fp8_gemm_bf16(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     uint16_t *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* f32-scale block scheme (no reference counterpart; generalises fp8_gemm to
+ * the 1xB activation / BxB weight f32 scales of DeepSeek-style checkpoints,
+ * block = 128): sa f32 [M,K/128], sb f32 [ceil(N/128),K/128]. out_bf16 selects
+ * bf16 (uint16_t*) instead of f32 output. */
+int ws_fp8_gemm_f32s(const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+                     void *out, int out_bf16, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* Activation quantisation for the f32-scale scheme: per 1x128 block,
+ * s = max(amax,1e-4)/448, q = e4m3(clamp(x/s, +-448)). */
+int ws_act_quant_f32s(const float *x, uint8_t *q, float *s, int64_t m, int64_t k,
+                      ws_stream_t stream);
+/* launch.rs:769-779 fp4_gemm (fp4_expert_gemm.cu:9): A e4m3 + sa[M,K/32],
+ * B packed e2m1 [N,K/2] + sb[N,K/32], C f32 [M,N]. */
+int ws_fp4_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* launch.rs:781-804 fp4_gemm_tile (fp4_gemm_tile.cu:21): same contract. */
+int ws_fp4_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * MoE routing (weightstream-cuda/kernels/moe.cu; CPU: weightstream-ref
+ * moe.rs:20-69). Selection and weights are bit-exact with the CPU path for
+ * softmax and sigmoid (a shared expf, sequential-order dots and sums).
+ * ------------------------------------------------------------------- */
+/* Gate logits, num::gemv order (num.rs:18-28: one sequential dot per expert):
+ * logits[M,E] = x[M,dim] . W[E,dim]^T, W f32 (w_bf16 = 0) or bf16. */
+int ws_moe_gate_logits(const float *x, const void *gate_w, int w_bf16, float *logits,
+                       int64_t m, int64_t dim, int64_t n_experts, ws_stream_t stream);
+/* Scores + top-k + weights for M rows (moe.rs:24-69): scores = score_func(
+ * logits / gate_temp); top-k of scores+bias by (value desc, index asc) under
+ * f32 total order; weights = scores of the picks, / (sum + 1e-20) when
+ * norm_topk_prob && top_k > 1, * route_scale. scores_out may be NULL.
+ * E <= 1024, top_k <= 16. */
+int ws_moe_topk(const float *logits, const float *bias, float *scores_out, int32_t *out_idx,
+                float *out_w, int64_t m, int64_t n_experts, int64_t top_k, int score_func,
+                float gate_temp, int norm_topk_prob, float route_scale, ws_stream_t stream);
+/* launch.rs:998-1018 moe_gate (moe.cu:18): bf16 gate, sqrtsoftplus scores[E]
+ * for one token (bias unused, as in the reference kernel). */
+int ws_moe_gate(const float *x, const uint16_t *gate_w, const float *bias, float *scores,
+                int64_t dim, int64_t n_experts, ws_stream_t stream);
+/* launch.rs:1020-1041 moe_gate_m (moe.cu:160): M rows, scores[M,E]. */
+int ws_moe_gate_m(const float *x, const uint16_t *gate_w, const float *bias, float *scores,
+                  int64_t m, int64_t dim, int64_t n_experts, ws_stream_t stream);
+/* launch.rs:1043-1066 moe_select (moe.cu:48): top-k of scores+bias, weights
+ * normalised by (sum + 1e-20) and * route_scale. scores is not modified
+ * (the reference kernel overwrites taken entries; callers must not rely on
+ * either). */
+int ws_moe_select(const float *scores, const float *bias, float *out_w, int32_t *out_idx,
+                  int64_t n_experts, int64_t top_k, float route_scale, ws_stream_t stream);
+/* launch.rs:1068-1093 moe_route (moe.cu:100): gate + select fused. */
+int ws_moe_route(const float *x, const uint16_t *gate_w, const float *bias, float *out_w,
+                 int32_t *out_idx, int64_t dim, int64_t n_experts, int64_t top_k,
+                 float route_scale, ws_stream_t stream);
+/* launch.rs:1095-1100 swiglu (moe.cu:143 swiglu_limit10):
+ * out = silu(min(g,10)) * clamp(u,-10,10) * rw, in moe.rs:187-201's order. */
+int ws_swiglu(const float *gate, const float *up, float *out, int64_t n, float rw,
+              ws_stream_t stream);
+
+/* ---------------------------------------------------------------------
+ * Routed experts, M = 1 decode (moe.rs:75-84,162-208; moe_grouped.cu:61-224).
+ * Expert slabs: w1/w3 packed e2m1 [E, inter, dim/2] + UE8M0 [E, inter, dim/32];
+ * w2 [E, dim, inter/2] + [E, dim, inter/32]. topk_idx/topk_w as ws_moe_topk
+ * writes them (top-k order); kernels sort the picks by ascending expert id.
+ * ------------------------------------------------------------------- */
+/* Fused expert_glu + expert_quant (moe_grouped.cu:61,128): for each pick p
+ * (rank r by ascending expert id) h = silu(min(w1.x,L)) * clamp(w3.x,+-L) * w_p,
+ * then FP8 1x32 quantisation of h: hq[r, inter] e4m3, hs[r, inter/32].
+ * x is the quantised token (xq[dim], xs[dim/32], as ws_emit8 writes). */
+int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *topk_idx,
+                        const float *topk_w, const uint8_t *w1, const uint8_t *s1,
+                        const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                        int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                        float swiglu_limit, ws_stream_t stream);
+/* expert_reduce (moe_grouped.cu:165, launch.rs:178-206): y[dim] = sum over
+ * picks in ascending expert id of w2_e . h_e, one f32 add per expert. */
+int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
+                     const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
+                     int64_t inter, int64_t n_experts, int64_t top_k, ws_stream_t stream);
+/* Whole routed MoE for one token from f32 x: emit8(x) -> glu_quant -> reduce.
+ * workspace >= ws_moe_decode_workspace_size(dim, inter, top_k) bytes. */
+size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k);
+int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,
+                  const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
+                  const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim, int64_t inter,
+                  int64_t n_experts, int64_t top_k, float swiglu_limit, void *workspace,
+                  size_t workspace_bytes, ws_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,8 +1,8 @@
 /* Exhaustive comparison of ws_expf (weightstream_amd/csrc/ws_expf.h) with the
  * host libm expf over every 32-bit pattern in [lo, hi). Test infrastructure:
- * called by tests/test_oracle_expf.py. Also folds glibc's results into an
- * order-independent checksum that the GPU test compares its device results
- * against. */
+ * called by tests/test_oracle_expf.py and tests/test_gpu_route.py (glibc's
+ * results, raw or folded into a digest, are what the device ws_expf is
+ * compared against). */
 #include <math.h>
 #include <stdint.h>
 #include "../weightstream_amd/csrc/ws_expf.h"
@@ -19,20 +19,25 @@ uint64_t ws_expf_mismatches(uint64_t lo, uint64_t hi) {
     return mism;
 }
 
-/* sum over u in [lo,hi) of mix(u, bits(expf(u))) mod 2^64, NaNs canonical */
-static inline uint64_t mix(uint64_t u, uint32_t r) {
-    uint64_t z = (u << 32) ^ r;
-    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-    return z ^ (z >> 31);
+/* glibc expf bits for the 32-bit patterns [lo, lo+n) (NaNs canonical). */
+void glibc_expf_bits(uint32_t lo, uint32_t n, uint32_t *out) {
+#pragma omp parallel for schedule(static, 1 << 16)
+    for (long long i = 0; i < (long long)n; i++) {
+        float r = expf(ws_u2f(lo + (uint32_t)i));
+        out[i] = (r != r) ? 0x7fc00000u : ws_f2u(r);
+    }
 }
-uint64_t glibc_expf_checksum(uint64_t lo, uint64_t hi) {
+
+/* sum over u in [lo,hi) of (bits(expf(u)) ^ (u * 0x9E3779B1)) * (2u+1) mod
+ * 2^64, NaNs canonical: an order-independent digest that a GPU can compute
+ * with wrapping int64 arithmetic. */
+uint64_t glibc_expf_digest(uint64_t lo, uint64_t hi) {
     uint64_t acc = 0;
 #pragma omp parallel for reduction(+ : acc) schedule(static, 1 << 16)
     for (long long u = (long long)lo; u < (long long)hi; u++) {
         float r = expf(ws_u2f((uint32_t)u));
         uint32_t b = (r != r) ? 0x7fc00000u : ws_f2u(r);
-        acc += mix((uint64_t)u, b);
+        acc += (uint64_t)(b ^ (uint32_t)((uint32_t)u * 0x9E3779B1u)) * (2 * (uint64_t)u + 1);
     }
     return acc;
 }

@@ -310,6 +310,8 @@ def expfcheck():
         _expf_lib = _load("libexpfcheck.so")
         _expf_lib.ws_expf_mismatches.restype = C.c_uint64
         _expf_lib.ws_expf_mismatches.argtypes = [C.c_uint64, C.c_uint64]
-        _expf_lib.glibc_expf_checksum.restype = C.c_uint64
-        _expf_lib.glibc_expf_checksum.argtypes = [C.c_uint64, C.c_uint64]
+        _expf_lib.glibc_expf_digest.restype = C.c_uint64
+        _expf_lib.glibc_expf_digest.argtypes = [C.c_uint64, C.c_uint64]
+        _expf_lib.glibc_expf_bits.restype = None
+        _expf_lib.glibc_expf_bits.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p]
     return _expf_lib

@@ -1,0 +1,194 @@
+"""GPU parity: activation/weight quantisation and the block-scaled GEMMs,
+called through the C ABI (weightstream_amd.launch) and checked against the
+C oracle on the same seeded inputs.
+
+Tolerances: quantisation is integer/byte work and must be bit-exact. GEMM
+outputs are f32 sums of exact fp8 x fp8 (or fp8 x fp4) products; the MFMA
+accumulation order differs from the oracle's sequential per-32-block order,
+so outputs are compared with max relative error <= 1e-3 (floor at 1% of the
+output scale, see gpu_util.rel_err_stats); observed errors are ~1e-6.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_util import DEV, activations, announce, assert_close, dev, host
+from weightstream_amd import launch as L
+
+pytestmark = pytest.mark.gpu
+
+GEMM_TOL = 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    L.Hip.global_()
+
+
+def _wide_range_acts(rng, n):
+    x = rng.standard_normal(n).astype(np.float32)
+    x *= np.repeat(10.0 ** rng.uniform(-7, 4, n // 32), 32).astype(np.float32)
+    x[:32] = 0.0                                   # zero block -> amax floor
+    x[32:64] = np.float32(15.2 / 1024) * np.sign(rng.standard_normal(32))  # carry quirk
+    x[32] = 448.0                                  # scale 1: the rest sit in [15/1024, 2^-6)
+    x[70] = np.float32(np.nan)
+    x[100] = np.float32(1e30)
+    return x
+
+
+def test_emit8_and_snap8_bit_exact():
+    rng = np.random.default_rng(100)
+    n = 32 * 4096
+    x = _wide_range_acts(rng, n)
+    q_ref, s_ref = O.fp8_act_emit(x)
+    announce("emit8 n=%d" % n)
+    dx = dev(x)
+    q = torch.empty(n, dtype=torch.uint8, device=DEV)
+    s = torch.empty(n // 32, dtype=torch.uint8, device=DEV)
+    L.emit8(dx, q, s, n)
+    assert np.array_equal(host(q), q_ref)
+    assert np.array_equal(host(s), s_ref)
+    announce("snap8 n=%d" % n)
+    L.snap8(dx, n)
+    got = host(dx)
+    want = O.fp8_snap(x)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_emit8_packed_and_pack_scales():
+    rng = np.random.default_rng(101)
+    n = 32 * 100
+    x = rng.standard_normal(n).astype(np.float32)
+    q_ref, s_ref = O.fp8_act_emit(x)
+    raw = n // 32
+    off = (raw + 15) // 16 * 16
+    announce("emit8_packed n=%d" % n)
+    q = torch.empty(n, dtype=torch.uint8, device=DEV)
+    s = torch.zeros(off + raw, dtype=torch.uint8, device=DEV)
+    L.emit8_packed(dev(x), q, s, n)
+    sh = host(s)
+    assert np.array_equal(host(q), q_ref)
+    assert np.array_equal(sh[:raw], s_ref) and np.array_equal(sh[off:off + raw], s_ref)
+    n2 = 128 * 7
+    src = rng.integers(0, 256, n2 // 32).astype(np.uint8)
+    dst = torch.empty(n2 // 128, dtype=torch.int32, device=DEV)
+    L.pack_scales(dev(src), dst, n2)
+    assert np.array_equal(host(dst).view(np.uint32), src.view("<u4"))
+
+
+def test_weight_quant_bit_exact():
+    rng = np.random.default_rng(102)
+    rows, cols = 200, 512
+    w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    w[3, 5] = 7.0
+    w[40:72, 64:96] = 0.0
+    announce("weight_quant fp4/fp8 %dx%d" % (rows, cols))
+    q4 = torch.empty((rows, cols // 2), dtype=torch.uint8, device=DEV)
+    s4 = torch.empty((rows, cols // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp4(dev(w), q4, s4, rows, cols)
+    q4r, s4r = O.weight_quant_fp4(w)
+    assert np.array_equal(host(q4), q4r) and np.array_equal(host(s4), s4r)
+    q8 = torch.empty((rows, cols), dtype=torch.uint8, device=DEV)
+    s8 = torch.empty(((rows + 31) // 32, cols // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(dev(w), q8, s8, rows, cols)
+    q8r, s8r = O.weight_quant_fp8(w)
+    assert np.array_equal(host(q8), q8r) and np.array_equal(host(s8), s8r)
+
+
+def _quantised_case(rng, m, n, k, fp4):
+    x = activations(rng, m, k)
+    aq, as_ = O.fp8_act_emit(x)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wq, ws = O.weight_quant_fp4(wf) if fp4 else O.weight_quant_fp8(wf)
+    return aq, as_, wq, ws
+
+
+GEMM_SHAPES = [(1, 4096, 4096), (1, 1024, 2048), (4, 256, 512), (16, 512, 1024),
+               (17, 96, 384), (64, 256, 1024), (128, 512, 4096), (130, 48, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
+def test_fp8_gemm_matches_oracle(m, n, k):
+    rng = np.random.default_rng(1000 + m + n + k)
+    aq, as_, wq, ws = _quantised_case(rng, m, n, k, False)
+    want = O.gemm_q(aq, as_, m, wq, ws, n, k, False)
+    announce("fp8_gemm m=%d n=%d k=%d" % (m, n, k))
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm(dev(aq), dev(as_), dev(wq), dev(ws), out, m, n, k)
+    assert_close(host(out), want, GEMM_TOL, "fp8_gemm %dx%dx%d" % (m, n, k))
+    announce("fp8_gemm_bf16 m=%d n=%d k=%d" % (m, n, k))
+    ob = torch.empty((m, n), dtype=torch.int16, device=DEV)
+    L.fp8_gemm_bf16(dev(aq), dev(as_), dev(wq), dev(ws), ob, m, n, k)
+    got = (host(ob).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    # bf16 keeps 8 significant bits: RNE error <= 2^-9 relative
+    assert_close(got, want, 2.0 ** -9 + GEMM_TOL, "fp8_gemm_bf16 %dx%dx%d" % (m, n, k))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (8, 512, 1024), (128, 256, 2048),
+                                   (33, 80, 512)])
+def test_fp4_gemm_matches_oracle(m, n, k):
+    rng = np.random.default_rng(2000 + m + n + k)
+    aq, as_, wq, ws = _quantised_case(rng, m, n, k, True)
+    want = O.gemm_q(aq, as_, m, wq, ws, n, k, True)
+    announce("fp4_gemm m=%d n=%d k=%d" % (m, n, k))
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp4_gemm(dev(aq), dev(as_), dev(wq), dev(ws), out, m, n, k)
+    assert_close(host(out), want, GEMM_TOL, "fp4_gemm %dx%dx%d" % (m, n, k))
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (128, 384, 4096), (20, 256, 512)])
+def test_fp8_gemm_f32s_matches_oracle(m, n, k):
+    rng = np.random.default_rng(3000 + m + n + k)
+    x = activations(rng, m, k)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wq, ws = O.weight_quant_fp8_f32s(wf, 128)
+    aq_ref, as_ref = O.act_quant_f32s(x, 128)
+    want = O.gemm_f32s(aq_ref, as_ref, wq, ws, 128)
+    announce("act_quant_f32s + fp8_gemm_f32s m=%d n=%d k=%d" % (m, n, k))
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    as_ = torch.empty((m, k // 128), dtype=torch.float32, device=DEV)
+    L.act_quant_f32s(dev(x), aq, as_, m, k)
+    assert np.array_equal(host(aq), aq_ref)
+    assert np.array_equal(host(as_).view(np.uint32), as_ref.view(np.uint32))
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm_f32s(aq, as_, dev(wq), dev(ws), out, m, n, k)
+    assert_close(host(out), want, GEMM_TOL, "fp8_gemm_f32s %dx%dx%d" % (m, n, k))
+
+
+@pytest.mark.parametrize("n", [4096, 12288, 2048])
+def test_fp8_gemm_full_size_vs_fp64_dequant(n):
+    """BASELINE config 2 shapes (M=128, K=4096) against an f64 matmul of the
+    dequantised operands on the device (too large for the scalar oracle)."""
+    m, k = 128, 4096
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(n)
+    announce("fp8_gemm full m=%d n=%d k=%d" % (m, n, k))
+    x = torch.randn((m, k), device=DEV, generator=gen)
+    x = torch.where(torch.rand((m, k), device=DEV, generator=gen) < 0.01, x * 20, x)
+    w = torch.randn((n, k), device=DEV, generator=gen) * 0.02
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    as_ = torch.empty((m, k // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, aq, as_, m * k)
+    wq = torch.empty((n, k), dtype=torch.uint8, device=DEV)
+    ws = torch.empty((n // 32, k // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(w, wq, ws, n, k)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm(aq, as_, wq, ws, out, m, n, k)
+    table = torch.from_numpy(O.e4m3_decode_table().astype(np.float64)).to(DEV)
+    pw = lambda s: torch.pow(2.0, s.to(torch.float64) - 127)
+    da = table[aq.long()] * pw(as_).repeat_interleave(32, 1)
+    dw = table[wq.long()] * pw(ws).repeat_interleave(32, 0).repeat_interleave(32, 1)
+    want = (da @ dw.T).cpu().numpy()
+    assert_close(host(out), want, GEMM_TOL, "fp8_gemm full %dx%dx%d" % (m, n, k))
+
+
+def test_gemm_rejects_bad_shapes():
+    a = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    out = torch.zeros(256, dtype=torch.float32, device=DEV)
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        L.fp8_gemm(a, a, a, a, out, 1, 16, 100)     # K % 128 != 0
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        L.fp8_gemm(a, a, a, a, out, 1, 10, 128)     # N % 16 != 0

@@ -1,0 +1,162 @@
+"""GPU parity of the routed FP4 MoE for one token (weightstream-ref moe.rs:
+75-84, 162-208): fused gate/up + SwiGLU + FP8 re-quantisation, down
+projection and the ascending-expert-id sum, against the C oracle.
+
+Tolerance: max relative error <= 1e-3 on the f32 output (floor at 1% of the
+output scale). The GPU's gate/up sums differ from the oracle's by f32
+reassociation only; re-quantising h to FP8 can move a value that sits on a
+rounding boundary by one e4m3 step, which the tolerance covers.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_util import DEV, announce, assert_close, dev, host, rand_fp4_weights
+from weightstream_amd import launch as L
+
+pytestmark = pytest.mark.gpu
+MOE_TOL = 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    L.Hip.global_()
+
+
+def _slabs(gen, E, dim, inter):
+    w1, s1 = rand_fp4_weights(gen, E * inter, dim)
+    w3, s3 = rand_fp4_weights(gen, E * inter, dim)
+    w2, s2 = rand_fp4_weights(gen, E * dim, inter)
+    return w1, s1, w3, s3, w2, s2
+
+
+def _host_experts(slabs, experts, E, dim, inter):
+    """Copy only the picked experts to the host, placed at their ids in
+    zero-filled slabs of E experts (the oracle indexes by expert id)."""
+    w1, s1, w3, s3, w2, s2 = slabs
+    shapes = [(inter, dim // 2), (inter, dim // 32), (inter, dim // 2), (inter, dim // 32),
+              (dim, inter // 2), (dim, inter // 32)]
+    out = []
+    for t, shp in zip((w1, s1, w3, s3, w2, s2), shapes):
+        h = np.zeros((E,) + shp, np.uint8)
+        tv = t.view(E, *shp)
+        for e in experts:
+            h[e] = tv[e].cpu().numpy()
+        out.append(h)
+    return out
+
+
+def _run_decode(x, idx, w, slabs, dim, inter, E, k, limit=10.0):
+    ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
+    y = torch.empty(dim, dtype=torch.float32, device=DEV)
+    L.moe_decode(x, idx, w, *slabs, y, dim, inter, E, k, ws, swiglu_limit=limit)
+    return y
+
+
+@pytest.mark.parametrize("E,dim,inter,k", [(16, 1024, 512, 4), (64, 2048, 768, 6),
+                                           (384, 4096, 2048, 8)])
+def test_moe_decode_matches_oracle(E, dim, inter, k):
+    rng = np.random.default_rng(700 + E)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(E)
+    announce("moe_decode E=%d dim=%d inter=%d k=%d" % (E, dim, inter, k))
+    slabs = _slabs(gen, E, dim, inter)
+    logits = rng.standard_normal(E).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    idx = torch.empty(k, dtype=torch.int32, device=DEV)
+    w = torch.empty(k, dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), None, idx, w, 1, E, k, O.SCORE_SIGMOID, 1.0, True, 1.0)
+    x = rng.standard_normal(dim).astype(np.float32)
+    y = _run_decode(dev(x), idx, w, slabs, dim, inter, E, k)
+    hi, hw = host(idx), host(w)
+    ri, rw = O.route(O.score(logits, O.SCORE_SIGMOID), bias, k)
+    assert np.array_equal(hi, ri) and np.array_equal(hw.view(np.uint32), rw.view(np.uint32))
+    H = _host_experts(slabs, hi, E, dim, inter)
+    want = O.moe_routed(*H, dim, inter, x, hi, hw)
+    assert_close(host(y), want, MOE_TOL, "moe_decode E=%d" % E)
+
+
+def test_moe_decode_split_entry_points_and_order():
+    """expert_glu_quant writes picks in ascending expert id; expert_reduce
+    sums them in that order; the result equals the one-call moe_decode
+    bit for bit, whatever order the picks arrive in."""
+    rng = np.random.default_rng(710)
+    E, dim, inter, k = 32, 1024, 256, 5
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(710)
+    slabs = _slabs(gen, E, dim, inter)
+    x = rng.standard_normal(dim).astype(np.float32)
+    ids = np.array([20, 3, 31, 0, 7], np.int32)
+    wts = np.array([0.3, 0.1, 0.25, 0.15, 0.2], np.float32)
+    announce("moe_decode split entry points")
+    y1 = _run_decode(dev(x), dev(ids), dev(wts), slabs, dim, inter, E, k)
+    perm = np.array([3, 0, 4, 1, 2])
+    y2 = _run_decode(dev(x), dev(ids[perm]), dev(wts[perm]), slabs, dim, inter, E, k)
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
+    xq = torch.empty(dim, dtype=torch.uint8, device=DEV)
+    xs = torch.empty(dim // 32, dtype=torch.uint8, device=DEV)
+    L.emit8(dev(x), xq, xs, dim)
+    hq = torch.empty((k, inter), dtype=torch.uint8, device=DEV)
+    hs = torch.empty((k, inter // 32), dtype=torch.uint8, device=DEV)
+    w1, s1, w3, s3, w2, s2 = slabs
+    L.expert_glu_quant(xq, xs, dev(ids), dev(wts), w1, s1, w3, s3, hq, hs, inter, dim, E, k)
+    y3 = torch.empty(dim, dtype=torch.float32, device=DEV)
+    L.expert_reduce(hq, hs, w2, s2, dev(ids), y3, dim, inter, E, k)
+    assert np.array_equal(host(y1).view(np.uint32), host(y3).view(np.uint32))
+    # row r of hq is the r-th smallest expert id's hidden state
+    H = _host_experts(slabs, ids, E, dim, inter)
+    order = np.argsort(ids)
+    hq_h, hs_h = host(hq), host(hs)
+    table = O.e4m3_decode_table()
+    for r, p in enumerate(order):
+        e = ids[p]
+        g = O.fp4_gemv(H[0][e].ravel(), H[1][e].ravel(), inter, dim, x)
+        u = O.fp4_gemv(H[2][e].ravel(), H[3][e].ravel(), inter, dim, x)
+        h = np.array([np.float32(np.float32(O.silu(float(min(a, 10.0)))) * np.float32(np.clip(b, -10, 10))) * wts[p]
+                      for a, b in zip(g, u)], np.float32)
+        dec = table[hq_h[r]] * np.repeat(np.ldexp(np.float32(1), hs_h[r].astype(np.int32) - 127), 32)
+        assert_close(dec, O.fp8_snap(h), 2 ** -3, "hq row %d (one e4m3 step)" % r)
+
+
+def test_moe_decode_closed_form_of_reference_gpu_test():
+    """weightstream-gpu/src/tests.rs:837-1020 at the BASELINE shape: all-0x11
+    FP4 weights (0.5) with unit scales and x = 0.01; experts 0 and 1 with
+    weight 1 each: y = 2 * hq * 0.5 * inter, hq the FP8 snap of
+    silu(10) * 10."""
+    E, dim, inter, k = 4, 4096, 2048, 2
+    announce("moe_decode closed form")
+    w1 = torch.full((E * inter, dim // 2), 0x11, dtype=torch.uint8, device=DEV)
+    s1 = torch.full((E * inter, dim // 32), 127, dtype=torch.uint8, device=DEV)
+    w2 = torch.full((E * dim, inter // 2), 0x11, dtype=torch.uint8, device=DEV)
+    s2 = torch.full((E * dim, inter // 32), 127, dtype=torch.uint8, device=DEV)
+    x = torch.full((dim,), 0.01, dtype=torch.float32, device=DEV)
+    idx = torch.tensor([1, 0], dtype=torch.int32, device=DEV)
+    w = torch.tensor([1.0, 1.0], dtype=torch.float32, device=DEV)
+    y = host(_run_decode(x, idx, w, (w1, s1, w1, s1, w2, s2), dim, inter, E, k))
+    g = dim * 0.5 * 0.009765625                      # 20.0 -> clamped to 10
+    assert g > 10
+    h = np.float32(np.float32(O.silu(10.0)) * np.float32(10.0))
+    sc = 2.0 ** math.ceil(math.log2(h / 448.0))
+    hq = O.e4m3_to_f32(O.f32_to_e4m3(float(h / sc))) * sc
+    want = np.float32(2.0 * hq * 0.5 * inter)
+    assert np.all(y == want), (y[:4], want)
+
+
+def test_moe_decode_invalid_picks_are_skipped():
+    """A pick outside [0, E) (an expert another rank owns) contributes
+    nothing, as moe_local_slots drops non-local experts."""
+    rng = np.random.default_rng(720)
+    E, dim, inter, k = 8, 1024, 256, 3
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(720)
+    slabs = _slabs(gen, E, dim, inter)
+    x = dev(rng.standard_normal(dim).astype(np.float32))
+    announce("moe_decode invalid picks")
+    ya = _run_decode(x, dev(np.array([2, -1, 5], np.int32)), dev(np.array([.5, .9, .5], np.float32)),
+                     slabs, dim, inter, E, k)
+    yb = _run_decode(x, dev(np.array([5, 2], np.int32)), dev(np.array([.5, .5], np.float32)),
+                     slabs, dim, inter, E, 2)
+    assert np.array_equal(host(ya).view(np.uint32), host(yb).view(np.uint32))

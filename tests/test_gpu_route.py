@@ -1,0 +1,172 @@
+"""GPU parity of MoE routing (weightstream-ref moe.rs:20-69): device expf,
+gate logits, scores, top-k selection and weights are bit-exact with the C
+oracle for sigmoid and softmax; sqrtsoftplus picks the same experts with
+weights within a few ulp (device logf is not glibc's)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_util import DEV, announce, dev, host
+from weightstream_amd import launch as L
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    L.Hip.global_()
+
+
+def test_device_expf_equals_glibc_on_every_input():
+    """All 2^32 inputs: the device digest equals glibc's, and 2^24 inputs
+    spread over the whole range are compared value by value."""
+    lib = L._lib.load()
+    chunk = 1 << 28
+    out = torch.empty(chunk, dtype=torch.int32, device=DEV)
+    total = 0
+    for c in range(16):
+        lo = c * chunk
+        announce("expf probe chunk %d" % c)
+        L._lib.check("ws_expf_probe", lib.ws_expf_probe(lo, chunk, out.data_ptr(),
+                                                         torch.cuda.current_stream().cuda_stream))
+        r = out.to(torch.int64) & 0xFFFFFFFF
+        # canonical NaN, as the host digest does
+        nan = ((r & 0x7F800000) == 0x7F800000) & ((r & 0x7FFFFF) != 0)
+        r = torch.where(nan, torch.full_like(r, 0x7FC00000), r)
+        u = torch.arange(lo, lo + chunk, dtype=torch.int64, device=DEV)
+        mixed = (r ^ ((u * 0x9E3779B1) & 0xFFFFFFFF)) * (2 * u + 1)
+        total = (total + int(mixed.sum().item())) & ((1 << 64) - 1)
+    want = O.expfcheck().glibc_expf_digest(0, 1 << 32)
+    assert total == want
+    # direct comparison on a strided sample
+    lo, n = 0x3C000000, 1 << 24
+    L._lib.check("ws_expf_probe", lib.ws_expf_probe(lo, n, out.data_ptr(),
+                                                     torch.cuda.current_stream().cuda_stream))
+    got = host(out[:n]).view(np.uint32)
+    ref = np.empty(n, np.uint32)
+    O.expfcheck().glibc_expf_bits(lo, n, ref.ctypes.data)
+    nan = (got & 0x7F800000 == 0x7F800000) & (got & 0x7FFFFF != 0)
+    got = np.where(nan, np.uint32(0x7FC00000), got)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_gate_logits_bit_exact(bf16):
+    rng = np.random.default_rng(200 + bf16)
+    m, dim, E = 3, 4096, 384
+    x = rng.standard_normal((m, dim)).astype(np.float32)
+    w = (rng.standard_normal((E, dim)) * 0.02).astype(np.float32)
+    if bf16:
+        wb = np.array([O.f32_to_bf16(float(v)) for v in w.ravel()], np.uint16).reshape(E, dim)
+        w = (wb.astype(np.uint32) << 16).view(np.float32)
+        dw = dev(wb.view(np.int16))
+    else:
+        dw = dev(w)
+    announce("gate_logits bf16=%d" % bf16)
+    logits = torch.empty((m, E), dtype=torch.float32, device=DEV)
+    L.moe_gate_logits(dev(x), dw, logits, m, dim, E)
+    got = host(logits)
+    for r in range(m):
+        want = O.gemv_f32(w, x[r])
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32))
+
+
+def _rows_with_ties(rng, m, E, score_func):
+    logits = rng.standard_normal((m, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    # exact ties of score+bias between experts (9, 5) and (3, 17) on row 0
+    s0 = O.score(logits[0], score_func)
+    bias[5] = np.float32(s0[9] + bias[9] - s0[5])
+    logits[1, 40] = logits[1, 41]                  # equal logits, equal scores
+    bias[40] = bias[41]
+    return logits, bias
+
+
+@pytest.mark.parametrize("score_func", [O.SCORE_SIGMOID, O.SCORE_SOFTMAX])
+@pytest.mark.parametrize("E,k", [(384, 8), (256, 6), (64, 1), (1000, 16)])
+def test_topk_bit_exact(score_func, E, k):
+    rng = np.random.default_rng(300 + E + k + score_func)
+    m = 48
+    logits, bias = _rows_with_ties(rng, m, E, score_func)
+    temp, rscale = (1.0, 1.0) if k != 6 else (1.7, 2.5)
+    announce("moe_topk E=%d k=%d f=%d" % (E, k, score_func))
+    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    sc = torch.empty((m, E), dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), sc, idx, w, m, E, k, score_func, temp, True, rscale)
+    gi, gw, gs = host(idx), host(w), host(sc)
+    for r in range(m):
+        s = O.score(logits[r], score_func, temp)
+        assert np.array_equal(gs[r].view(np.uint32), s.view(np.uint32))
+        ri, rw = O.route(s, bias, k, True, rscale)
+        assert np.array_equal(gi[r], ri), (r, gi[r], ri)
+        assert np.array_equal(gw[r].view(np.uint32), rw.view(np.uint32))
+
+
+def test_topk_sqrtsoftplus_same_experts():
+    rng = np.random.default_rng(400)
+    m, E, k = 64, 384, 6
+    logits = rng.standard_normal((m, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    announce("moe_topk sqrtsoftplus")
+    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    sc = torch.empty((m, E), dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), sc, idx, w, m, E, k, O.SCORE_SQRTSOFTPLUS, 1.0, True, 1.5)
+    gi, gw, gs = host(idx), host(w), host(sc)
+    for r in range(m):
+        s = O.score(logits[r], O.SCORE_SQRTSOFTPLUS)
+        ulp = np.abs(gs[r].view(np.int32) - s.view(np.int32))
+        assert ulp.max() <= 2
+        ri, rw = O.route(s, bias, k, True, 1.5)
+        b = np.sort(s + bias)[::-1]
+        if b[k - 1] - b[k] > 1e-5:                   # no near-tie at the cut
+            assert np.array_equal(np.sort(gi[r]), np.sort(ri))
+            np.testing.assert_allclose(gw[r], rw, rtol=1e-6)
+
+
+def test_reference_gate_select_route_contract():
+    """moe_gate (bf16, sqrtsoftplus scores), moe_select (always-normalised
+    top-k of given scores) and the fused moe_route agree with each other and
+    with the oracle's selection on the same scores."""
+    rng = np.random.default_rng(500)
+    dim, E, k = 512, 96, 6
+    x = rng.standard_normal(dim).astype(np.float32)
+    wf = (rng.standard_normal((E, dim)) * 0.05).astype(np.float32)
+    wb = np.array([O.f32_to_bf16(float(v)) for v in wf.ravel()], np.uint16).reshape(E, dim)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    dx, dwb, db = dev(x), dev(wb.view(np.int16)), dev(bias)
+    announce("moe_gate/moe_select/moe_route")
+    scores = torch.empty(E, dtype=torch.float32, device=DEV)
+    L.moe_gate(dx, dwb, db, scores, dim, E)
+    w1 = torch.empty(k, dtype=torch.float32, device=DEV)
+    i1 = torch.empty(k, dtype=torch.int32, device=DEV)
+    L.moe_select(scores, db, w1, i1, E, k, 1.5)
+    w2 = torch.empty(k, dtype=torch.float32, device=DEV)
+    i2 = torch.empty(k, dtype=torch.int32, device=DEV)
+    L.moe_route(dx, dwb, db, w2, i2, dim, E, k, 1.5)
+    s = host(scores)
+    ri, rw = O.route(s, bias, k, True, 1.5)
+    assert np.array_equal(host(i1), ri) and np.array_equal(host(i2), ri)
+    assert np.array_equal(host(w1).view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(host(w2).view(np.uint32), rw.view(np.uint32))
+    wdense = (wb.astype(np.uint32) << 16).view(np.float32)
+    ref_s = O.score(O.gemv_f32(wdense, x), O.SCORE_SQRTSOFTPLUS)
+    assert np.abs(s.view(np.int32) - ref_s.view(np.int32)).max() <= 2
+
+
+def test_swiglu_bit_exact():
+    rng = np.random.default_rng(600)
+    n = 4096
+    g = (rng.standard_normal(n) * 8).astype(np.float32)
+    u = (rng.standard_normal(n) * 8).astype(np.float32)
+    announce("swiglu")
+    out = torch.empty(n, dtype=torch.float32, device=DEV)
+    L.swiglu(dev(g), dev(u), out, n, 0.37)
+    got = host(out)
+    gc = np.minimum(g, np.float32(10))
+    uc = np.clip(u, np.float32(-10), np.float32(10))
+    want = np.array([np.float32(np.float32(O.silu(float(a)) * b) * np.float32(0.37))
+                     for a, b in zip(gc, uc)], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

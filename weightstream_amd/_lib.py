@@ -1,0 +1,100 @@
+"""Loader of the in-tree HIP library libweightstream_hip.so.
+
+The library is the product: there is no CPU or PyTorch fallback. If it is
+missing, importing any entry point raises.
+"""
+import ctypes as C
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "libweightstream_hip.so")
+HEADER = os.path.join(ROOT, "include", "ws_hip.h")
+
+_lib = None
+
+
+def header_symbols():
+    """Every function the C header declares (ws_*)."""
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(ws_[a-z0-9_]+)\s*\(", txt)))
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                "libweightstream_hip.so is not built (python -m weightstream_amd.build); "
+                "weightstream_amd has no fallback path")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_p = C.c_void_p
+_i64 = C.c_int64
+_i = C.c_int
+_f = C.c_float
+_u32 = C.c_uint32
+
+SIGNATURES = {
+    "ws_init": (_i, []),
+    "ws_built_with_hip": (_i, []),
+    "ws_error_string": (C.c_char_p, [_i]),
+    "ws_expf_probe": (_i, [_u32, _u32, _p, _p]),
+    "ws_snap8": (_i, [_p, _i64, _p]),
+    "ws_emit8": (_i, [_p, _p, _p, _i64, _p]),
+    "ws_emit8_packed": (_i, [_p, _p, _p, _i64, _p]),
+    "ws_pack_scales": (_i, [_p, _p, _i64, _p]),
+    "ws_weight_quant_fp4": (_i, [_p, _p, _p, _i64, _i64, _p]),
+    "ws_weight_quant_fp8": (_i, [_p, _p, _p, _i64, _i64, _p]),
+    "ws_fp8_gemm": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_fp8_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_fp8_gemm_bf16": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_fp8_gemm_f32s": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _p]),
+    "ws_act_quant_f32s": (_i, [_p, _p, _p, _i64, _i64, _p]),
+    "ws_fp4_gemm": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_fp4_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_moe_gate_logits": (_i, [_p, _p, _i, _p, _i64, _i64, _i64, _p]),
+    "ws_moe_topk": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i, _f, _i, _f, _p]),
+    "ws_moe_gate": (_i, [_p, _p, _p, _p, _i64, _i64, _p]),
+    "ws_moe_gate_m": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_moe_select": (_i, [_p, _p, _p, _p, _i64, _i64, _f, _p]),
+    "ws_moe_route": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p]),
+    "ws_swiglu": (_i, [_p, _p, _p, _i64, _f, _p]),
+    "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),
+    "ws_expert_reduce": (_i, [_p] * 6 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
+    "ws_moe_decode": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
+    "ws_moe_dispatch": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_grouped_glu_quant": (_i, [_p] * 12 + [_i64, _i64, _i64, _i64, _i64, _f, _p]),
+    "ws_moe_grouped_down": (_i, [_p] * 7 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_combine": (_i, [_p] * 3 + [_i64, _i64, _i64, _p]),
+    "ws_moe_prefill_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "ws_moe_prefill": (_i, [_p] * 10 + [_i64] * 5 + [_f, _p, C.c_size_t, _p]),
+}
+
+
+def _declare(lib):
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name, None)
+        if fn is None:
+            continue
+        fn.restype = res
+        fn.argtypes = args
+
+
+class WsError(RuntimeError):
+    def __init__(self, fn, code):
+        msg = load().ws_error_string(code).decode()
+        super().__init__("%s failed: %s (code %d)" % (fn, msg, code))
+        self.code = code
+
+
+def check(fn, code):
+    """Raise on a nonzero status, as launch.rs `.unwrap()`s every launch."""
+    if code != 0:
+        raise WsError(fn, code)

@@ -1,0 +1,285 @@
+// Block-scaled GEMM on CDNA4 scaled MFMA: C[M,N] = A[M,K] . B[N,K]^T.
+//
+// Replaces fp8_gemm.cu:9 (M=1 decode), fp8_gemm_tile.cu:28 (M-batch),
+// fp4_expert_gemm.cu:9 / fp4_gemm_tile.cu:21 and the TileLang gemm_mxfp8
+// kernels (launch.rs:344-377, 717-804). CPU semantics: weightstream-ref
+// actquant.rs:110-173 (per-32 block dot, scale-corrected, f32 accumulate).
+//
+// Design (gfx950):
+//  - one v_mfma_scale_f32_16x16x128_f8f6f4 per 16x16 output fragment and
+//    128-K step. The hardware applies the UE8M0 scales per lane, i.e. per
+//    (row, 32-K block), which is exactly the reference's activation (1x32) and
+//    FP4 weight (1x32) granularity; FP8 32x32 weight scales are broadcast to
+//    the 32 rows of their block. The f32-scale scheme runs the MFMA with unit
+//    scales and applies sa*sb once per 128-K step in f32.
+//  - lane l holds row/col (l % 16) and K block (l / 16) of each fragment:
+//    16-byte global loads, 64 (fp8) or 32 (fp4) contiguous bytes per row and
+//    step, no LDS staging of the streamed operand.
+//  - a workgroup is GM x GK waves: GM waves along M share the weight
+//    fragments through L1/L2; GK waves split K and are reduced through LDS in
+//    wave order (deterministic).
+//  - the weight operand is streamed with non-temporal loads: each weight byte
+//    is used by exactly one workgroup.
+#include "ws_internal.hpp"
+
+#include <stdlib.h>
+
+namespace ws {
+
+enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
+enum OutMode { kOutF32 = 0, kOutBf16 = 1 };
+
+template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U>
+__global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__restrict__ A,
+                                                            const void *__restrict__ SA,
+                                                            const uint8_t *__restrict__ B,
+                                                            const void *__restrict__ SB,
+                                                            void *__restrict__ C, int M, int N,
+                                                            int K) {
+    constexpr int kTileM = 16 * WM * GM;
+    constexpr int kTileN = 16 * WN;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int wm = w % GM, wk = w / GM;
+    const int r = lane & 15, kb = lane >> 4;
+    const int m_base = blockIdx.y * kTileM + wm * 16 * WM;
+    const int n_base = blockIdx.x * kTileN;
+    const int ksteps = K / 128;
+    const int k0 = wk * ksteps / GK, k1 = (wk + 1) * ksteps / GK;
+    const int kbn = K / 32;  // UE8M0 scale columns
+    const int kb128 = K / 128;
+
+    // per-fragment row / column this lane loads (clamped; stores are guarded)
+    const uint8_t *arow[WM];
+    const uint8_t *brow[WN];
+    const uint8_t *sarow[WM];
+    const uint8_t *sbrow[WN];
+    int col_of[WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+        int row = min(m_base + i * 16 + r, M - 1);
+        arow[i] = A + (size_t)row * K + kb * 32;
+        if (SMODE == kUe8m0) sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
+    }
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+        int col = min(n_base + j * 16 + r, N - 1);
+        col_of[j] = col;
+        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + kb * 16 : B + (size_t)col * K + kb * 32;
+        if (SMODE == kUe8m0)
+            sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
+    }
+
+    v4f acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // f32-scale mode: the activation scales of the 4 D rows of each fragment
+    // and the weight scale of the lane's column, per 128-K step.
+    const float *saf = (const float *)SA;
+    const float *sbf = (const float *)SB;
+
+    for (int ks0 = k0; ks0 < k1; ks0 += U) {
+        uint4 af[U][WM][2];
+        uint4 bf[U][WN][2];
+        uint32_t sav[U][WM], sbv[U][WN];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int ks = ks0 + u;
+            if (ks < k1) {
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    const uint8_t *p = arow[i] + (size_t)ks * 128;
+                    af[u][i][0] = ldg16(p);
+                    af[u][i][1] = ldg16(p + 16);
+                    if (SMODE == kUe8m0)
+                        sav[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
+                }
+#pragma unroll
+                for (int j = 0; j < WN; j++) {
+                    if (BFP4) {
+                        bf[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                    } else {
+                        const uint8_t *p = brow[j] + (size_t)ks * 128;
+                        bf[u][j][0] = ldg16_stream(p);
+                        bf[u][j][1] = ldg16_stream(p + 16);
+                    }
+                    if (SMODE == kUe8m0)
+                        sbv[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int ks = ks0 + u;
+            if (ks < k1) {
+#pragma unroll
+                for (int i = 0; i < WM; i++) {
+                    v8i a = frag_from(af[u][i][0], af[u][i][1]);
+#pragma unroll
+                    for (int j = 0; j < WN; j++) {
+                        v8i b = BFP4 ? frag_from4(bf[u][j][0]) : frag_from(bf[u][j][0], bf[u][j][1]);
+                        if (SMODE == kUe8m0) {
+                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b, acc[i][j],
+                                                                             (int)sav[u][i],
+                                                                             (int)sbv[u][j])
+                                             : mfma_scaled<kFmtFp8, kFmtFp8>(a, b, acc[i][j],
+                                                                             (int)sav[u][i],
+                                                                             (int)sbv[u][j]);
+                        } else {
+                            v4f t = mfma_scaled<kFmtFp8, kFmtFp8>(a, b, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                  kScaleOne, kScaleOne);
+                            float sb = sbf[(size_t)(col_of[j] / 128) * kb128 + ks];
+#pragma unroll
+                            for (int v = 0; v < 4; v++) {
+                                int row = min(m_base + i * 16 + 4 * kb + v, M - 1);
+                                float s = saf[(size_t)row * kb128 + ks] * sb;
+                                acc[i][j][v] = acc[i][j][v] + t[v] * s;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (GK > 1) {
+        // ordered reduction of the K-split partials through LDS
+        __shared__ float red[GK > 1 ? (GK - 1) * GM * WM * WN * 4 * 64 : 1];
+        if (wk > 0) {
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        red[((((wk - 1) * GM + wm) * WM + i) * WN + j) * 256 + v * 64 + lane] =
+                            acc[i][j][v];
+        }
+        __syncthreads();
+        if (wk > 0) return;
+#pragma unroll
+        for (int s = 1; s < GK; s++)
+#pragma unroll
+            for (int i = 0; i < WM; i++)
+#pragma unroll
+                for (int j = 0; j < WN; j++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        acc[i][j][v] =
+                            acc[i][j][v] +
+                            red[((((s - 1) * GM + wm) * WM + i) * WN + j) * 256 + v * 64 + lane];
+    }
+
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+            int col = n_base + j * 16 + r;
+            if (col >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                int row = m_base + i * 16 + 4 * kb + v;
+                if (row >= M) continue;
+                if (OMODE == kOutF32)
+                    ((float *)C)[(size_t)row * N + col] = acc[i][j][v];
+                else
+                    ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(acc[i][j][v]);
+            }
+        }
+}
+
+// Tile configurations. A config is chosen from M unless WS_GEMM_CFG forces one
+// (a tuning knob for measurements).
+struct GemmCfg {
+    int tile_m, tile_n;
+};
+
+template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U>
+static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
+                      int m, int n, int k, hipStream_t stream) {
+    constexpr int tm = 16 * WM * GM, tn = 16 * WN;
+    dim3 grid((n + tn - 1) / tn, (m + tm - 1) / tm);
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, GM, GK, BFP4, SMODE, OMODE, U>), grid,
+                       dim3(64 * GM * GK), 0, stream, a, sa, b, sb, out, m, n, k);
+    return launch_status();
+}
+
+static int forced_cfg() {
+    static int cfg = [] {
+        const char *e = getenv("WS_GEMM_CFG");
+        return e ? atoi(e) : -1;
+    }();
+    return cfg;
+}
+
+template <bool BFP4, int SMODE, int OMODE>
+static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb,
+                         void *out, int64_t m, int64_t n, int64_t k, hipStream_t stream) {
+    if (!a || !sa || !b || !sb || !out) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || n <= 0 || k <= 0) return WS_ERR_INVALID_ARG;
+    if (k % 128 || n % 16 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return WS_ERR_SHAPE;
+    int M = (int)m, N = (int)n, K = (int)k;
+    int cfg = forced_cfg();
+    if (cfg < 0) cfg = (M <= 16) ? 0 : (M <= 64 ? 1 : 2);
+    switch (cfg) {
+        case 0:  // decode: 16 x 16 tile, K split over 4 waves
+            return launch_cfg<1, 1, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 1:  // 64 x 16 tile
+            return launch_cfg<1, 1, 4, 1, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 2:  // 128 x 16 tile
+            return launch_cfg<2, 1, 4, 1, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 3:  // 128 x 32 tile
+            return launch_cfg<2, 2, 4, 1, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        case 4:  // 64 x 16 tile, K split over 2
+            return launch_cfg<1, 1, 4, 2, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 5:  // 16 x 16 tile, K split over 8 waves
+            return launch_cfg<1, 1, 1, 8, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 6:  // 16 x 32 tile, K split over 4
+            return launch_cfg<1, 2, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        default:
+            return WS_ERR_INVALID_ARG;
+    }
+}
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" {
+
+int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<false, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp8_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<false, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp8_gemm_bf16(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     uint16_t *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<false, kUe8m0, kOutBf16>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp8_gemm_f32s(const uint8_t *a, const float *sa, const uint8_t *b, const float *sb,
+                     void *out, int out_bf16, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    if (out_bf16)
+        return gemm_dispatch<false, kF32s, kOutBf16>(a, sa, b, sb, out, m, n, k, stream);
+    return gemm_dispatch<false, kF32s, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp4_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<true, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp4_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                     float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<true, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+}  // extern "C"

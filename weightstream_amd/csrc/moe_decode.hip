@@ -1,0 +1,263 @@
+// Routed FP4 experts for one token (M = 1 decode).
+//
+// Replaces the reference's device-side grouped decode chain
+// moe_local_slots -> expert_glu -> expert_quant -> expert_reduce
+// (weightstream-cuda/kernels/moe_grouped.cu:23-224, launch.rs:89-206) with two
+// kernels. CPU semantics: weightstream-ref moe.rs:75-84 (experts summed in
+// ascending id) and :162-208 (gate/up, asymmetric swiglu clamps, routing
+// weight before the FP8 re-quantisation and the down projection).
+//
+// M = 1 is HBM-bound: the two kernels stream 8 x 3 x 4.45 MB of packed FP4
+// weights + UE8M0 scales once. Each wave owns 16 weight rows and walks K in
+// 128-wide steps with one 16-byte load per lane per step; the token sits in
+// LDS and feeds the MFMA's other operand (every column of the 16x16 MFMA
+// output is the same token). The hardware applies both UE8M0 scales.
+//
+//  glu_quant: grid (inter/32, top_k), 4 waves: waves 0-1 -> w1 rows, 2-3 -> w3
+//    rows of one 32-row tile; the epilogue applies SwiGLU x routing weight and
+//    quantises the 32 values (one FP8 1x32 block) straight to e4m3 + UE8M0.
+//  reduce: grid (dim/16), 4 waves: each wave runs whole experts for 16 output
+//    rows; per-expert results meet in LDS and are added in ascending expert id,
+//    one f32 add per expert like the reference's acc_f32 chain.
+#include "ws_internal.hpp"
+
+namespace ws {
+
+constexpr int kDecThreads = 256;
+constexpr int kMaxTopkDec = 16;
+constexpr int kU = 8;  // K steps in flight per wave
+
+// rank of pick `slot` among valid picks ordered by (expert id, slot)
+__device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_experts, int slot) {
+    int e = idx[slot];
+    int rank = 0;
+    for (int j = 0; j < top_k; j++) {
+        int f = idx[j];
+        if (f < 0 || f >= n_experts) continue;
+        if (f < e || (f == e && j < slot)) rank++;
+    }
+    return rank;
+}
+
+// Stream a 16-row FP4 weight tile against the token in LDS: returns the 16x16
+// MFMA accumulator (all columns equal). w_rows points at row 0 of the tile,
+// s_rows at its scale row 0; row stride k/2 bytes (weights) and k/32 (scales).
+__device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_rows,
+                                               const uint8_t *__restrict__ s_rows,
+                                               const uint8_t *xq_lds, const uint8_t *xs_lds,
+                                               int k, int lane) {
+    const int r = lane & 15, kb = lane >> 4;
+    const uint8_t *wp = w_rows + (size_t)r * (k / 2) + kb * 16;
+    const uint8_t *sp = s_rows + (size_t)r * (k / 32);
+    const int ksteps = k / 128;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int ks0 = 0; ks0 < ksteps; ks0 += kU) {
+        uint4 wf[kU];
+        uint32_t ws_[kU];
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            int ks = ks0 + u;
+            if (ks < ksteps) {
+                wf[u] = ldg16_stream(wp + (size_t)ks * 64);
+                ws_[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; u++) {
+            int ks = ks0 + u;
+            if (ks < ksteps) {
+                const uint4 *xp = (const uint4 *)(xq_lds + ks * 128 + kb * 32);
+                v8i b = frag_from(xp[0], xp[1]);
+                int sx = xs_lds[ks * 4 + kb];
+                acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(wf[u]), b, acc, (int)ws_[u], sx);
+            }
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
+    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs, const int32_t *__restrict__ idx,
+    const float *__restrict__ topk_w, const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
+    const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
+    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t *xq_l = lds;             // dim bytes
+    uint8_t *xs_l = lds + dim;       // dim/32 bytes
+    __shared__ float gu[2][32];
+    const int slot = blockIdx.y;
+    const int e = idx[slot];
+    if (e < 0 || e >= n_experts) return;  // whole workgroup
+    const int tile = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+
+    for (int i = t * 16; i < dim; i += kDecThreads * 16) *(uint4 *)(xq_l + i) = *(const uint4 *)(xq + i);
+    for (int i = t; i < dim / 32; i += kDecThreads) xs_l[i] = xs[i];
+    __syncthreads();
+
+    const int mat = w >> 1;
+    const int row0 = tile * 32 + (w & 1) * 16;
+    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
+    const uint8_t *W = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2);
+    const uint8_t *S = (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32);
+    v4f acc = stream_fp4_rows(W, S, xq_l, xs_l, dim, lane);
+    // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
+    if ((lane & 15) == 0) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) gu[mat][(w & 1) * 16 + 4 * (lane >> 4) + v] = acc[v];
+    }
+    __syncthreads();
+    if (w != 0) return;
+    // lanes 0-31 own the tile's 32 values; lanes 32-63 mirror them so the
+    // half-wave reduction stays uniform, and do not store
+    const int n = lane & 31;
+    float g = gu[0][n], u = gu[1][n];
+    if (limit > 0.0f) {
+        u = rclamp(u, -limit, limit);
+        g = fminf(g, limit);
+    }
+    const float rw = topk_w[slot];
+    float h = ws_silu(g) * u * rw;
+    uint32_t sb;
+    uint32_t qb = quant_fp8_block32(h, &sb);
+    if (lane < 32) {
+        const int rank = pick_rank(idx, top_k, n_experts, slot);
+        hq[(size_t)rank * inter + tile * 32 + n] = (uint8_t)qb;
+        if (n == 0) hs[(size_t)rank * (inter / 32) + tile] = (uint8_t)sb;
+    }
+}
+
+__global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
+    const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs, const int32_t *__restrict__ idx,
+    const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
+    int inter, int n_experts, int top_k) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int32_t sorted_e[kMaxTopkDec];
+    __shared__ int32_t n_valid;
+    __shared__ float part[kMaxTopkDec][16];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int row0 = blockIdx.x * 16;
+    if (t == 0) {
+        int cnt = 0;
+        for (int s = 0; s < top_k; s++) {
+            int e = idx[s];
+            if (e < 0 || e >= n_experts) continue;
+            sorted_e[pick_rank(idx, top_k, n_experts, s)] = e;
+            cnt++;
+        }
+        n_valid = cnt;
+    }
+    uint8_t *hq_l = lds;                            // top_k * inter
+    uint8_t *hs_l = lds + (size_t)top_k * inter;    // top_k * inter/32
+    __syncthreads();
+    const int nv = n_valid;
+    for (int i = t * 16; i < nv * inter; i += kDecThreads * 16)
+        *(uint4 *)(hq_l + i) = *(const uint4 *)(hq + i);
+    for (int i = t; i < nv * (inter / 32); i += kDecThreads) hs_l[i] = hs[i];
+    __syncthreads();
+
+    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
+    for (int p = w; p < nv; p += kDecThreads / 64) {
+        const int e = sorted_e[p];
+        const uint8_t *W = w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2);
+        const uint8_t *S = s2 + (size_t)e * smat + (size_t)row0 * (inter / 32);
+        v4f acc = stream_fp4_rows(W, S, hq_l + (size_t)p * inter, hs_l + (size_t)p * (inter / 32),
+                                  inter, lane);
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) part[p][4 * (lane >> 4) + v] = acc[v];
+        }
+    }
+    __syncthreads();
+    if (t < 16) {
+        float acc = 0.0f;
+        for (int p = 0; p < nv; p++) acc = acc + part[p][t];
+        y[row0 + t] = acc;
+    }
+}
+
+static int check_decode_shapes(int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k) {
+    if (dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
+    if (dim % 128 || inter % 128 || top_k > kMaxTopkDec) return WS_ERR_SHAPE;
+    if (dim > 65536 || inter > 65536 || top_k * inter > 65536 || n_experts > (1 << 20))
+        return WS_ERR_SHAPE;
+    return WS_OK;
+}
+
+static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" {
+
+int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *topk_idx,
+                        const float *topk_w, const uint8_t *w1, const uint8_t *s1,
+                        const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                        int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                        float swiglu_limit, ws_stream_t stream) {
+    if (!xq || !xs || !topk_idx || !topk_w || !w1 || !s1 || !w3 || !s3 || !hq || !hs)
+        return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 3) ||
+        ((uintptr_t)s3 & 3))
+        return WS_ERR_INVALID_ARG;
+    dim3 grid((unsigned)(inter / 32), (unsigned)top_k);
+    size_t lds = (size_t)dim + dim / 32;
+    hipLaunchKernelGGL(expert_glu_quant_kernel, grid, dim3(kDecThreads), lds, stream, xq, xs,
+                       topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
+                       (int)n_experts, (int)top_k, swiglu_limit);
+    return launch_status();
+}
+
+int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
+                     const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim, int64_t inter,
+                     int64_t n_experts, int64_t top_k, ws_stream_t stream) {
+    if (!hq || !hs || !topk_idx || !w2 || !s2 || !y) return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 3)) return WS_ERR_INVALID_ARG;
+    size_t lds = (size_t)top_k * inter + (size_t)top_k * (inter / 32);
+    hipLaunchKernelGGL(expert_reduce_kernel, dim3((unsigned)(dim / 16)), dim3(kDecThreads), lds,
+                       stream, hq, hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
+                       (int)top_k);
+    return launch_status();
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k) {
+    if (dim <= 0 || inter <= 0 || top_k <= 0) return 0;
+    return align256(dim) + align256(dim / 32) + align256(top_k * inter) +
+           align256(top_k * (inter / 32));
+}
+
+int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, const uint8_t *w1,
+                  const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                  const uint8_t *s2, float *y, int64_t dim, int64_t inter, int64_t n_experts,
+                  int64_t top_k, float swiglu_limit, void *workspace, size_t workspace_bytes,
+                  ws_stream_t stream) {
+    if (!x || !workspace) return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (workspace_bytes < ws_moe_decode_workspace_size(dim, inter, top_k) || !aligned16(workspace))
+        return WS_ERR_INVALID_ARG;
+    uint8_t *p = (uint8_t *)workspace;
+    uint8_t *xq = p;
+    p += align256(dim);
+    uint8_t *xs = p;
+    p += align256(dim / 32);
+    uint8_t *hq = p;
+    p += align256(top_k * inter);
+    uint8_t *hs = p;
+    rc = ws_emit8(x, xq, xs, dim, stream);
+    if (rc) return rc;
+    rc = ws_expert_glu_quant(xq, xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                             n_experts, top_k, swiglu_limit, stream);
+    if (rc) return rc;
+    return ws_expert_reduce(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+}
+
+}  // extern "C"

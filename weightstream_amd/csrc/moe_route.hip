@@ -1,0 +1,318 @@
+// MoE routing: gate logits, score function, top-k and routing weights.
+//
+// Reference GPU kernels: weightstream-cuda/kernels/moe.cu (moe_gate :18,
+// moe_select :48, moe_route :100, moe_gate_m :160), launched by
+// launch.rs:998-1093. CPU semantics (the parity target): weightstream-ref
+// moe.rs:20-69 and num.rs:8-88.
+//
+// Bit-exactness with the CPU path:
+//  - gate logits follow num::gemv: one sequential f32 dot per (token, expert);
+//    a lane owns one expert and walks d = 0..dim-1 in order, multiply then add
+//    (compiled without contraction);
+//  - sigmoid / softmax use ws_expf, equal to glibc expf on every input;
+//  - top-k orders by f32 total order of score+bias, ties to the lower index
+//    (moe.rs:50 `total_cmp(..).then(a.cmp(&b))`);
+//  - the weight normaliser is the sequential sum in top-k order plus 1e-20
+//    (moe.rs:61-66), then * route_scale.
+// sqrtsoftplus uses the device logf and sqrtf; sqrtf is correctly rounded,
+// logf is within 1 ulp of glibc's (not bit-exact).
+#include "ws_internal.hpp"
+
+namespace ws {
+
+constexpr int kScoreIdentity = 3;  // scores given (moe_select)
+
+// ---- gate logits ----------------------------------------------------------
+// grid (ceil(E/64), M), 64 threads: lane = expert. Each lane streams its own
+// weight row with 16-byte loads (consecutive iterations reuse the cache line).
+template <bool BF16>
+__global__ __launch_bounds__(64) void gate_logits_kernel(const float *__restrict__ x,
+                                                         const void *__restrict__ gw,
+                                                         float *__restrict__ logits, int dim,
+                                                         int n_experts) {
+    int e = blockIdx.x * 64 + threadIdx.x;
+    int m = blockIdx.y;
+    __shared__ float xs[4096];
+    const float *xr = x + (size_t)m * dim;
+    float s = 0.0f;
+    for (int d0 = 0; d0 < dim; d0 += 4096) {
+        int len = min(4096, dim - d0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < len; i += 64) xs[i] = xr[d0 + i];
+        __syncthreads();
+        if (e < n_experts) {
+            if (BF16) {
+                const uint16_t *w = (const uint16_t *)gw + (size_t)e * dim + d0;
+                int i = 0;
+                for (; i + 8 <= len; i += 8) {
+                    uint4 q = *(const uint4 *)(w + i);
+                    uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        s = s + xs[i + 2 * t] * __uint_as_float(wd[t] << 16);
+                        s = s + xs[i + 2 * t + 1] * __uint_as_float(wd[t] & 0xFFFF0000u);
+                    }
+                }
+                for (; i < len; i++) s = s + xs[i] * __uint_as_float((uint32_t)w[i] << 16);
+            } else {
+                const float *w = (const float *)gw + (size_t)e * dim + d0;
+                int i = 0;
+                for (; i + 4 <= len; i += 4) {
+                    float4 q = *(const float4 *)(w + i);
+                    s = s + xs[i] * q.x;
+                    s = s + xs[i + 1] * q.y;
+                    s = s + xs[i + 2] * q.z;
+                    s = s + xs[i + 3] * q.w;
+                }
+                for (; i < len; i++) s = s + xs[i] * w[i];
+            }
+        }
+    }
+    if (e < n_experts) logits[(size_t)m * n_experts + e] = s;
+}
+
+__device__ __forceinline__ float score_fn(float v, int score_func, float gate_temp) {
+    if (gate_temp != 1.0f) v = v / gate_temp;
+    if (score_func == WS_SCORE_SIGMOID) return ws_sigmoid(v);
+    if (score_func == WS_SCORE_SQRTSOFTPLUS) {
+        float sp = v > 20.0f ? v : logf(1.0f + ws_expf(v));
+        return sqrtf(sp);
+    }
+    return v;  // softmax handled by the caller, identity for given scores
+}
+
+// f32 total order (Rust f32::total_cmp) as an unsigned key: larger = greater.
+__device__ __forceinline__ uint32_t total_key_u(float v) {
+    int32_t b = (int32_t)__float_as_uint(v);
+    int32_t k = b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+    return (uint32_t)k ^ 0x80000000u;
+}
+
+constexpr int kTopkThreads = 256;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopk = 16;
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        uint64_t o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// One workgroup per token row: scores, top-k selection, weights.
+__global__ __launch_bounds__(kTopkThreads) void topk_kernel(
+    const float *__restrict__ logits, const float *__restrict__ bias, float *__restrict__ scores_out,
+    int32_t *__restrict__ out_idx, float *__restrict__ out_w, int n_experts, int top_k,
+    int score_func, float gate_temp, int norm, float route_scale) {
+    __shared__ float sc[kMaxExperts];
+    __shared__ uint64_t wave_best[kTopkThreads / 64];
+    __shared__ int32_t picked[kMaxTopk];
+    const int m = blockIdx.x;
+    const int t = threadIdx.x;
+    const float *lg = logits + (size_t)m * n_experts;
+
+    for (int e = t; e < n_experts; e += kTopkThreads) sc[e] = score_fn(lg[e], score_func, gate_temp);
+    __syncthreads();
+    if (score_func == WS_SCORE_SOFTMAX) {
+        // num.rs:46-62: max, exp(x - max) in place with a sequential sum, divide
+        if (t == 0) {
+            float mx = -__builtin_inff();
+            for (int e = 0; e < n_experts; e++)
+                if (sc[e] > mx) mx = sc[e];
+            float s = 0.0f;
+            for (int e = 0; e < n_experts; e++) {
+                sc[e] = ws_expf(sc[e] - mx);
+                s = s + sc[e];
+            }
+            wave_best[0] = (uint64_t)__float_as_uint(s);
+        }
+        __syncthreads();
+        float s = __uint_as_float((uint32_t)wave_best[0]);
+        for (int e = t; e < n_experts; e += kTopkThreads) sc[e] = sc[e] / s;
+        __syncthreads();
+    }
+    if (scores_out)
+        for (int e = t; e < n_experts; e += kTopkThreads) scores_out[(size_t)m * n_experts + e] = sc[e];
+
+    // candidate keys: (total-order key of score+bias) << 32 | (~index)
+    uint64_t cand[kMaxExperts / kTopkThreads];
+#pragma unroll
+    for (int c = 0; c < kMaxExperts / kTopkThreads; c++) {
+        int e = t + c * kTopkThreads;
+        cand[c] = e < n_experts
+                      ? ((uint64_t)total_key_u(sc[e] + bias[e]) << 32) | (uint32_t)(~(uint32_t)e)
+                      : 0ull;
+    }
+    for (int k = 0; k < top_k; k++) {
+        uint64_t best = 0;
+#pragma unroll
+        for (int c = 0; c < kMaxExperts / kTopkThreads; c++) best = cand[c] > best ? cand[c] : best;
+        best = wave_max_u64(best);
+        if ((t & 63) == 0) wave_best[t >> 6] = best;
+        __syncthreads();
+        best = wave_best[0];
+#pragma unroll
+        for (int wv = 1; wv < kTopkThreads / 64; wv++) best = wave_best[wv] > best ? wave_best[wv] : best;
+        int e = (int)(~(uint32_t)best);
+        if (t == 0) picked[k] = e;
+#pragma unroll
+        for (int c = 0; c < kMaxExperts / kTopkThreads; c++)
+            if (t + c * kTopkThreads == e) cand[c] = 0ull;
+        __syncthreads();
+    }
+    if (t == 0) {
+        float w[kMaxTopk];
+        for (int k = 0; k < top_k; k++) w[k] = sc[picked[k]];
+        // norm 1: moe.rs:61 (only when top_k > 1); norm 2: moe_select's
+        // unconditional normalisation (moe.cu:84-88)
+        if ((norm == 1 && top_k > 1) || norm == 2) {
+            float s = -0.0f;
+            for (int k = 0; k < top_k; k++) s = s + w[k];
+            for (int k = 0; k < top_k; k++) w[k] = w[k] / (s + 1e-20f);
+        }
+        for (int k = 0; k < top_k; k++) {
+            out_idx[(size_t)m * top_k + k] = picked[k];
+            out_w[(size_t)m * top_k + k] = w[k] * route_scale;
+        }
+    }
+}
+
+// Fused single-workgroup gate + select for one token (moe.cu:100 moe_route).
+__global__ __launch_bounds__(1024) void route_fused_kernel(const float *__restrict__ x,
+                                                           const uint16_t *__restrict__ gw,
+                                                           const float *__restrict__ bias,
+                                                           float *__restrict__ out_w,
+                                                           int32_t *__restrict__ out_idx, int dim,
+                                                           int n_experts, int top_k,
+                                                           float route_scale) {
+    __shared__ float sc[kMaxExperts];
+    __shared__ int32_t picked[kMaxTopk];
+    __shared__ uint64_t wave_best[16];
+    const int t = threadIdx.x;
+    if (t < n_experts) {
+        const uint16_t *w = gw + (size_t)t * dim;
+        float s = 0.0f;
+        for (int d = 0; d < dim; d++) s = s + x[d] * __uint_as_float((uint32_t)w[d] << 16);
+        sc[t] = score_fn(s, WS_SCORE_SQRTSOFTPLUS, 1.0f);
+    }
+    __syncthreads();
+    uint64_t cand = t < n_experts
+                        ? ((uint64_t)total_key_u(sc[t] + bias[t]) << 32) | (uint32_t)(~(uint32_t)t)
+                        : 0ull;
+    const int nw = (blockDim.x + 63) / 64;
+    for (int k = 0; k < top_k; k++) {
+        uint64_t best = wave_max_u64(cand);
+        if ((t & 63) == 0) wave_best[t >> 6] = best;
+        __syncthreads();
+        best = wave_best[0];
+        for (int wv = 1; wv < nw; wv++) best = wave_best[wv] > best ? wave_best[wv] : best;
+        int e = (int)(~(uint32_t)best);
+        if (t == 0) picked[k] = e;
+        if (t == e) cand = 0ull;
+        __syncthreads();
+    }
+    if (t == 0) {
+        float w[kMaxTopk];
+        float s = 0.0f;
+        for (int k = 0; k < top_k; k++) {
+            w[k] = sc[picked[k]];
+            s = s + w[k];
+        }
+        for (int k = 0; k < top_k; k++) {
+            out_idx[k] = picked[k];
+            out_w[k] = w[k] / (s + 1e-20f) * route_scale;
+        }
+    }
+}
+
+// Score-only pass (moe_gate / moe_gate_m write scores, no selection).
+__global__ __launch_bounds__(256) void score_kernel(float *__restrict__ v, int64_t n, int score_func) {
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) v[i] = score_fn(v[i], score_func, 1.0f);
+}
+
+static int gate_logits_launch(const float *x, const void *gw, int bf16, float *logits, int64_t m,
+                              int64_t dim, int64_t n_experts, hipStream_t stream) {
+    if (!x || !gw || !logits) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || dim <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
+    if (dim % 8 || m > 65535 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
+    dim3 grid((unsigned)((n_experts + 63) / 64), (unsigned)m);
+    if (bf16)
+        hipLaunchKernelGGL(gate_logits_kernel<true>, grid, dim3(64), 0, stream, x, gw, logits,
+                           (int)dim, (int)n_experts);
+    else
+        hipLaunchKernelGGL(gate_logits_kernel<false>, grid, dim3(64), 0, stream, x, gw, logits,
+                           (int)dim, (int)n_experts);
+    return launch_status();
+}
+
+static int topk_launch(const float *logits, const float *bias, float *scores_out, int32_t *idx,
+                       float *w, int64_t m, int64_t n_experts, int64_t top_k, int score_func,
+                       float gate_temp, int norm, float route_scale, hipStream_t stream) {
+    if (!logits || !bias || !idx || !w) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExperts || top_k > kMaxTopk || top_k > n_experts || m > (1 << 30))
+        return WS_ERR_SHAPE;
+    if (score_func < 0 || score_func > kScoreIdentity) return WS_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)m), dim3(kTopkThreads), 0, stream, logits, bias,
+                       scores_out, idx, w, (int)n_experts, (int)top_k, score_func, gate_temp, norm,
+                       route_scale);
+    return launch_status();
+}
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" {
+
+int ws_moe_gate_logits(const float *x, const void *gate_w, int w_bf16, float *logits, int64_t m,
+                       int64_t dim, int64_t n_experts, ws_stream_t stream) {
+    return gate_logits_launch(x, gate_w, w_bf16, logits, m, dim, n_experts, stream);
+}
+
+int ws_moe_topk(const float *logits, const float *bias, float *scores_out, int32_t *out_idx,
+                float *out_w, int64_t m, int64_t n_experts, int64_t top_k, int score_func,
+                float gate_temp, int norm_topk_prob, float route_scale, ws_stream_t stream) {
+    if (score_func == kScoreIdentity) return WS_ERR_INVALID_ARG;
+    return topk_launch(logits, bias, scores_out, out_idx, out_w, m, n_experts, top_k, score_func,
+                       gate_temp, norm_topk_prob, route_scale, stream);
+}
+
+int ws_moe_gate_m(const float *x, const uint16_t *gate_w, const float *bias, float *scores,
+                  int64_t m, int64_t dim, int64_t n_experts, ws_stream_t stream) {
+    (void)bias;
+    int rc = gate_logits_launch(x, gate_w, 1, scores, m, dim, n_experts, stream);
+    if (rc) return rc;
+    int64_t n = m * n_experts;
+    hipLaunchKernelGGL(score_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, scores,
+                       n, WS_SCORE_SQRTSOFTPLUS);
+    return launch_status();
+}
+
+int ws_moe_gate(const float *x, const uint16_t *gate_w, const float *bias, float *scores,
+                int64_t dim, int64_t n_experts, ws_stream_t stream) {
+    return ws_moe_gate_m(x, gate_w, bias, scores, 1, dim, n_experts, stream);
+}
+
+int ws_moe_select(const float *scores, const float *bias, float *out_w, int32_t *out_idx,
+                  int64_t n_experts, int64_t top_k, float route_scale, ws_stream_t stream) {
+    return topk_launch(scores, bias, nullptr, out_idx, out_w, 1, n_experts, top_k, kScoreIdentity,
+                       1.0f, 2, route_scale, stream);
+}
+
+int ws_moe_route(const float *x, const uint16_t *gate_w, const float *bias, float *out_w,
+                 int32_t *out_idx, int64_t dim, int64_t n_experts, int64_t top_k,
+                 float route_scale, ws_stream_t stream) {
+    if (!x || !gate_w || !bias || !out_w || !out_idx) return WS_ERR_INVALID_ARG;
+    if (dim <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExperts || top_k > kMaxTopk || top_k > n_experts) return WS_ERR_SHAPE;
+    unsigned threads = (unsigned)((n_experts + 63) / 64 * 64);
+    hipLaunchKernelGGL(route_fused_kernel, dim3(1), dim3(threads), 0, stream, x, gate_w, bias, out_w,
+                       out_idx, (int)dim, (int)n_experts, (int)top_k, route_scale);
+    return launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,140 @@
+// Device helpers shared by the gfx950 kernels: the reference's FP8/FP4/UE8M0
+// encodings, the per-32 activation quantiser, wave reductions and the
+// CDNA4 scaled-MFMA wrapper.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ws_expf.h"
+
+namespace ws {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// MFMA operand format codes of v_mfma_scale_f32_*_f8f6f4 (cbsz / blgp).
+constexpr int kFmtFp8 = 0;   // e4m3
+constexpr int kFmtFp4 = 4;   // e2m1
+constexpr int kScaleOne = 127;  // UE8M0 byte of 1.0
+
+// UE8M0 byte -> f32 (weightstream-core quant.rs:41-48): 2^(b-127) built from
+// bits, exact for every byte including b=0 (2^-127, subnormal).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
+    if (b == 0xFF) return __builtin_nanf("");
+    if (b == 0) return __uint_as_float(0x00400000u);
+    return __uint_as_float(b << 23);
+}
+
+// quant.rs:60-73 log2_ceil via the exponent field.
+__device__ __forceinline__ int log2_ceil(float x) {
+    uint32_t bits = __float_as_uint(x);
+    int e = (int)((bits >> 23) & 0xFF) - 127;
+    return (bits & 0x7FFFFF) ? e + 1 : e;
+}
+
+// e4m3fn decode (quant.rs:24-39): sign * 2^(E-7) * (1 + M/8), subnormal M/512.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+    uint32_t e = (b >> 3) & 0xF, m = b & 7;
+    float mag;
+    if (e == 0xF && m == 7) return __builtin_nanf("");
+    if (e == 0) mag = (float)m * (1.0f / 512.0f);
+    else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+    return (b & 0x80) ? -mag : mag;
+}
+
+// f32 -> e4m3 byte exactly as weightstream-core quant.rs:103-137 computes it:
+// RNE, saturating at +-448, NaN -> 0x7F|sign. In the subnormal range a value
+// rounding up to 2^-6 returns 0x38, as the reference does (quant.rs:120-122);
+// inputs reaching that branch are in [15/1024, 2^-6).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
+    uint32_t bits = __float_as_uint(v);
+    uint32_t sign = (bits >> 24) & 0x80;
+    if (v != v) return sign | 0x7F;
+    float a = __builtin_fabsf(v);
+    if (a >= 448.0f) return sign | 0x7E;
+    if (a < 0.015625f) {
+        int m = (int)__builtin_rintf(a * 512.0f);
+        if (m == 8) return sign | 0x38;
+        return sign | (uint32_t)m;
+    }
+    int e = (int)((bits >> 23) & 0xFF) - 127;
+    float q = a * __builtin_ldexpf(1.0f, 3 - e);
+    int m8 = (int)__builtin_rintf(q);
+    int ef = (m8 == 16) ? e + 8 : e + 7;
+    int mant = (m8 == 16) ? 0 : m8 - 8;
+    return sign | (uint32_t)(ef << 3) | (uint32_t)mant;
+}
+
+// Rust f32::clamp (NaN passes through).
+__device__ __forceinline__ float rclamp(float v, float lo, float hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// bf16 RNE of quant.rs:95-101.
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+    uint32_t bits = __float_as_uint(v);
+    uint32_t round = ((bits >> 16) & 1) + 0x7FFF;
+    return (uint16_t)((bits + round) >> 16);
+}
+
+// Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 reduce
+// separately). Max is exact, so the order does not matter.
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// FP8 activation quantisation of one 1x32 block held one value per lane in a
+// 32-lane group (weightstream-ref actquant.rs:21-45 / act_quant_fp8_emit,
+// actquant.cu:47): amax floored at 1e-4, scale 2^log2_ceil(amax/448),
+// q = e4m3(clamp(x/s, +-448)). Returns the e4m3 byte; *scale_byte gets the
+// UE8M0 byte. fmaxf drops NaN like the reference's `a > amax` scan.
+__device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_byte) {
+    float amax = half_wave_max(__builtin_fabsf(x));
+    if (amax < 1e-4f) amax = 1e-4f;
+    int e = log2_ceil(amax / 448.0f);
+    *scale_byte = (uint32_t)(e + 127) & 0xFF;
+    float s = __builtin_ldexpf(1.0f, e);
+    return f32_to_e4m3(rclamp(x / s, -448.0f, 448.0f));
+}
+
+// Scaled MFMA, 16x16 output, K = 128: D += (A * 2^sa) (B * 2^sb) where each
+// lane supplies 32 K-values of its A row / B column and one UE8M0 byte for
+// them (lane l: row/col l%16, K block l/16).
+template <int FMT_A, int FMT_B>
+__device__ __forceinline__ v4f mfma_scaled(const v8i &a, const v8i &b, v4f c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);
+}
+
+// 16-byte global load that bypasses nothing special; kept in one place so the
+// load flavour of every streaming kernel can be changed together.
+__device__ __forceinline__ uint4 ldg16(const uint8_t *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ldg16_stream(const uint8_t *p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+
+__device__ __forceinline__ v8i frag_from(uint4 lo, uint4 hi) {
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+    return r;
+}
+
+__device__ __forceinline__ v8i frag_from4(uint4 lo) {
+    v8i r;
+    r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+    r[4] = 0; r[5] = 0; r[6] = 0; r[7] = 0;
+    return r;
+}
+
+}  // namespace ws

@@ -1,0 +1,194 @@
+"""Host mirror of weightstream-gpu's launch.rs over the HIP C ABI.
+
+One function per reference wrapper, same names and argument order as
+weightstream-gpu/src/launch.rs, minus the `&Cuda` handle, which is replaced
+by an optional `stream=` keyword (the `*_on` variants). Arguments are torch
+device tensors (their data pointers are passed) or plain ints/floats. Every
+call enqueues on the stream and returns immediately; a rejected argument or a
+failed launch raises WsError, where launch.rs panics.
+
+`Hip.global()` mirrors weightstream_cuda::gpu::Cuda::global() (gpu.rs:93):
+one process-wide handle holding `stream` and `aux_stream`.
+"""
+import threading
+
+import torch
+
+from . import _lib
+
+_lock = threading.Lock()
+
+
+class Hip:
+    """Process-wide runtime handle (gpu.rs:42-81): a main and an aux stream."""
+    _inst = None
+
+    def __init__(self):
+        lib = _lib.load()
+        _lib.check("ws_init", lib.ws_init())
+        self.stream = torch.cuda.current_stream()
+        self.aux_stream = torch.cuda.Stream()
+
+    @classmethod
+    def global_(cls):
+        with _lock:
+            if cls._inst is None:
+                cls._inst = Hip()
+            return cls._inst
+
+
+def built_with_hip():
+    """weightstream-cuda lib.rs:11-13 built_with_cuda()."""
+    return bool(_lib.load().ws_built_with_hip())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise ValueError("weightstream_amd expects device tensors")
+    return t.data_ptr()
+
+
+def _s(stream):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _call(name, *args):
+    fn = getattr(_lib.load(), name)
+    _lib.check(name, fn(*args))
+
+
+# ---- actquant.cu (launch.rs:296-326) -------------------------------------
+def snap8(x, n, stream=None):
+    _call("ws_snap8", _ptr(x), n, _s(stream))
+
+
+def emit8(x, q, s, n, stream=None):
+    _call("ws_emit8", _ptr(x), _ptr(q), _ptr(s), n, _s(stream))
+
+
+def emit8_packed(x, q, s, n, stream=None):
+    _call("ws_emit8_packed", _ptr(x), _ptr(q), _ptr(s), n, _s(stream))
+
+
+def pack_scales(src, dst, n, stream=None):
+    _call("ws_pack_scales", _ptr(src), _ptr(dst), n, _s(stream))
+
+
+def act_quant_f32s(x, q, s, m, k, stream=None):
+    _call("ws_act_quant_f32s", _ptr(x), _ptr(q), _ptr(s), m, k, _s(stream))
+
+
+def weight_quant_fp4(w, q, s, rows, cols, stream=None):
+    _call("ws_weight_quant_fp4", _ptr(w), _ptr(q), _ptr(s), rows, cols, _s(stream))
+
+
+def weight_quant_fp8(w, q, s, rows, cols, stream=None):
+    _call("ws_weight_quant_fp8", _ptr(w), _ptr(q), _ptr(s), rows, cols, _s(stream))
+
+
+# ---- GEMMs (launch.rs:344-377, 717-804) -------------------------------------
+def fp8_gemm(a, sa, b, sb, out, m, n, k, stream=None):
+    _call("ws_fp8_gemm", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k, _s(stream))
+
+
+def fp8_gemm_on(a, sa, b, sb, out, m, n, k, stream):
+    fp8_gemm(a, sa, b, sb, out, m, n, k, stream=stream)
+
+
+def fp8_gemm_tile(a, sa, b, sb, out, m, n, k, stream=None):
+    _call("ws_fp8_gemm_tile", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k,
+          _s(stream))
+
+
+def fp8_gemm_bf16(a, sa, b, sb, out, m, n, k, stream=None):
+    _call("ws_fp8_gemm_bf16", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k,
+          _s(stream))
+
+
+def fp8_gemm_f32s(a, sa, b, sb, out, m, n, k, out_bf16=False, stream=None):
+    _call("ws_fp8_gemm_f32s", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), int(out_bf16),
+          m, n, k, _s(stream))
+
+
+def fp4_gemm(a, sa, b, sb, out, m, n, k, stream=None):
+    _call("ws_fp4_gemm", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k, _s(stream))
+
+
+def fp4_gemm_tile(a, sa, b, sb, out, m, n, k, stream=None):
+    _call("ws_fp4_gemm_tile", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k,
+          _s(stream))
+
+
+# ---- routing (launch.rs:998-1100) ---------------------------------------------
+SCORE_SOFTMAX, SCORE_SIGMOID, SCORE_SQRTSOFTPLUS = 0, 1, 2
+
+
+def moe_gate_logits(x, gate_w, logits, m, dim, n_experts, stream=None):
+    bf16 = gate_w.dtype in (torch.bfloat16, torch.int16, torch.uint16)
+    _call("ws_moe_gate_logits", _ptr(x), _ptr(gate_w), int(bf16), _ptr(logits), m, dim,
+          n_experts, _s(stream))
+
+
+def moe_topk(logits, bias, scores_out, out_idx, out_w, m, n_experts, top_k,
+             score_func=SCORE_SIGMOID, gate_temp=1.0, norm_topk_prob=True, route_scale=1.0,
+             stream=None):
+    _call("ws_moe_topk", _ptr(logits), _ptr(bias), _ptr(scores_out), _ptr(out_idx),
+          _ptr(out_w), m, n_experts, top_k, score_func, gate_temp, int(norm_topk_prob),
+          route_scale, _s(stream))
+
+
+def moe_gate(x, gate_w, bias, scores, dim, n_experts, stream=None):
+    _call("ws_moe_gate", _ptr(x), _ptr(gate_w), _ptr(bias), _ptr(scores), dim, n_experts,
+          _s(stream))
+
+
+def moe_gate_m(x, gate_w, bias, scores, m, dim, n_experts, stream=None):
+    _call("ws_moe_gate_m", _ptr(x), _ptr(gate_w), _ptr(bias), _ptr(scores), m, dim, n_experts,
+          _s(stream))
+
+
+def moe_select(scores, bias, out_w, out_i, n_experts, top_k, route_scale, stream=None):
+    _call("ws_moe_select", _ptr(scores), _ptr(bias), _ptr(out_w), _ptr(out_i), n_experts, top_k,
+          route_scale, _s(stream))
+
+
+def moe_route(x, gate_w, bias, out_w, out_i, dim, n_experts, top_k, route_scale, stream=None):
+    _call("ws_moe_route", _ptr(x), _ptr(gate_w), _ptr(bias), _ptr(out_w), _ptr(out_i), dim,
+          n_experts, top_k, route_scale, _s(stream))
+
+
+def swiglu(gate, up, out, n, rw, stream=None):
+    _call("ws_swiglu", _ptr(gate), _ptr(up), _ptr(out), n, rw, _s(stream))
+
+
+# ---- routed experts, decode (launch.rs:89-206) ---------------------------------
+def expert_glu_quant(act_x, act_x_s, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slots, s_slots,
+                     n, k, n_experts, top_k, swiglu_limit=10.0, stream=None):
+    """expert_glu + expert_quant fused: rows of q_slots/s_slots are the picks
+    in ascending expert id."""
+    _call("ws_expert_glu_quant", _ptr(act_x), _ptr(act_x_s), _ptr(topk_idx), _ptr(topk_w),
+          _ptr(w1), _ptr(w1_s), _ptr(w3), _ptr(w3_s), _ptr(q_slots), _ptr(s_slots), k, n,
+          n_experts, top_k, swiglu_limit, _s(stream))
+
+
+def expert_reduce(act_slots, act_s_slots, w2, w2_s, gate_idx, y, dim, inter, n_experts, top_k,
+                  stream=None):
+    _call("ws_expert_reduce", _ptr(act_slots), _ptr(act_s_slots), _ptr(gate_idx), _ptr(w2),
+          _ptr(w2_s), _ptr(y), dim, inter, n_experts, top_k, _s(stream))
+
+
+def moe_decode_workspace_size(dim, inter, top_k):
+    return int(_lib.load().ws_moe_decode_workspace_size(dim, inter, top_k))
+
+
+def moe_decode(x, topk_idx, topk_w, w1, s1, w3, s3, w2, s2, y, dim, inter, n_experts, top_k,
+               workspace, swiglu_limit=10.0, stream=None):
+    _call("ws_moe_decode", _ptr(x), _ptr(topk_idx), _ptr(topk_w), _ptr(w1), _ptr(s1), _ptr(w3),
+          _ptr(s3), _ptr(w2), _ptr(s2), _ptr(y), dim, inter, n_experts, top_k, swiglu_limit,
+          _ptr(workspace), workspace.numel() * workspace.element_size(), _s(stream))
