@@ -183,6 +183,59 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,
                   int64_t n_experts, int64_t top_k, float swiglu_limit, void *workspace,
                   size_t workspace_bytes, ws_stream_t stream);
 
+/* ---------------------------------------------------------------------
+ * Routed experts, M tokens (grouped prefill / batched decode). Replaces the
+ * TileLang pipeline of engine.rs:4125-4243 (moe_dispatch_tl launch.rs:430,
+ * moe_grouped_tl(_cached)(_on) :478-580, moe_swiglu_route :673,
+ * moe_combine_f32 :689). Routes r = token * top_k + j.
+ * ------------------------------------------------------------------- */
+/* launch.rs:430-468 moe_dispatch_tl (moe_dispatch.cu:17): per-expert counts,
+ * 32-padded offsets in ascending expert id (exclusive scan), psum = offset +
+ * count, order[slot] = route or -1 (padding), layout_w[slot] = route weight or
+ * 0, route_pos[route] = slot (-1 for an expert id outside [0,E)),
+ * tile_expert[t] = expert of 32-slot tile t or -1, num_tiles[0] = used tiles.
+ * Inside an expert the routes keep ascending route index. Slots >= tiles*32
+ * are not written. topk_idx is int32 (the reference kernel takes int64). */
+int ws_moe_dispatch(const int32_t *topk_idx, const float *topk_w, int32_t *order,
+                    float *layout_w, int32_t *route_pos, int32_t *tile_expert,
+                    int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
+                    int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
+                    int64_t n_experts, ws_stream_t stream);
+/* Grouped gate/up (moe_grouped_tl GateUp) fused with moe_swiglu_route and the
+ * FP8 emit: for every used tile, the 32 slots' tokens (xq [rows, dim] e4m3,
+ * xs [rows, dim/32]) against the expert's w1/w3 rows; h = silu(min(g,L)) *
+ * clamp(u,+-L) * layout_w[slot] quantised per 1x32 to hq [tiles*32, inter] +
+ * hs [tiles*32, inter/32]; padding slots get h = 0. */
+int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *order,
+                             const float *layout_w, const int32_t *tile_expert,
+                             const int32_t *num_tiles, const uint8_t *w1, const uint8_t *s1,
+                             const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                             int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                             int64_t tiles, float swiglu_limit, ws_stream_t stream);
+/* Grouped down (moe_grouped_tl Down): out [tiles*32, dim] f32 = hq . w2_e^T
+ * for every used tile. */
+int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+                        const int32_t *num_tiles, const uint8_t *w2, const uint8_t *s2,
+                        float *out, int64_t dim, int64_t inter, int64_t n_experts, int64_t tiles,
+                        ws_stream_t stream);
+/* moe_combine_f32 (moe_grouped.cu:260): y[row] = sum of out[route_pos[row,
+ * j]] over j, added in ascending slot order, i.e. ascending expert id (the
+ * reference kernel adds in top-k order; moe.rs:76-84 adds by expert id). */
+int ws_moe_combine(const float *down, const int32_t *route_pos, float *y, int64_t rows,
+                   int64_t dim, int64_t top_k, int64_t tiles, ws_stream_t stream);
+/* Whole routed MoE for `rows` tokens from f32 x [rows, dim] and routing
+ * (topk_idx/topk_w [rows, top_k]): emit8 -> dispatch -> grouped glu_quant ->
+ * grouped down -> combine into y [rows, dim]. tiles = ceil(rows*top_k/32) +
+ * min(rows*top_k, E) (engine.rs:4131). workspace >=
+ * ws_moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts). */
+size_t ws_moe_prefill_workspace_size(int64_t rows, int64_t dim, int64_t inter, int64_t top_k,
+                                     int64_t n_experts);
+int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
+                   const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
+                   const uint8_t *w2, const uint8_t *s2, float *y, int64_t rows, int64_t dim,
+                   int64_t inter, int64_t n_experts, int64_t top_k, float swiglu_limit,
+                   void *workspace, size_t workspace_bytes, ws_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,7 +72,7 @@ SIGNATURES = {
     "ws_moe_dispatch": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_grouped_glu_quant": (_i, [_p] * 12 + [_i64, _i64, _i64, _i64, _i64, _f, _p]),
     "ws_moe_grouped_down": (_i, [_p] * 7 + [_i64, _i64, _i64, _i64, _p]),
-    "ws_moe_combine": (_i, [_p] * 3 + [_i64, _i64, _i64, _p]),
+    "ws_moe_combine": (_i, [_p] * 3 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_prefill_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "ws_moe_prefill": (_i, [_p] * 10 + [_i64] * 5 + [_f, _p, C.c_size_t, _p]),
 }

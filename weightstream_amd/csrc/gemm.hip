@@ -12,9 +12,12 @@
 //    FP4 weight (1x32) granularity; FP8 32x32 weight scales are broadcast to
 //    the 32 rows of their block. The f32-scale scheme runs the MFMA with unit
 //    scales and applies sa*sb once per 128-K step in f32.
-//  - lane l holds row/col (l % 16) and K block (l / 16) of each fragment:
-//    16-byte global loads, 64 (fp8) or 32 (fp4) contiguous bytes per row and
-//    step, no LDS staging of the streamed operand.
+//  - fragment layout (measured on gfx950): lane l holds row/col l % 16; with
+//    g = l / 16, an FP8 lane holds K [16g, 16g+16) and [64+16g, 64+16g+16) of
+//    the 128-K step, an FP4 lane holds K [32g, 32g+32) (low nibble = even K),
+//    and the lane's UE8M0 byte scales K block [32g, 32g+32) of its row in
+//    both cases. The four lanes of a row therefore read 128 contiguous FP8
+//    bytes (64 FP4 bytes) per step with 16-byte loads; no LDS staging.
 //  - a workgroup is GM x GK waves: GM waves along M share the weight
 //    fragments through L1/L2; GK waves split K and are reduced through LDS in
 //    wave order (deterministic).
@@ -58,14 +61,14 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 #pragma unroll
     for (int i = 0; i < WM; i++) {
         int row = min(m_base + i * 16 + r, M - 1);
-        arow[i] = A + (size_t)row * K + kb * 32;
+        arow[i] = A + (size_t)row * K + kb * 16;
         if (SMODE == kUe8m0) sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
     }
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         int col = min(n_base + j * 16 + r, N - 1);
         col_of[j] = col;
-        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + kb * 16 : B + (size_t)col * K + kb * 32;
+        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + kb * 16 : B + (size_t)col * K + kb * 16;
         if (SMODE == kUe8m0)
             sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
     }
@@ -93,7 +96,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                 for (int i = 0; i < WM; i++) {
                     const uint8_t *p = arow[i] + (size_t)ks * 128;
                     af[u][i][0] = ldg16(p);
-                    af[u][i][1] = ldg16(p + 16);
+                    af[u][i][1] = ldg16(p + 64);
                     if (SMODE == kUe8m0)
                         sav[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
                 }
@@ -104,7 +107,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                     } else {
                         const uint8_t *p = brow[j] + (size_t)ks * 128;
                         bf[u][j][0] = ldg16_stream(p);
-                        bf[u][j][1] = ldg16_stream(p + 16);
+                        bf[u][j][1] = ldg16_stream(p + 64);
                     }
                     if (SMODE == kUe8m0)
                         sbv[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);

@@ -66,8 +66,8 @@ __device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_row
         for (int u = 0; u < kU; u++) {
             int ks = ks0 + u;
             if (ks < ksteps) {
-                const uint4 *xp = (const uint4 *)(xq_lds + ks * 128 + kb * 32);
-                v8i b = frag_from(xp[0], xp[1]);
+                const uint8_t *xp = xq_lds + ks * 128 + kb * 16;
+                v8i b = frag_from(*(const uint4 *)xp, *(const uint4 *)(xp + 64));
                 int sx = xs_lds[ks * 4 + kb];
                 acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(wf[u]), b, acc, (int)ws_[u], sx);
             }

@@ -1,0 +1,450 @@
+// Grouped (M-token) routed-expert MoE: dispatch, grouped gate/up + SwiGLU +
+// FP8 re-quantisation, grouped down projection, ordered combine.
+//
+// Replaces the reference's TileLang pipeline moe_dispatch_kernel ->
+// moe_grouped_fp8_fp4_gemm_kernel (gate/up) -> moe_swiglu_route ->
+// emit8_packed -> moe_grouped_fp8_fp4_gemm_kernel (down) -> moe_combine_f32
+// (weightstream-cuda/kernels/tilelang/moe_dispatch.cu:17, moe_gate_up.cu,
+// moe_down.cu, moe_grouped.cu:239,260; launch.rs:430-689; engine.rs:4125-4243).
+// The TileLang kernels hard-code 96 local experts, 512 routes, K=5120/2304;
+// these kernels take E <= 1024 experts, any route count and any dim/inter that
+// are multiples of 128. CPU semantics: weightstream-ref moe.rs:75-84,162-208
+// per token.
+//
+// Layout: routes r = token * top_k + j. The dispatch places each expert's
+// routes contiguously (ascending route index), padded to 32-slot tiles, the
+// experts in ascending id. A tile is 32 slots of one expert, so its weight
+// rows are streamed once for up to 32 tokens; the grouped kernels gather the
+// tokens' FP8 rows (L2-resident) as the MFMA's A operand and stream the
+// expert's FP4 rows as B. Tiles past the used count exit at once, so the grid
+// is sized from the host-known upper bound and nothing is read back.
+// Because slots ascend with expert id, the combine sums each token's expert
+// outputs in ascending expert id, the reference CPU order.
+#include "ws_internal.hpp"
+
+namespace ws {
+
+constexpr int kDispThreads = 1024;
+constexpr int kMaxExpertsG = 1024;
+constexpr int kTile = 32;
+
+// ---- dispatch (one workgroup) -------------------------------------------
+__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
+    const int32_t *__restrict__ idx, const float *__restrict__ wts, int32_t *__restrict__ order,
+    float *__restrict__ layout_w, int32_t *__restrict__ route_pos,
+    int32_t *__restrict__ tile_expert, int32_t *__restrict__ count_out,
+    int32_t *__restrict__ offset_out, int32_t *__restrict__ psum_out,
+    int32_t *__restrict__ num_tiles_out, int routes, int tiles, int n_experts) {
+    __shared__ int32_t base[kMaxExpertsG];
+    __shared__ int32_t wcnt[kDispThreads / 64][kMaxExpertsG];
+    __shared__ int32_t scan[kMaxExpertsG];
+    __shared__ int32_t wsum[kDispThreads / 64];
+    const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+    base[t] = 0;
+    __syncthreads();
+    // pass 1: stable rank of every route inside its expert
+    for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
+        const int r = c0 + t;
+        const int e = r < routes ? idx[r] : -1;
+        const bool valid = e >= 0 && e < n_experts;
+#pragma unroll
+        for (int ww = 0; ww < kDispThreads / 64; ww++) wcnt[ww][t] = 0;
+        __syncthreads();
+        int inrank = 0, cnt = 0;
+        for (int l = 0; l < 64; l++) {
+            int el = __shfl(e, l, 64);
+            bool same = el == e;
+            cnt += same;
+            inrank += (same && l < lane);
+        }
+        if (valid && inrank == 0) wcnt[w][e] = cnt;
+        __syncthreads();
+        if (t < n_experts) {
+            int run = base[t];
+#pragma unroll
+            for (int ww = 0; ww < kDispThreads / 64; ww++) {
+                int v = wcnt[ww][t];
+                wcnt[ww][t] = run;
+                run += v;
+            }
+            base[t] = run;
+        }
+        __syncthreads();
+        if (valid) route_pos[r] = wcnt[w][e] + inrank;
+        __syncthreads();
+    }
+    // exclusive scan of the 32-padded counts over experts
+    const int count = t < n_experts ? base[t] : 0;
+    const int padded = (count + kTile - 1) / kTile * kTile;
+    int v = padded;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    int wbase = 0;
+    for (int ww = 0; ww < w; ww++) wbase += wsum[ww];
+    int total = 0;
+    for (int ww = 0; ww < kDispThreads / 64; ww++) total += wsum[ww];
+    const int offset = wbase + v - padded;
+    scan[t] = offset;
+    const int used = total / kTile;
+    const int cap = tiles * kTile;
+    if (t < n_experts) {
+        count_out[t] = count;
+        offset_out[t] = offset;
+        psum_out[t] = offset + count;
+        for (int i = count; i < padded; i++) {
+            int slot = offset + i;
+            if (slot < cap) {
+                order[slot] = -1;
+                layout_w[slot] = 0.0f;
+            }
+        }
+        for (int tt = 0; tt < padded / kTile; tt++) {
+            int ti = offset / kTile + tt;
+            if (ti < tiles) tile_expert[ti] = t;
+        }
+    }
+    if (t == 0) *num_tiles_out = used;
+    for (int ti = used + t; ti < tiles; ti += kDispThreads) tile_expert[ti] = -1;
+    __syncthreads();
+    // pass 2: slots
+    for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
+        const int r = c0 + t;
+        if (r >= routes) break;
+        const int e = idx[r];
+        if (e < 0 || e >= n_experts) {
+            route_pos[r] = -1;
+            continue;
+        }
+        const int slot = scan[e] + route_pos[r];
+        if (slot < cap) {
+            order[slot] = r;
+            layout_w[slot] = wts[r];
+        }
+        route_pos[r] = slot;
+    }
+}
+
+// ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
+// grid (inter/32, tiles), 4 waves: wave (mat = w>>1, half = w&1) computes the
+// 32 slots x 16 output columns of w1 (mat 0) or w3 (mat 1).
+__global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
+    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs,
+    const int32_t *__restrict__ order, const float *__restrict__ layout_w,
+    const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ num_tiles,
+    const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
+    const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
+    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
+    __shared__ float gu[2][kTile][kTile + 1];
+    const int tile = blockIdx.y;
+    if (tile >= *num_tiles) return;
+    const int e = tile_expert[tile];
+    if (e < 0 || e >= n_experts) return;
+    const int nt = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int r = lane & 15, kb = lane >> 4;
+    const int slot0 = tile * kTile;
+    const int mat = w >> 1, half = w & 1;
+
+    const uint8_t *arow[2];
+    const uint8_t *srow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        int route = order[slot0 + i * 16 + r];
+        int tok = route >= 0 ? route / top_k : 0;
+        arow[i] = xq + (size_t)tok * dim + kb * 16;
+        srow[i] = xs + (size_t)tok * (dim / 32);
+    }
+    const int n = nt * kTile + half * 16 + r;
+    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
+    const uint8_t *bp = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)n * (dim / 2) + kb * 16;
+    const uint8_t *sp = (mat ? s3 : s1) + (size_t)e * smat + (size_t)n * (dim / 32);
+
+    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    const int ksteps = dim / 128;
+    constexpr int U = 4;
+    for (int ks0 = 0; ks0 < ksteps; ks0 += U) {
+        uint4 bf[U], af[U][2][2];
+        uint32_t sb[U], sa[U][2];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int ks = ks0 + u;
+            if (ks < ksteps) {
+                bf[u] = ldg16_stream(bp + (size_t)ks * 64);
+                sb[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    af[u][i][0] = ldg16(arow[i] + ks * 128);
+                    af[u][i][1] = ldg16(arow[i] + ks * 128 + 64);
+                    sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (ks0 + u < ksteps) {
+                v8i b = frag_from4(bf[u]);
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(frag_from(af[u][i][0], af[u][i][1]), b,
+                                                           acc[i], (int)sa[u][i], (int)sb[u]);
+            }
+        }
+    }
+    // D[m][n]: m = slot row 4*(lane/16)+v of fragment i, n = lane%16
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) gu[mat][i * 16 + 4 * kb + v][half * 16 + r] = acc[i][v];
+    __syncthreads();
+    // epilogue: a half-wave per slot row (32 values = one FP8 block)
+    const int col = t & 31;
+    for (int srow_i = t >> 5; srow_i < kTile; srow_i += 8) {
+        const int slot = slot0 + srow_i;
+        const bool pad = order[slot] < 0;
+        float g = gu[0][srow_i][col], u = gu[1][srow_i][col];
+        if (limit > 0.0f) {
+            u = rclamp(u, -limit, limit);
+            g = fminf(g, limit);
+        }
+        float h = pad ? 0.0f : ws_silu(g) * u * layout_w[slot];
+        uint32_t sbyte;
+        uint32_t q = quant_fp8_block32(h, &sbyte);
+        hq[(size_t)slot * inter + nt * kTile + col] = (uint8_t)q;
+        if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
+    }
+}
+
+// ---- grouped down ---------------------------------------------------------
+// grid (dim/64, tiles), 4 waves: wave w computes 32 slots x 16 output columns
+// (columns nt*64 + w*16 ..) of the expert's w2; f32 out[slot, dim].
+__global__ __launch_bounds__(256) void grouped_down_kernel(
+    const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs,
+    const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ num_tiles,
+    const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
+    int dim, int inter, int n_experts) {
+    const int tile = blockIdx.y;
+    if (tile >= *num_tiles) return;
+    const int e = tile_expert[tile];
+    if (e < 0 || e >= n_experts) return;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int r = lane & 15, kb = lane >> 4;
+    const int slot0 = tile * kTile;
+    const int n = blockIdx.x * 64 + w * 16 + r;
+    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
+    const uint8_t *bp = w2 + (size_t)e * wmat + (size_t)n * (inter / 2) + kb * 16;
+    const uint8_t *sp = s2 + (size_t)e * smat + (size_t)n * (inter / 32);
+    const uint8_t *arow[2];
+    const uint8_t *srow[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        arow[i] = hq + (size_t)(slot0 + i * 16 + r) * inter + kb * 16;
+        srow[i] = hs + (size_t)(slot0 + i * 16 + r) * (inter / 32);
+    }
+    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    const int ksteps = inter / 128;
+    constexpr int U = 4;
+    for (int ks0 = 0; ks0 < ksteps; ks0 += U) {
+        uint4 bf[U], af[U][2][2];
+        uint32_t sb[U], sa[U][2];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int ks = ks0 + u;
+            if (ks < ksteps) {
+                bf[u] = ldg16_stream(bp + (size_t)ks * 64);
+                sb[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    af[u][i][0] = ldg16(arow[i] + ks * 128);
+                    af[u][i][1] = ldg16(arow[i] + ks * 128 + 64);
+                    sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (ks0 + u < ksteps) {
+                v8i b = frag_from4(bf[u]);
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(frag_from(af[u][i][0], af[u][i][1]), b,
+                                                           acc[i], (int)sa[u][i], (int)sb[u]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            out[(size_t)(slot0 + i * 16 + 4 * kb + v) * dim + n] = acc[i][v];
+}
+
+// ---- combine: y[row] = sum of its routes' outputs in ascending slot order --
+__global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ down,
+                                                      const int32_t *__restrict__ route_pos,
+                                                      float *__restrict__ y, int dim, int top_k,
+                                                      int cap) {
+    __shared__ int32_t slots[16];
+    __shared__ int32_t ns;
+    const int row = blockIdx.y;
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int j = 0; j < top_k; j++) {
+            int s = route_pos[(size_t)row * top_k + j];
+            if (s < 0 || s >= cap) continue;
+            int i = n++;
+            while (i > 0 && slots[i - 1] > s) {
+                slots[i] = slots[i - 1];
+                i--;
+            }
+            slots[i] = s;
+        }
+        ns = n;
+    }
+    __syncthreads();
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    if (d >= dim) return;
+    float acc = 0.0f;
+    for (int i = 0; i < ns; i++) acc = acc + down[(size_t)slots[i] * dim + d];
+    y[(size_t)row * dim + d] = acc;
+}
+
+static inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+static inline bool al4(const void *p) { return ((uintptr_t)p & 3) == 0; }
+static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static int64_t tiles_for(int64_t routes, int64_t n_experts) {
+    return (routes + kTile - 1) / kTile + (routes < n_experts ? routes : n_experts);
+}
+
+}  // namespace ws
+
+using namespace ws;
+
+extern "C" {
+
+int ws_moe_dispatch(const int32_t *topk_idx, const float *topk_w, int32_t *order,
+                    float *layout_w, int32_t *route_pos, int32_t *tile_expert,
+                    int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
+                    int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
+                    int64_t n_experts, ws_stream_t stream) {
+    if (!topk_idx || !topk_w || !order || !layout_w || !route_pos || !tile_expert ||
+        !expert_count || !expert_offset || !expert_psum || !num_tiles)
+        return WS_ERR_INVALID_ARG;
+    if (rows <= 0 || top_k <= 0 || tiles <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExpertsG || rows * top_k > (1 << 26) || tiles > (1 << 24))
+        return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, stream, topk_idx, topk_w,
+                       order, layout_w, route_pos, tile_expert, expert_count, expert_offset,
+                       expert_psum, num_tiles, (int)(rows * top_k), (int)tiles, (int)n_experts);
+    return launch_status();
+}
+
+int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *order,
+                             const float *layout_w, const int32_t *tile_expert,
+                             const int32_t *num_tiles, const uint8_t *w1, const uint8_t *s1,
+                             const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                             int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                             int64_t tiles, float swiglu_limit, ws_stream_t stream) {
+    if (!xq || !xs || !order || !layout_w || !tile_expert || !num_tiles || !w1 || !s1 || !w3 ||
+        !s3 || !hq || !hs)
+        return WS_ERR_INVALID_ARG;
+    if (dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0 || tiles <= 0)
+        return WS_ERR_INVALID_ARG;
+    if (dim % 128 || inter % 128 || tiles > 65535 || dim > (1 << 20) || inter > (1 << 20))
+        return WS_ERR_SHAPE;
+    if (!al16(xq) || !al16(w1) || !al16(w3) || !al4(xs) || !al4(s1) || !al4(s3))
+        return WS_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(grouped_glu_quant_kernel, dim3((unsigned)(inter / 32), (unsigned)tiles),
+                       dim3(256), 0, stream, xq, xs, order, layout_w, tile_expert, num_tiles, w1,
+                       s1, w3, s3, hq, hs, (int)dim, (int)inter, (int)n_experts, (int)top_k,
+                       swiglu_limit);
+    return launch_status();
+}
+
+int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+                        const int32_t *num_tiles, const uint8_t *w2, const uint8_t *s2,
+                        float *out, int64_t dim, int64_t inter, int64_t n_experts, int64_t tiles,
+                        ws_stream_t stream) {
+    if (!hq || !hs || !tile_expert || !num_tiles || !w2 || !s2 || !out) return WS_ERR_INVALID_ARG;
+    if (dim <= 0 || inter <= 0 || n_experts <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
+    if (dim % 128 || inter % 128 || tiles > 65535) return WS_ERR_SHAPE;
+    if (!al16(hq) || !al16(w2) || !al4(hs) || !al4(s2)) return WS_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(grouped_down_kernel, dim3((unsigned)(dim / 64), (unsigned)tiles), dim3(256),
+                       0, stream, hq, hs, tile_expert, num_tiles, w2, s2, out, (int)dim,
+                       (int)inter, (int)n_experts);
+    return launch_status();
+}
+
+int ws_moe_combine(const float *down, const int32_t *route_pos, float *y, int64_t rows,
+                   int64_t dim, int64_t top_k, int64_t tiles, ws_stream_t stream) {
+    if (!down || !route_pos || !y) return WS_ERR_INVALID_ARG;
+    if (rows <= 0 || dim <= 0 || top_k <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
+    if (top_k > 16 || rows > 65535) return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((dim + 255) / 256), (unsigned)rows),
+                       dim3(256), 0, stream, down, route_pos, y, (int)dim, (int)top_k,
+                       (int)(tiles * kTile));
+    return launch_status();
+}
+
+size_t ws_moe_prefill_workspace_size(int64_t rows, int64_t dim, int64_t inter, int64_t top_k,
+                                     int64_t n_experts) {
+    if (rows <= 0 || dim <= 0 || inter <= 0 || top_k <= 0 || n_experts <= 0) return 0;
+    const int64_t routes = rows * top_k, tiles = tiles_for(routes, n_experts);
+    const int64_t slots = tiles * kTile;
+    return a256(rows * dim) + a256(rows * (dim / 32)) + a256(slots * 4) * 2 + a256(routes * 4) +
+           a256(tiles * 4) + a256(n_experts * 4) * 3 + a256(4) + a256(slots * inter) +
+           a256(slots * (inter / 32)) + a256(slots * dim * 4);
+}
+
+int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
+                   const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
+                   const uint8_t *w2, const uint8_t *s2, float *y, int64_t rows, int64_t dim,
+                   int64_t inter, int64_t n_experts, int64_t top_k, float swiglu_limit,
+                   void *workspace, size_t workspace_bytes, ws_stream_t stream) {
+    if (!x || !topk_idx || !topk_w || !y || !workspace) return WS_ERR_INVALID_ARG;
+    if (rows <= 0 || dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0)
+        return WS_ERR_INVALID_ARG;
+    if (workspace_bytes < ws_moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts) ||
+        !al16(workspace))
+        return WS_ERR_INVALID_ARG;
+    const int64_t routes = rows * top_k, tiles = tiles_for(routes, n_experts);
+    const int64_t slots = tiles * kTile;
+    uint8_t *p = (uint8_t *)workspace;
+    auto take = [&](size_t bytes) {
+        uint8_t *q = p;
+        p += a256(bytes);
+        return q;
+    };
+    uint8_t *xq = take(rows * dim);
+    uint8_t *xs = take(rows * (dim / 32));
+    int32_t *order = (int32_t *)take(slots * 4);
+    float *layout_w = (float *)take(slots * 4);
+    int32_t *route_pos = (int32_t *)take(routes * 4);
+    int32_t *tile_expert = (int32_t *)take(tiles * 4);
+    int32_t *cnt = (int32_t *)take(n_experts * 4);
+    int32_t *off = (int32_t *)take(n_experts * 4);
+    int32_t *psum = (int32_t *)take(n_experts * 4);
+    int32_t *ntiles = (int32_t *)take(4);
+    uint8_t *hq = take(slots * inter);
+    uint8_t *hs = take(slots * (inter / 32));
+    float *down = (float *)take(slots * dim * 4);
+    int rc = ws_emit8(x, xq, xs, rows * dim, stream);
+    if (rc) return rc;
+    rc = ws_moe_dispatch(topk_idx, topk_w, order, layout_w, route_pos, tile_expert, cnt, off, psum,
+                         ntiles, rows, top_k, tiles, n_experts, stream);
+    if (rc) return rc;
+    rc = ws_moe_grouped_glu_quant(xq, xs, order, layout_w, tile_expert, ntiles, w1, s1, w3, s3, hq,
+                                  hs, dim, inter, n_experts, top_k, tiles, swiglu_limit, stream);
+    if (rc) return rc;
+    rc = ws_moe_grouped_down(hq, hs, tile_expert, ntiles, w2, s2, down, dim, inter, n_experts,
+                             tiles, stream);
+    if (rc) return rc;
+    return ws_moe_combine(down, route_pos, y, rows, dim, top_k, tiles, stream);
+}
+
+}  // extern "C"

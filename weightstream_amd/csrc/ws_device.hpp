@@ -102,9 +102,13 @@ __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_b
     return f32_to_e4m3(rclamp(x / s, -448.0f, 448.0f));
 }
 
-// Scaled MFMA, 16x16 output, K = 128: D += (A * 2^sa) (B * 2^sb) where each
-// lane supplies 32 K-values of its A row / B column and one UE8M0 byte for
-// them (lane l: row/col l%16, K block l/16).
+// Scaled MFMA, 16x16 output, K = 128: D += (A * 2^sa) (B * 2^sb).
+// Operand layout (measured on gfx950): lane l supplies row (A) / column (B)
+// l % 16. With g = l / 16, an FP8 operand lane holds K [16g, 16g+16) in its
+// bytes 0-15 and K [64+16g, 64+16g+16) in bytes 16-31; an FP4 operand lane
+// holds K [32g, 32g+32) in bytes 0-15, low nibble first. The UE8M0 byte of
+// lane l scales K block [32g, 32g+32) of its row/column, for either format.
+// D: lane l, element v holds row 4*(l/16)+v, column l%16.
 template <int FMT_A, int FMT_B>
 __device__ __forceinline__ v4f mfma_scaled(const v8i &a, const v8i &b, v4f c, int sa, int sb) {
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);

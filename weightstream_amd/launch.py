@@ -192,3 +192,49 @@ def moe_decode(x, topk_idx, topk_w, w1, s1, w3, s3, w2, s2, y, dim, inter, n_exp
     _call("ws_moe_decode", _ptr(x), _ptr(topk_idx), _ptr(topk_w), _ptr(w1), _ptr(s1), _ptr(w3),
           _ptr(s3), _ptr(w2), _ptr(s2), _ptr(y), dim, inter, n_experts, top_k, swiglu_limit,
           _ptr(workspace), workspace.numel() * workspace.element_size(), _s(stream))
+
+
+# ---- routed experts, M tokens (launch.rs:430-689) -------------------------------
+def moe_tiles(routes, n_experts):
+    """Upper bound on 32-slot tiles (engine.rs:4131, 6232-6233)."""
+    return (routes + 31) // 32 + min(routes, n_experts)
+
+
+def moe_dispatch_tl(topk_idx, topk_weights, order, layout_weights, route_pos, tile_expert,
+                    expert_count, expert_offset, expert_psum, num_tiles, rows, top_k, tiles,
+                    n_experts, stream=None):
+    _call("ws_moe_dispatch", _ptr(topk_idx), _ptr(topk_weights), _ptr(order),
+          _ptr(layout_weights), _ptr(route_pos), _ptr(tile_expert), _ptr(expert_count),
+          _ptr(expert_offset), _ptr(expert_psum), _ptr(num_tiles), rows, top_k, tiles, n_experts,
+          _s(stream))
+
+
+def moe_grouped_glu_quant(xq, xs, order, layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq,
+                          hs, dim, inter, n_experts, top_k, tiles, swiglu_limit=10.0,
+                          stream=None):
+    _call("ws_moe_grouped_glu_quant", _ptr(xq), _ptr(xs), _ptr(order), _ptr(layout_w),
+          _ptr(tile_expert), _ptr(num_tiles), _ptr(w1), _ptr(s1), _ptr(w3), _ptr(s3), _ptr(hq),
+          _ptr(hs), dim, inter, n_experts, top_k, tiles, swiglu_limit, _s(stream))
+
+
+def moe_grouped_down(hq, hs, tile_expert, num_tiles, w2, s2, out, dim, inter, n_experts, tiles,
+                     stream=None):
+    _call("ws_moe_grouped_down", _ptr(hq), _ptr(hs), _ptr(tile_expert), _ptr(num_tiles),
+          _ptr(w2), _ptr(s2), _ptr(out), dim, inter, n_experts, tiles, _s(stream))
+
+
+def moe_combine_f32(y, route_pos, out, dim, top_k, rows, tiles, stream=None):
+    """launch.rs:689 argument order (y = grouped down output, out = result)."""
+    _call("ws_moe_combine", _ptr(y), _ptr(route_pos), _ptr(out), rows, dim, top_k, tiles,
+          _s(stream))
+
+
+def moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts):
+    return int(_lib.load().ws_moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts))
+
+
+def moe_prefill(x, topk_idx, topk_w, w1, s1, w3, s3, w2, s2, y, rows, dim, inter, n_experts,
+                top_k, workspace, swiglu_limit=10.0, stream=None):
+    _call("ws_moe_prefill", _ptr(x), _ptr(topk_idx), _ptr(topk_w), _ptr(w1), _ptr(s1), _ptr(w3),
+          _ptr(s3), _ptr(w2), _ptr(s2), _ptr(y), rows, dim, inter, n_experts, top_k, swiglu_limit,
+          _ptr(workspace), workspace.numel() * workspace.element_size(), _s(stream))
