@@ -36,6 +36,15 @@ typedef struct ihipStream_t *ws_stream_t;
 #define WS_ERR_SHAPE 1002         /* shape outside what the kernels support */
 #define WS_ERR_NO_DEVICE 1003     /* no gfx950 device */
 
+/* Math modes of the GEMM-type kernels (ws_set_math_mode). EXACT (default):
+ * FP8/FP4 operands are dequantised exactly to bf16 in registers and multiplied
+ * with f32-accumulating bf16 MFMAs -- the reference's dequantise-then-f32-
+ * accumulate product, rounding aside. NATIVE: the CDNA4 FP8 / MXFP4 scaled
+ * MFMAs, faster but their internal accumulation keeps about 13 bits
+ * (relative error up to ~2^-12 of the sum of |products| per 128-K step). */
+#define WS_MATH_EXACT 0
+#define WS_MATH_NATIVE 1
+
 /* Score functions of weightstream-ref moe.rs:29-42. */
 #define WS_SCORE_SOFTMAX 0
 #define WS_SCORE_SIGMOID 1
@@ -49,6 +58,10 @@ typedef struct ihipStream_t *ws_stream_t;
 int ws_init(void);
 int ws_built_with_hip(void);
 const char *ws_error_string(int code);
+/* Process-wide math mode of every later launch (no reference counterpart:
+ * weightstream-cuda has one precision). Returns the previous mode. */
+int ws_set_math_mode(int mode);
+int ws_get_math_mode(void);
 /* Device ws_expf over the 32-bit patterns [lo, lo+n): out[i] = bits(expf(x)).
  * Test hook for the exhaustive host/device expf agreement check. */
 int ws_expf_probe(uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);

@@ -6,6 +6,8 @@
 // actquant.rs:21-57.
 #include "ws_internal.hpp"
 
+#include <atomic>
+
 namespace ws {
 
 // One thread per element; each 32-lane half of a wave is one 1x32 block.
@@ -134,6 +136,9 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const fl
     out[i] = ws_silu(g) * u * rw;
 }
 
+static std::atomic<int> g_math_mode{WS_MATH_EXACT};
+int math_mode() { return g_math_mode.load(std::memory_order_relaxed); }
+
 }  // namespace ws
 
 using namespace ws;
@@ -141,6 +146,13 @@ using namespace ws;
 extern "C" {
 
 int ws_built_with_hip(void) { return 1; }
+
+int ws_set_math_mode(int mode) {
+    if (mode != WS_MATH_EXACT && mode != WS_MATH_NATIVE) return -1;
+    return g_math_mode.exchange(mode);
+}
+
+int ws_get_math_mode(void) { return g_math_mode.load(); }
 
 const char *ws_error_string(int code) {
     switch (code) {

@@ -32,7 +32,7 @@ namespace ws {
 enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
 enum OutMode { kOutF32 = 0, kOutBf16 = 1 };
 
-template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U>
+template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT>
 __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__restrict__ A,
                                                             const void *__restrict__ SA,
                                                             const uint8_t *__restrict__ B,
@@ -61,14 +61,16 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 #pragma unroll
     for (int i = 0; i < WM; i++) {
         int row = min(m_base + i * 16 + r, M - 1);
-        arow[i] = A + (size_t)row * K + kb * 16;
+        // exact: contiguous K [32g, 32g+32); native FP8 MFMA: split halves
+        arow[i] = A + (size_t)row * K + (EXACT ? kb * 32 : kb * 16);
         if (SMODE == kUe8m0) sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
     }
 #pragma unroll
     for (int j = 0; j < WN; j++) {
         int col = min(n_base + j * 16 + r, N - 1);
         col_of[j] = col;
-        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + kb * 16 : B + (size_t)col * K + kb * 16;
+        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + kb * 16
+                       : B + (size_t)col * K + (EXACT ? kb * 32 : kb * 16);
         if (SMODE == kUe8m0)
             sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
     }
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                 for (int i = 0; i < WM; i++) {
                     const uint8_t *p = arow[i] + (size_t)ks * 128;
                     af[u][i][0] = ldg16(p);
-                    af[u][i][1] = ldg16(p + 64);
+                    af[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
                     if (SMODE == kUe8m0)
                         sav[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
                 }
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                     } else {
                         const uint8_t *p = brow[j] + (size_t)ks * 128;
                         bf[u][j][0] = ldg16_stream(p);
-                        bf[u][j][1] = ldg16_stream(p + 64);
+                        bf[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
                     }
                     if (SMODE == kUe8m0)
                         sbv[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
@@ -117,30 +119,60 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 #pragma unroll
         for (int u = 0; u < U; u++) {
             int ks = ks0 + u;
-            if (ks < k1) {
+            if (ks >= k1) continue;
+            if (EXACT) {
+                v8bf bq[WN][4];
+#pragma unroll
+                for (int j = 0; j < WN; j++) {
+                    float sbv_f = SMODE == kUe8m0 ? e8m0_to_f32(sbv[u][j] & 0xFF) : 1.0f;
+                    if (BFP4) cvt_fp4x32(bf[u][j][0], sbv_f, bq[j]);
+                    else cvt_fp8x32(bf[u][j][0], bf[u][j][1], sbv_f, bq[j]);
+                }
 #pragma unroll
                 for (int i = 0; i < WM; i++) {
-                    v8i a = frag_from(af[u][i][0], af[u][i][1]);
+                    v8bf aq[4];
+                    float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(sav[u][i] & 0xFF) : 1.0f;
+                    cvt_fp8x32(af[u][i][0], af[u][i][1], sav_f, aq);
 #pragma unroll
                     for (int j = 0; j < WN; j++) {
-                        v8i b = BFP4 ? frag_from4(bf[u][j][0]) : frag_from(bf[u][j][0], bf[u][j][1]);
                         if (SMODE == kUe8m0) {
-                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b, acc[i][j],
-                                                                             (int)sav[u][i],
-                                                                             (int)sbv[u][j])
-                                             : mfma_scaled<kFmtFp8, kFmtFp8>(a, b, acc[i][j],
-                                                                             (int)sav[u][i],
-                                                                             (int)sbv[u][j]);
+                            acc[i][j] = mfma_bf16_k128(aq, bq[j], acc[i][j]);
                         } else {
-                            v4f t = mfma_scaled<kFmtFp8, kFmtFp8>(a, b, v4f{0.f, 0.f, 0.f, 0.f},
-                                                                  kScaleOne, kScaleOne);
+                            v4f t = mfma_bf16_k128(aq, bq[j], v4f{0.f, 0.f, 0.f, 0.f});
                             float sb = sbf[(size_t)(col_of[j] / 128) * kb128 + ks];
 #pragma unroll
                             for (int v = 0; v < 4; v++) {
                                 int row = min(m_base + i * 16 + 4 * kb + v, M - 1);
-                                float s = saf[(size_t)row * kb128 + ks] * sb;
-                                acc[i][j][v] = acc[i][j][v] + t[v] * s;
+                                float sc = saf[(size_t)row * kb128 + ks] * sb;
+                                acc[i][j][v] = acc[i][j][v] + t[v] * sc;
                             }
+                        }
+                    }
+                }
+                continue;
+            }
+#pragma unroll
+            for (int i = 0; i < WM; i++) {
+                v8i a = frag_from(af[u][i][0], af[u][i][1]);
+#pragma unroll
+                for (int j = 0; j < WN; j++) {
+                    v8i b = BFP4 ? frag_from4(bf[u][j][0]) : frag_from(bf[u][j][0], bf[u][j][1]);
+                    if (SMODE == kUe8m0) {
+                        acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b, acc[i][j],
+                                                                         (int)sav[u][i],
+                                                                         (int)sbv[u][j])
+                                         : mfma_scaled<kFmtFp8, kFmtFp8>(a, b, acc[i][j],
+                                                                         (int)sav[u][i],
+                                                                         (int)sbv[u][j]);
+                    } else {
+                        v4f t = mfma_scaled<kFmtFp8, kFmtFp8>(a, b, v4f{0.f, 0.f, 0.f, 0.f},
+                                                              kScaleOne, kScaleOne);
+                        float sb = sbf[(size_t)(col_of[j] / 128) * kb128 + ks];
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            int row = min(m_base + i * 16 + 4 * kb + v, M - 1);
+                            float sc = saf[(size_t)row * kb128 + ks] * sb;
+                            acc[i][j][v] = acc[i][j][v] + t[v] * sc;
                         }
                     }
                 }
@@ -205,8 +237,12 @@ static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const 
                       int m, int n, int k, hipStream_t stream) {
     constexpr int tm = 16 * WM * GM, tn = 16 * WN;
     dim3 grid((n + tn - 1) / tn, (m + tm - 1) / tm);
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, GM, GK, BFP4, SMODE, OMODE, U>), grid,
-                       dim3(64 * GM * GK), 0, stream, a, sa, b, sb, out, m, n, k);
+    if (math_mode() == WS_MATH_NATIVE)
+        hipLaunchKernelGGL((gemm_kernel<WM, WN, GM, GK, BFP4, SMODE, OMODE, U, false>), grid,
+                           dim3(64 * GM * GK), 0, stream, a, sa, b, sb, out, m, n, k);
+    else
+        hipLaunchKernelGGL((gemm_kernel<WM, WN, GM, GK, BFP4, SMODE, OMODE, U, true>), grid,
+                           dim3(64 * GM * GK), 0, stream, a, sa, b, sb, out, m, n, k);
     return launch_status();
 }
 
@@ -224,6 +260,8 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
     if (!a || !sa || !b || !sb || !out) return WS_ERR_INVALID_ARG;
     if (m <= 0 || n <= 0 || k <= 0) return WS_ERR_INVALID_ARG;
     if (k % 128 || n % 16 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return WS_ERR_SHAPE;
+    if (((uintptr_t)a | (uintptr_t)b) & 15 || ((uintptr_t)sa | (uintptr_t)sb) & 3)
+        return WS_ERR_INVALID_ARG;
     int M = (int)m, N = (int)n, K = (int)k;
     int cfg = forced_cfg();
     if (cfg < 0) cfg = (M <= 16) ? 0 : (M <= 64 ? 1 : 2);

@@ -11,7 +11,9 @@
 // weights + UE8M0 scales once. Each wave owns 16 weight rows and walks K in
 // 128-wide steps with one 16-byte load per lane per step; the token sits in
 // LDS and feeds the MFMA's other operand (every column of the 16x16 MFMA
-// output is the same token). The hardware applies both UE8M0 scales.
+// output is the same token). Exact mode dequantises the weights to bf16 in
+// registers (v_cvt_scalef32_pk_bf16_fp4 applies the UE8M0 scale) and keeps
+// the token as exact bf16 in LDS; native mode feeds the scaled FP4 x FP8 MFMA.
 //
 //  glu_quant: grid (inter/32, top_k), 4 waves: waves 0-1 -> w1 rows, 2-3 -> w3
 //    rows of one 32-row tile; the epilogue applies SwiGLU x routing weight and
@@ -39,13 +41,17 @@ __device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_ex
     return rank;
 }
 
-// Stream a 16-row FP4 weight tile against the token in LDS: returns the 16x16
-// MFMA accumulator (all columns equal). w_rows points at row 0 of the tile,
-// s_rows at its scale row 0; row stride k/2 bytes (weights) and k/32 (scales).
+// Stream a 16-row FP4 weight tile against the token held in LDS and return the
+// 16x16 MFMA accumulator (all columns equal). w_rows / s_rows point at row 0
+// of the tile and its scale row; row strides k/2 bytes and k/32 bytes.
+// EXACT: the token is bf16 in LDS (x_lds, k values), the weights are
+// dequantised to bf16 in registers, bf16 MFMA. Native: the token is e4m3 +
+// UE8M0 in LDS (xq_lds, xs_lds) and feeds the scaled FP4 x FP8 MFMA.
+template <bool EXACT>
 __device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_rows,
                                                const uint8_t *__restrict__ s_rows,
                                                const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                               int k, int lane) {
+                                               const __bf16 *x_lds, int k, int lane) {
     const int r = lane & 15, kb = lane >> 4;
     const uint8_t *wp = w_rows + (size_t)r * (k / 2) + kb * 16;
     const uint8_t *sp = s_rows + (size_t)r * (k / 32);
@@ -65,7 +71,15 @@ __device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_row
 #pragma unroll
         for (int u = 0; u < kU; u++) {
             int ks = ks0 + u;
-            if (ks < ksteps) {
+            if (ks >= ksteps) continue;
+            if (EXACT) {
+                v8bf wq[4], xb[4];
+                cvt_fp4x32(wf[u], e8m0_to_f32(ws_[u] & 0xFF), wq);
+                const v8bf *xp = (const v8bf *)(x_lds + ks * 128 + kb * 32);
+#pragma unroll
+                for (int j = 0; j < 4; j++) xb[j] = xp[j];
+                acc = mfma_bf16_k128(wq, xb, acc);
+            } else {
                 const uint8_t *xp = xq_lds + ks * 128 + kb * 16;
                 v8i b = frag_from(*(const uint4 *)xp, *(const uint4 *)(xp + 64));
                 int sx = xs_lds[ks * 4 + kb];
@@ -76,14 +90,32 @@ __device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_row
     return acc;
 }
 
+// n e4m3 values + their UE8M0 scales (global) -> exact bf16 values in LDS.
+// n % 8 == 0; every thread converts 8 values (one 8-byte chunk of one block).
+__device__ __forceinline__ void fp8_to_bf16_lds(const uint8_t *q, const uint8_t *s, __bf16 *dst,
+                                                int n, int t, int nthreads) {
+    for (int i = t * 8; i < n; i += nthreads * 8) {
+        uint2 v = *(const uint2 *)(q + i);
+        float sc = e8m0_to_f32(s[i / 32]);
+        u32x4v o = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, sc, false),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, sc, true),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, sc, false),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, sc, true));
+        *(u32x4v *)(dst + i) = o;
+    }
+}
+
+template <bool EXACT>
 __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs, const int32_t *__restrict__ idx,
     const float *__restrict__ topk_w, const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
     uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
     extern __shared__ __align__(16) uint8_t lds[];
-    uint8_t *xq_l = lds;             // dim bytes
-    uint8_t *xs_l = lds + dim;       // dim/32 bytes
+    // EXACT: bf16 token (2*dim bytes); native: e4m3 token + scales
+    __bf16 *x_l = (__bf16 *)lds;
+    uint8_t *xq_l = lds;
+    uint8_t *xs_l = lds + dim;
     __shared__ float gu[2][32];
     const int slot = blockIdx.y;
     const int e = idx[slot];
@@ -91,8 +123,13 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const int tile = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
-    for (int i = t * 16; i < dim; i += kDecThreads * 16) *(uint4 *)(xq_l + i) = *(const uint4 *)(xq + i);
-    for (int i = t; i < dim / 32; i += kDecThreads) xs_l[i] = xs[i];
+    if (EXACT) {
+        fp8_to_bf16_lds(xq, xs, x_l, dim, t, kDecThreads);
+    } else {
+        for (int i = t * 16; i < dim; i += kDecThreads * 16)
+            *(uint4 *)(xq_l + i) = *(const uint4 *)(xq + i);
+        for (int i = t; i < dim / 32; i += kDecThreads) xs_l[i] = xs[i];
+    }
     __syncthreads();
 
     const int mat = w >> 1;
@@ -100,7 +137,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
     const uint8_t *W = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2);
     const uint8_t *S = (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32);
-    v4f acc = stream_fp4_rows(W, S, xq_l, xs_l, dim, lane);
+    v4f acc = stream_fp4_rows<EXACT>(W, S, xq_l, xs_l, x_l, dim, lane);
     // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
     if ((lane & 15) == 0) {
 #pragma unroll
@@ -127,6 +164,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     }
 }
 
+template <bool EXACT>
 __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
     const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs, const int32_t *__restrict__ idx,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
@@ -147,13 +185,19 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
         }
         n_valid = cnt;
     }
-    uint8_t *hq_l = lds;                            // top_k * inter
-    uint8_t *hs_l = lds + (size_t)top_k * inter;    // top_k * inter/32
+    // EXACT: picks as bf16 (2 * top_k * inter bytes); native: e4m3 + scales
+    __bf16 *h_l = (__bf16 *)lds;
+    uint8_t *hq_l = lds;
+    uint8_t *hs_l = lds + (size_t)top_k * inter;
     __syncthreads();
     const int nv = n_valid;
-    for (int i = t * 16; i < nv * inter; i += kDecThreads * 16)
-        *(uint4 *)(hq_l + i) = *(const uint4 *)(hq + i);
-    for (int i = t; i < nv * (inter / 32); i += kDecThreads) hs_l[i] = hs[i];
+    if (EXACT) {
+        fp8_to_bf16_lds(hq, hs, h_l, nv * inter, t, kDecThreads);
+    } else {
+        for (int i = t * 16; i < nv * inter; i += kDecThreads * 16)
+            *(uint4 *)(hq_l + i) = *(const uint4 *)(hq + i);
+        for (int i = t; i < nv * (inter / 32); i += kDecThreads) hs_l[i] = hs[i];
+    }
     __syncthreads();
 
     const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
@@ -161,8 +205,9 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
         const int e = sorted_e[p];
         const uint8_t *W = w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2);
         const uint8_t *S = s2 + (size_t)e * smat + (size_t)row0 * (inter / 32);
-        v4f acc = stream_fp4_rows(W, S, hq_l + (size_t)p * inter, hs_l + (size_t)p * (inter / 32),
-                                  inter, lane);
+        v4f acc = stream_fp4_rows<EXACT>(W, S, hq_l + (size_t)p * inter,
+                                         hs_l + (size_t)p * (inter / 32),
+                                         h_l + (size_t)p * inter, inter, lane);
         if ((lane & 15) == 0) {
 #pragma unroll
             for (int v = 0; v < 4; v++) part[p][4 * (lane >> 4) + v] = acc[v];
@@ -179,7 +224,8 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
 static int check_decode_shapes(int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || top_k > kMaxTopkDec) return WS_ERR_SHAPE;
-    if (dim > 65536 || inter > 65536 || top_k * inter > 65536 || n_experts > (1 << 20))
+    // LDS holds the token / the picks as bf16 (2 bytes per value)
+    if (dim > 32768 || inter > 32768 || top_k * inter > 32768 || n_experts > (1 << 20))
         return WS_ERR_SHAPE;
     return WS_OK;
 }
@@ -205,10 +251,16 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
         ((uintptr_t)s3 & 3))
         return WS_ERR_INVALID_ARG;
     dim3 grid((unsigned)(inter / 32), (unsigned)top_k);
-    size_t lds = (size_t)dim + dim / 32;
-    hipLaunchKernelGGL(expert_glu_quant_kernel, grid, dim3(kDecThreads), lds, stream, xq, xs,
-                       topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
-                       (int)n_experts, (int)top_k, swiglu_limit);
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
+    if (exact)
+        hipLaunchKernelGGL(expert_glu_quant_kernel<true>, grid, dim3(kDecThreads), lds, stream, xq,
+                           xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
+                           (int)n_experts, (int)top_k, swiglu_limit);
+    else
+        hipLaunchKernelGGL(expert_glu_quant_kernel<false>, grid, dim3(kDecThreads), lds, stream, xq,
+                           xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
+                           (int)n_experts, (int)top_k, swiglu_limit);
     return launch_status();
 }
 
@@ -219,10 +271,16 @@ int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_i
     int rc = check_decode_shapes(dim, inter, n_experts, top_k);
     if (rc) return rc;
     if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 3)) return WS_ERR_INVALID_ARG;
-    size_t lds = (size_t)top_k * inter + (size_t)top_k * (inter / 32);
-    hipLaunchKernelGGL(expert_reduce_kernel, dim3((unsigned)(dim / 16)), dim3(kDecThreads), lds,
-                       stream, hq, hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
-                       (int)top_k);
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    size_t lds = exact ? (size_t)top_k * inter * 2 : (size_t)top_k * inter + (size_t)top_k * (inter / 32);
+    if (exact)
+        hipLaunchKernelGGL(expert_reduce_kernel<true>, dim3((unsigned)(dim / 16)), dim3(kDecThreads),
+                           lds, stream, hq, hs, topk_idx, w2, s2, y, (int)dim, (int)inter,
+                           (int)n_experts, (int)top_k);
+    else
+        hipLaunchKernelGGL(expert_reduce_kernel<false>, dim3((unsigned)(dim / 16)),
+                           dim3(kDecThreads), lds, stream, hq, hs, topk_idx, w2, s2, y, (int)dim,
+                           (int)inter, (int)n_experts, (int)top_k);
     return launch_status();
 }
 

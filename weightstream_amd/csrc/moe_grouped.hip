@@ -132,6 +132,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
 // ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
 // grid (inter/32, tiles), 4 waves: wave (mat = w>>1, half = w&1) computes the
 // 32 slots x 16 output columns of w1 (mat 0) or w3 (mat 1).
+template <bool EXACT>
 __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
     const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs,
     const int32_t *__restrict__ order, const float *__restrict__ layout_w,
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
     for (int i = 0; i < 2; i++) {
         int route = order[slot0 + i * 16 + r];
         int tok = route >= 0 ? route / top_k : 0;
-        arow[i] = xq + (size_t)tok * dim + kb * 16;
+        arow[i] = xq + (size_t)tok * dim + (EXACT ? kb * 32 : kb * 16);
         srow[i] = xs + (size_t)tok * (dim / 32);
     }
     const int n = nt * kTile + half * 16 + r;
@@ -179,14 +180,24 @@ __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     af[u][i][0] = ldg16(arow[i] + ks * 128);
-                    af[u][i][1] = ldg16(arow[i] + ks * 128 + 64);
+                    af[u][i][1] = ldg16(arow[i] + ks * 128 + (EXACT ? 16 : 64));
                     sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
                 }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (ks0 + u < ksteps) {
+            if (ks0 + u >= ksteps) continue;
+            if (EXACT) {
+                v8bf bq[4];
+                cvt_fp4x32(bf[u], e8m0_to_f32(sb[u] & 0xFF), bq);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    v8bf aq[4];
+                    cvt_fp8x32(af[u][i][0], af[u][i][1], e8m0_to_f32(sa[u][i] & 0xFF), aq);
+                    acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
+                }
+            } else {
                 v8i b = frag_from4(bf[u]);
 #pragma unroll
                 for (int i = 0; i < 2; i++)
@@ -222,6 +233,7 @@ __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
 // ---- grouped down ---------------------------------------------------------
 // grid (dim/64, tiles), 4 waves: wave w computes 32 slots x 16 output columns
 // (columns nt*64 + w*16 ..) of the expert's w2; f32 out[slot, dim].
+template <bool EXACT>
 __global__ __launch_bounds__(256) void grouped_down_kernel(
     const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs,
     const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ num_tiles,
@@ -242,7 +254,7 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
     const uint8_t *srow[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        arow[i] = hq + (size_t)(slot0 + i * 16 + r) * inter + kb * 16;
+        arow[i] = hq + (size_t)(slot0 + i * 16 + r) * inter + (EXACT ? kb * 32 : kb * 16);
         srow[i] = hs + (size_t)(slot0 + i * 16 + r) * (inter / 32);
     }
     v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
@@ -260,14 +272,24 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     af[u][i][0] = ldg16(arow[i] + ks * 128);
-                    af[u][i][1] = ldg16(arow[i] + ks * 128 + 64);
+                    af[u][i][1] = ldg16(arow[i] + ks * 128 + (EXACT ? 16 : 64));
                     sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
                 }
             }
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (ks0 + u < ksteps) {
+            if (ks0 + u >= ksteps) continue;
+            if (EXACT) {
+                v8bf bq[4];
+                cvt_fp4x32(bf[u], e8m0_to_f32(sb[u] & 0xFF), bq);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    v8bf aq[4];
+                    cvt_fp8x32(af[u][i][0], af[u][i][1], e8m0_to_f32(sa[u][i] & 0xFF), aq);
+                    acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
+                }
+            } else {
                 v8i b = frag_from4(bf[u]);
 #pragma unroll
                 for (int i = 0; i < 2; i++)
@@ -359,10 +381,15 @@ int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t
         return WS_ERR_SHAPE;
     if (!al16(xq) || !al16(w1) || !al16(w3) || !al4(xs) || !al4(s1) || !al4(s3))
         return WS_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(grouped_glu_quant_kernel, dim3((unsigned)(inter / 32), (unsigned)tiles),
-                       dim3(256), 0, stream, xq, xs, order, layout_w, tile_expert, num_tiles, w1,
-                       s1, w3, s3, hq, hs, (int)dim, (int)inter, (int)n_experts, (int)top_k,
-                       swiglu_limit);
+    dim3 grid((unsigned)(inter / 32), (unsigned)tiles);
+    if (math_mode() == WS_MATH_EXACT)
+        hipLaunchKernelGGL(grouped_glu_quant_kernel<true>, grid, dim3(256), 0, stream, xq, xs, order,
+                           layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs, (int)dim,
+                           (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
+    else
+        hipLaunchKernelGGL(grouped_glu_quant_kernel<false>, grid, dim3(256), 0, stream, xq, xs,
+                           order, layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs,
+                           (int)dim, (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
     return launch_status();
 }
 
@@ -374,9 +401,15 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || tiles > 65535) return WS_ERR_SHAPE;
     if (!al16(hq) || !al16(w2) || !al4(hs) || !al4(s2)) return WS_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(grouped_down_kernel, dim3((unsigned)(dim / 64), (unsigned)tiles), dim3(256),
-                       0, stream, hq, hs, tile_expert, num_tiles, w2, s2, out, (int)dim,
-                       (int)inter, (int)n_experts);
+    dim3 grid((unsigned)(dim / 64), (unsigned)tiles);
+    if (math_mode() == WS_MATH_EXACT)
+        hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(256), 0, stream, hq, hs,
+                           tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
+                           (int)n_experts);
+    else
+        hipLaunchKernelGGL(grouped_down_kernel<false>, grid, dim3(256), 0, stream, hq, hs,
+                           tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
+                           (int)n_experts);
     return launch_status();
 }
 

@@ -12,6 +12,9 @@ namespace ws {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
@@ -139,6 +142,55 @@ __device__ __forceinline__ v8i frag_from4(uint4 lo) {
     r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
     r[4] = 0; r[5] = 0; r[6] = 0; r[7] = 0;
     return r;
+}
+
+// ---- exact math: dequantise to bf16, accumulate with bf16 MFMA -----------
+// The FP8/FP4 scaled MFMAs of gfx950 sum their products at reduced internal
+// precision (measured: up to 2^-12 of sum|p| per instruction, against 2^-24
+// for an f32 sum), while v_mfma_f32_16x16x32_bf16 accumulates in f32
+// (measured: 2e-7 of sum|p|). Every e4m3 / e2m1 value times a UE8M0 scale is
+// exactly representable in bf16 (4 and 2 significant bits, f32 exponent
+// range), so converting with v_cvt_scalef32_pk_bf16_{fp8,fp4} and running bf16
+// MFMAs computes the reference's dequantise-then-f32-accumulate product.
+// A lane's 32 K-values [32g, 32g+32) of one 128-K step feed 4 MFMAs of K=32,
+// 8 values each; operand A and B use the same assignment, so the dot product
+// covers every K exactly once.
+
+__device__ __forceinline__ u32x4v pk4(v2bf a, v2bf b, v2bf c, v2bf d) {
+    return u32x4v{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                  __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d)};
+}
+
+// 32 e4m3 bytes (K 0-15 in lo, 16-31 in hi) * scale -> 4 x 8 bf16
+__device__ __forceinline__ void cvt_fp8x32(uint4 lo, uint4 hi, float s, v8bf out[4]) {
+    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        u32x4v v = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], s, false),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j], s, true),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], s, false),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[2 * j + 1], s, true));
+        out[j] = __builtin_bit_cast(v8bf, v);
+    }
+}
+
+// 16 packed e2m1 bytes (32 values, low nibble first) * scale -> 4 x 8 bf16
+__device__ __forceinline__ void cvt_fp4x32(uint4 q, float s, v8bf out[4]) {
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        u32x4v v = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], s, 0),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], s, 1),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], s, 2),
+                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[j], s, 3));
+        out[j] = __builtin_bit_cast(v8bf, v);
+    }
+}
+
+__device__ __forceinline__ v4f mfma_bf16_k128(const v8bf a[4], const v8bf b[4], v4f c) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[j], b[j], c, 0, 0, 0);
+    return c;
 }
 
 }  // namespace ws

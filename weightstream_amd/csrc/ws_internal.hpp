@@ -17,4 +17,7 @@ inline int launch_status() {
     return e == hipSuccess ? WS_OK : (int)e;
 }
 
+// Math mode chosen by ws_set_math_mode (WS_MATH_EXACT by default).
+int math_mode();
+
 }  // namespace ws

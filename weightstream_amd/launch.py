@@ -42,6 +42,35 @@ def built_with_hip():
     return bool(_lib.load().ws_built_with_hip())
 
 
+MATH_EXACT, MATH_NATIVE = 0, 1
+
+
+def set_math_mode(mode):
+    """WS_MATH_EXACT (bf16 MFMA on exactly dequantised operands, default) or
+    WS_MATH_NATIVE (FP8/MXFP4 scaled MFMA). Returns the previous mode."""
+    prev = _lib.load().ws_set_math_mode(int(mode))
+    if prev < 0:
+        raise ValueError("unknown math mode %r" % (mode,))
+    return prev
+
+
+def get_math_mode():
+    return _lib.load().ws_get_math_mode()
+
+
+class math_mode:
+    """Context manager: `with math_mode(MATH_NATIVE): ...`."""
+
+    def __init__(self, mode):
+        self.mode = mode
+
+    def __enter__(self):
+        self.prev = set_math_mode(self.mode)
+
+    def __exit__(self, *exc):
+        set_math_mode(self.prev)
+
+
 def _ptr(t):
     if t is None:
         return None
