@@ -123,8 +123,13 @@ def test_fp8_gemm_matches_oracle(m, n, k):
     ob = torch.empty((m, n), dtype=torch.int16, device=DEV)
     L.fp8_gemm_bf16(dev(aq), dev(as_), dev(wq), dev(ws), ob, m, n, k)
     got = (host(ob).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
-    # bf16 keeps 8 significant bits: RNE error <= 2^-9 relative
-    assert_close(got, want, 2.0 ** -9 + GEMM_TOL, "fp8_gemm_bf16 %dx%dx%d" % (m, n, k))
+    # bf16 keeps 8 significant bits: RNE error <= 2^-8 relative; and the
+    # output equals the oracle's f32 rounded to bf16 except where the two f32
+    # values straddle a rounding boundary
+    assert_close(got, want, 2.0 ** -8 + GEMM_TOL, "fp8_gemm_bf16 %dx%dx%d" % (m, n, k))
+    want_b = np.array([O.f32_to_bf16(float(v)) for v in want.ravel()], np.uint16)
+    same = np.mean(host(ob).astype(np.uint16).ravel() == want_b)
+    assert same >= 0.999, same
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (8, 512, 1024), (128, 256, 2048),

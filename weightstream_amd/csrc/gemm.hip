@@ -247,11 +247,8 @@ static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const 
 }
 
 static int forced_cfg() {
-    static int cfg = [] {
-        const char *e = getenv("WS_GEMM_CFG");
-        return e ? atoi(e) : -1;
-    }();
-    return cfg;
+    const char *e = getenv("WS_GEMM_CFG");
+    return e ? atoi(e) : -1;
 }
 
 template <bool BFP4, int SMODE, int OMODE>
@@ -264,7 +261,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         return WS_ERR_INVALID_ARG;
     int M = (int)m, N = (int)n, K = (int)k;
     int cfg = forced_cfg();
-    if (cfg < 0) cfg = (M <= 16) ? 0 : (M <= 64 ? 1 : 2);
+    if (cfg < 0) cfg = (M <= 16) ? 5 : (M <= 64 ? 10 : 8);
     switch (cfg) {
         case 0:  // decode: 16 x 16 tile, K split over 4 waves
             return launch_cfg<1, 1, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
@@ -280,6 +277,18 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
             return launch_cfg<1, 1, 1, 8, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
         case 6:  // 16 x 32 tile, K split over 4
             return launch_cfg<1, 2, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 7:  // 16 x 16 tile, K split over 16 waves
+            return launch_cfg<1, 1, 1, 16, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        case 8:  // 128 x 16 tile, K split over 4 (16 waves)
+            return launch_cfg<2, 1, 4, 4, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        case 9:  // 128 x 32 tile, K split over 4 (16 waves)
+            return launch_cfg<2, 2, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+        case 11:  // 128 x 16 tile, K split over 2 (8 waves)
+            return launch_cfg<2, 1, 4, 2, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+        case 12:  // 128 x 32 tile, K split over 2 (8 waves)
+            return launch_cfg<2, 2, 4, 2, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        case 10:  // 64 x 16 tile, K split over 4 (16 waves)
+            return launch_cfg<1, 1, 4, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
         default:
             return WS_ERR_INVALID_ARG;
     }

@@ -15,17 +15,21 @@
 // registers (v_cvt_scalef32_pk_bf16_fp4 applies the UE8M0 scale) and keeps
 // the token as exact bf16 in LDS; native mode feeds the scaled FP4 x FP8 MFMA.
 //
-//  glu_quant: grid (inter/32, top_k), 4 waves: waves 0-1 -> w1 rows, 2-3 -> w3
-//    rows of one 32-row tile; the epilogue applies SwiGLU x routing weight and
-//    quantises the 32 values (one FP8 1x32 block) straight to e4m3 + UE8M0.
-//  reduce: grid (dim/16), 4 waves: each wave runs whole experts for 16 output
+//  glu_quant: grid (inter/32, top_k), 16 waves: a wave streams 16 rows of w1 or
+//    w3 of the 32-row tile over a quarter of K (8 KB at the BASELINE shape, all
+//    loads in flight at once); the quarters are added in LDS in fixed order,
+//    then the epilogue applies SwiGLU x routing weight and quantises the 32
+//    values (one FP8 1x32 block) straight to e4m3 + UE8M0.
+//  reduce: grid (dim/16), 16 waves over (expert, K part) units for 16 output
 //    rows; per-expert results meet in LDS and are added in ascending expert id,
 //    one f32 add per expert like the reference's acc_f32 chain.
 #include "ws_internal.hpp"
 
 namespace ws {
 
-constexpr int kDecThreads = 256;
+constexpr int kDecThreads = 1024;  // 16 waves: K is split across waves
+constexpr int kGluKSplit = 4;      // glu: 4 (matrix, half) units x 4 K parts
+constexpr int kRedKSplitMax = 16;
 constexpr int kMaxTopkDec = 16;
 constexpr int kU = 8;  // K steps in flight per wave
 
@@ -51,13 +55,13 @@ template <bool EXACT>
 __device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_rows,
                                                const uint8_t *__restrict__ s_rows,
                                                const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                               const __bf16 *x_lds, int k, int lane) {
+                                               const __bf16 *x_lds, int k, int kstep0,
+                                               int ksteps, int lane) {
     const int r = lane & 15, kb = lane >> 4;
     const uint8_t *wp = w_rows + (size_t)r * (k / 2) + kb * 16;
     const uint8_t *sp = s_rows + (size_t)r * (k / 32);
-    const int ksteps = k / 128;
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ks0 = 0; ks0 < ksteps; ks0 += kU) {
+    for (int ks0 = kstep0; ks0 < ksteps; ks0 += kU) {
         uint4 wf[kU];
         uint32_t ws_[kU];
 #pragma unroll
@@ -116,7 +120,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     __bf16 *x_l = (__bf16 *)lds;
     uint8_t *xq_l = lds;
     uint8_t *xs_l = lds + dim;
-    __shared__ float gu[2][32];
+    __shared__ float part[kGluKSplit][2][32];
     const int slot = blockIdx.y;
     const int e = idx[slot];
     if (e < 0 || e >= n_experts) return;  // whole workgroup
@@ -132,23 +136,32 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     }
     __syncthreads();
 
-    const int mat = w >> 1;
-    const int row0 = tile * 32 + (w & 1) * 16;
+    // wave -> (matrix, 16-row half of the tile, K quarter)
+    const int unit = w & 3, ksp = w >> 2;
+    const int mat = unit >> 1, half = unit & 1;
+    const int ksteps = dim / 128;
+    const int k0 = ksp * ksteps / kGluKSplit, k1 = (ksp + 1) * ksteps / kGluKSplit;
+    const int row0 = tile * 32 + half * 16;
     const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
     const uint8_t *W = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2);
     const uint8_t *S = (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32);
-    v4f acc = stream_fp4_rows<EXACT>(W, S, xq_l, xs_l, x_l, dim, lane);
+    v4f acc = stream_fp4_rows<EXACT>(W, S, xq_l, xs_l, x_l, dim, k0, k1, lane);
     // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
     if ((lane & 15) == 0) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) gu[mat][(w & 1) * 16 + 4 * (lane >> 4) + v] = acc[v];
+        for (int v = 0; v < 4; v++) part[ksp][mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
     }
     __syncthreads();
     if (w != 0) return;
     // lanes 0-31 own the tile's 32 values; lanes 32-63 mirror them so the
     // half-wave reduction stays uniform, and do not store
     const int n = lane & 31;
-    float g = gu[0][n], u = gu[1][n];
+    float g = part[0][0][n], u = part[0][1][n];
+#pragma unroll
+    for (int q = 1; q < kGluKSplit; q++) {
+        g = g + part[q][0][n];
+        u = u + part[q][1][n];
+    }
     if (limit > 0.0f) {
         u = rclamp(u, -limit, limit);
         g = fminf(g, limit);
@@ -172,7 +185,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int32_t sorted_e[kMaxTopkDec];
     __shared__ int32_t n_valid;
-    __shared__ float part[kMaxTopkDec][16];
+    __shared__ float part[kMaxTopkDec][kRedKSplitMax][16];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int row0 = blockIdx.x * 16;
     if (t == 0) {
@@ -200,23 +213,36 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
     }
     __syncthreads();
 
+    // work units (pick, K part): every wave streams 16 rows of one expert's
+    // w2 over 1/ksplit of inter
+    const int ksteps = inter / 128;
+    int ksplit = (kDecThreads / 64) / (nv > 0 ? nv : 1);
+    ksplit = ksplit < 1 ? 1 : (ksplit > kRedKSplitMax ? kRedKSplitMax : ksplit);
+    if (ksplit > ksteps) ksplit = ksteps;
     const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
-    for (int p = w; p < nv; p += kDecThreads / 64) {
+    for (int unit = w; unit < nv * ksplit; unit += kDecThreads / 64) {
+        const int p = unit / ksplit, ksp = unit % ksplit;
         const int e = sorted_e[p];
         const uint8_t *W = w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2);
         const uint8_t *S = s2 + (size_t)e * smat + (size_t)row0 * (inter / 32);
         v4f acc = stream_fp4_rows<EXACT>(W, S, hq_l + (size_t)p * inter,
                                          hs_l + (size_t)p * (inter / 32),
-                                         h_l + (size_t)p * inter, inter, lane);
+                                         h_l + (size_t)p * inter, inter, ksp * ksteps / ksplit,
+                                         (ksp + 1) * ksteps / ksplit, lane);
         if ((lane & 15) == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) part[p][4 * (lane >> 4) + v] = acc[v];
+            for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
         }
     }
     __syncthreads();
     if (t < 16) {
+        // one f32 add per expert, ascending expert id (moe.rs:76-84)
         float acc = 0.0f;
-        for (int p = 0; p < nv; p++) acc = acc + part[p][t];
+        for (int p = 0; p < nv; p++) {
+            float pe = part[p][0][t];
+            for (int q = 1; q < ksplit; q++) pe = pe + part[p][q][t];
+            acc = acc + pe;
+        }
         y[row0 + t] = acc;
     }
 }
