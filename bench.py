@@ -134,8 +134,8 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
         ms.sort()
         return sum(ms) / len(ms), ms[len(ms) // 2]
 
-    glu = lambda t: L.expert_glu_quant(xq[t], xs[t], idx[t], wts[t], w1, s1, w3, s3, hq[t], hs[t],
-                                       INTER, DIM, E, TOPK, stream=s)
+    glu = lambda t: L.expert_glu_quant_x(x[t], idx[t], wts[t], w1, s1, w3, s3, hq[t], hs[t],
+                                         INTER, DIM, E, TOPK, stream=s)
     red = lambda t: L.expert_reduce(hq[t], hs[t], w2, s2, idx[t], y[t], DIM, INTER, E, TOPK,
                                     stream=s)
     for t in range(n_tokens):
@@ -143,7 +143,7 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
     reps_k = max(200, n_tokens)
     glu_avg, glu_med = timed(glu, reps_k)
     red_avg, red_med = timed(red, reps_k)
-    glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + DIM + DIM // 32 + TOPK * (INTER + INTER // 32)
+    glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + 4 * DIM + TOPK * (INTER + INTER // 32)
     red_bytes = TOPK * (FP4_MAT + FP4_SC) + TOPK * (INTER + INTER // 32) + DIM * 4
     kern = {
         "expert_glu_quant_kernel": {"avg_us": glu_avg * 1e3, "median_us": glu_med * 1e3,

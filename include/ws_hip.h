@@ -182,12 +182,20 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
                         const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
                         int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
                         float swiglu_limit, ws_stream_t stream);
+/* As ws_expert_glu_quant with the activation quantisation (act_quant_fp8_emit,
+ * actquant.cu:47) fused in: x is the f32 token [dim]. */
+int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *topk_w,
+                          const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
+                          const uint8_t *s3, uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter,
+                          int64_t n_experts, int64_t top_k, float swiglu_limit,
+                          ws_stream_t stream);
 /* expert_reduce (moe_grouped.cu:165, launch.rs:178-206): y[dim] = sum over
  * picks in ascending expert id of w2_e . h_e, one f32 add per expert. */
 int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
                      const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
                      int64_t inter, int64_t n_experts, int64_t top_k, ws_stream_t stream);
-/* Whole routed MoE for one token from f32 x: emit8(x) -> glu_quant -> reduce.
+/* Whole routed MoE for one token from f32 x: glu_quant_x -> reduce (two
+ * kernels; hq/hs of the picks live in the workspace).
  * workspace >= ws_moe_decode_workspace_size(dim, inter, top_k) bytes. */
 size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k);
 int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,

@@ -52,5 +52,5 @@ def test_argument_validation_without_device(lib):
 
 def test_workspace_sizes(lib):
     n = lib.ws_moe_decode_workspace_size(4096, 2048, 8)
-    assert n >= 4096 + 128 + 8 * 2048 + 8 * 64
+    assert n >= 8 * 2048 + 8 * 64
     assert n % 256 == 0

@@ -106,6 +106,11 @@ def test_moe_decode_split_entry_points_and_order():
     y3 = torch.empty(dim, dtype=torch.float32, device=DEV)
     L.expert_reduce(hq, hs, w2, s2, dev(ids), y3, dim, inter, E, k)
     assert np.array_equal(host(y1).view(np.uint32), host(y3).view(np.uint32))
+    # the fused-quantisation variant writes the same bytes
+    hq2 = torch.empty_like(hq)
+    hs2 = torch.empty_like(hs)
+    L.expert_glu_quant_x(dev(x), dev(ids), dev(wts), w1, s1, w3, s3, hq2, hs2, inter, dim, E, k)
+    assert torch.equal(hq, hq2) and torch.equal(hs, hs2)
     # row r of hq is the r-th smallest expert id's hidden state
     H = _host_experts(slabs, ids, E, dim, inter)
     order = np.argsort(ids)

@@ -32,6 +32,14 @@ namespace ws {
 enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
 enum OutMode { kOutF32 = 0, kOutBf16 = 1 };
 
+// Operand registers of U consecutive 128-K steps of one wave.
+template <int WM, int WN, int U>
+struct GemmStage {
+    uint4 a[U][WM][2];
+    uint4 b[U][WN][2];
+    uint32_t sa[U][WM], sb[U][WN];
+};
+
 template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT>
 __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__restrict__ A,
                                                             const void *__restrict__ SA,
@@ -86,10 +94,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
     const float *saf = (const float *)SA;
     const float *sbf = (const float *)SB;
 
-    for (int ks0 = k0; ks0 < k1; ks0 += U) {
-        uint4 af[U][WM][2];
-        uint4 bf[U][WN][2];
-        uint32_t sav[U][WM], sbv[U][WN];
+    auto load = [&](GemmStage<WM, WN, U> &st, int ks0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             int ks = ks0 + u;
@@ -97,25 +102,28 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 #pragma unroll
                 for (int i = 0; i < WM; i++) {
                     const uint8_t *p = arow[i] + (size_t)ks * 128;
-                    af[u][i][0] = ldg16(p);
-                    af[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
+                    st.a[u][i][0] = ldg16(p);
+                    st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
                     if (SMODE == kUe8m0)
-                        sav[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
+                        st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
                 }
 #pragma unroll
                 for (int j = 0; j < WN; j++) {
                     if (BFP4) {
-                        bf[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                        st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
                     } else {
                         const uint8_t *p = brow[j] + (size_t)ks * 128;
-                        bf[u][j][0] = ldg16_stream(p);
-                        bf[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+                        st.b[u][j][0] = ldg16_stream(p);
+                        st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
                     }
                     if (SMODE == kUe8m0)
-                        sbv[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
+                        st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
                 }
             }
         }
+    };
+
+    auto compute = [&](const GemmStage<WM, WN, U> &st, int ks0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             int ks = ks0 + u;
@@ -124,15 +132,15 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                 v8bf bq[WN][4];
 #pragma unroll
                 for (int j = 0; j < WN; j++) {
-                    float sbv_f = SMODE == kUe8m0 ? e8m0_to_f32(sbv[u][j] & 0xFF) : 1.0f;
-                    if (BFP4) cvt_fp4x32(bf[u][j][0], sbv_f, bq[j]);
-                    else cvt_fp8x32(bf[u][j][0], bf[u][j][1], sbv_f, bq[j]);
+                    float sbv_f = SMODE == kUe8m0 ? e8m0_to_f32(st.sb[u][j] & 0xFF) : 1.0f;
+                    if (BFP4) cvt_fp4x32(st.b[u][j][0], sbv_f, bq[j]);
+                    else cvt_fp8x32(st.b[u][j][0], st.b[u][j][1], sbv_f, bq[j]);
                 }
 #pragma unroll
                 for (int i = 0; i < WM; i++) {
                     v8bf aq[4];
-                    float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(sav[u][i] & 0xFF) : 1.0f;
-                    cvt_fp8x32(af[u][i][0], af[u][i][1], sav_f, aq);
+                    float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(st.sa[u][i] & 0xFF) : 1.0f;
+                    cvt_fp8x32(st.a[u][i][0], st.a[u][i][1], sav_f, aq);
 #pragma unroll
                     for (int j = 0; j < WN; j++) {
                         if (SMODE == kUe8m0) {
@@ -149,35 +157,48 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
                         }
                     }
                 }
-                continue;
-            }
+            } else {
 #pragma unroll
-            for (int i = 0; i < WM; i++) {
-                v8i a = frag_from(af[u][i][0], af[u][i][1]);
+                for (int i = 0; i < WM; i++) {
+                    v8i a = frag_from(st.a[u][i][0], st.a[u][i][1]);
 #pragma unroll
-                for (int j = 0; j < WN; j++) {
-                    v8i b = BFP4 ? frag_from4(bf[u][j][0]) : frag_from(bf[u][j][0], bf[u][j][1]);
-                    if (SMODE == kUe8m0) {
-                        acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b, acc[i][j],
-                                                                         (int)sav[u][i],
-                                                                         (int)sbv[u][j])
-                                         : mfma_scaled<kFmtFp8, kFmtFp8>(a, b, acc[i][j],
-                                                                         (int)sav[u][i],
-                                                                         (int)sbv[u][j]);
-                    } else {
-                        v4f t = mfma_scaled<kFmtFp8, kFmtFp8>(a, b, v4f{0.f, 0.f, 0.f, 0.f},
-                                                              kScaleOne, kScaleOne);
-                        float sb = sbf[(size_t)(col_of[j] / 128) * kb128 + ks];
+                    for (int j = 0; j < WN; j++) {
+                        v8i b = BFP4 ? frag_from4(st.b[u][j][0])
+                                     : frag_from(st.b[u][j][0], st.b[u][j][1]);
+                        if (SMODE == kUe8m0) {
+                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(
+                                                   a, b, acc[i][j], (int)st.sa[u][i],
+                                                   (int)st.sb[u][j])
+                                             : mfma_scaled<kFmtFp8, kFmtFp8>(
+                                                   a, b, acc[i][j], (int)st.sa[u][i],
+                                                   (int)st.sb[u][j]);
+                        } else {
+                            v4f t = mfma_scaled<kFmtFp8, kFmtFp8>(
+                                a, b, v4f{0.f, 0.f, 0.f, 0.f}, kScaleOne, kScaleOne);
+                            float sb = sbf[(size_t)(col_of[j] / 128) * kb128 + ks];
 #pragma unroll
-                        for (int v = 0; v < 4; v++) {
-                            int row = min(m_base + i * 16 + 4 * kb + v, M - 1);
-                            float sc = saf[(size_t)row * kb128 + ks] * sb;
-                            acc[i][j][v] = acc[i][j][v] + t[v] * sc;
+                            for (int v = 0; v < 4; v++) {
+                                int row = min(m_base + i * 16 + 4 * kb + v, M - 1);
+                                float sc = saf[(size_t)row * kb128 + ks] * sb;
+                                acc[i][j][v] = acc[i][j][v] + t[v] * sc;
+                            }
                         }
                     }
                 }
             }
         }
+    };
+
+    // two register stages: the loads of stage n+1 are in flight while stage n
+    // is converted and multiplied, so a wave waits on memory once, not once per
+    // batch of U steps
+    GemmStage<WM, WN, U> s0, s1;
+    load(s0, k0);
+    for (int ks0 = k0; ks0 < k1; ks0 += 2 * U) {
+        if (ks0 + U < k1) load(s1, ks0 + U);
+        compute(s0, ks0);
+        if (ks0 + 2 * U < k1) load(s0, ks0 + 2 * U);
+        if (ks0 + U < k1) compute(s1, ks0 + U);
     }
 
     if (GK > 1) {
@@ -268,7 +289,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         case 1:  // 64 x 16 tile
             return launch_cfg<1, 1, 4, 1, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
         case 2:  // 128 x 16 tile
-            return launch_cfg<2, 1, 4, 1, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<2, 1, 4, 1, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         case 3:  // 128 x 32 tile
             return launch_cfg<2, 2, 4, 1, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         case 4:  // 64 x 16 tile, K split over 2
@@ -276,19 +297,17 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         case 5:  // 16 x 16 tile, K split over 8 waves
             return launch_cfg<1, 1, 1, 8, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
         case 6:  // 16 x 32 tile, K split over 4
-            return launch_cfg<1, 2, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<1, 2, 1, 4, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         case 7:  // 16 x 16 tile, K split over 16 waves
-            return launch_cfg<1, 1, 1, 16, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<1, 1, 1, 16, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         case 8:  // 128 x 16 tile, K split over 4 (16 waves)
-            return launch_cfg<2, 1, 4, 4, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
-        case 9:  // 128 x 32 tile, K split over 4 (16 waves)
-            return launch_cfg<2, 2, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<2, 1, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         case 11:  // 128 x 16 tile, K split over 2 (8 waves)
-            return launch_cfg<2, 1, 4, 2, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<2, 1, 4, 2, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         case 12:  // 128 x 32 tile, K split over 2 (8 waves)
-            return launch_cfg<2, 2, 4, 2, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<2, 2, 4, 2, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         case 10:  // 64 x 16 tile, K split over 4 (16 waves)
-            return launch_cfg<1, 1, 4, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
+            return launch_cfg<1, 1, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         default:
             return WS_ERR_INVALID_ARG;
     }

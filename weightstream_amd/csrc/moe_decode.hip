@@ -27,11 +27,11 @@
 
 namespace ws {
 
-constexpr int kDecThreads = 1024;  // 16 waves: K is split across waves
-constexpr int kGluKSplit = 4;      // glu: 4 (matrix, half) units x 4 K parts
-constexpr int kRedKSplitMax = 16;
+constexpr int kDecThreads = 256;   // glu: 4 waves = (w1|w3) x (rows 0-15|16-31)
+constexpr int kRedWaves = 8;       // reduce: 8 waves over (expert, K part) units
+constexpr int kRedThreads = 64 * kRedWaves;
 constexpr int kMaxTopkDec = 16;
-constexpr int kU = 8;  // K steps in flight per wave
+constexpr int kU = 8;  // 128-K steps per register stage (two stages in flight)
 
 // rank of pick `slot` among valid picks ordered by (expert id, slot)
 __device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_experts, int slot) {
@@ -45,51 +45,94 @@ __device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_ex
     return rank;
 }
 
+// expert id of the pick with rank p (ascending expert id, then slot)
+__device__ __forceinline__ int expert_of_rank(const int32_t *idx, int top_k, int n_experts, int p) {
+    for (int sidx = 0; sidx < top_k; sidx++) {
+        int e = idx[sidx];
+        if (e >= 0 && e < n_experts && pick_rank(idx, top_k, n_experts, sidx) == p) return e;
+    }
+    return 0;
+}
+
 // Stream a 16-row FP4 weight tile against the token held in LDS and return the
 // 16x16 MFMA accumulator (all columns equal). w_rows / s_rows point at row 0
-// of the tile and its scale row; row strides k/2 bytes and k/32 bytes.
-// EXACT: the token is bf16 in LDS (x_lds, k values), the weights are
-// dequantised to bf16 in registers, bf16 MFMA. Native: the token is e4m3 +
-// UE8M0 in LDS (xq_lds, xs_lds) and feeds the scaled FP4 x FP8 MFMA.
+// of the tile and its scale row; row strides k/2 bytes and k/32 bytes; the
+// 128-K steps [kstep0, kstep1) are streamed.
+// EXACT: the token is bf16 in LDS (x_lds), the weights are dequantised to
+// bf16 in registers, bf16 MFMA. Native: the token is e4m3 + UE8M0 in LDS
+// (xq_lds, xs_lds) and feeds the scaled FP4 x FP8 MFMA.
+// Loads run in two register stages of kU steps: stage n+1 is in flight while
+// stage n is multiplied, and the caller may issue the first stage (`first`)
+// before it prepares the token in LDS, hiding that work behind the loads.
+struct Fp4Stage {
+    uint4 w[kU];
+    uint32_t s[kU];
+};
+
+__device__ __forceinline__ void fp4_load_stage(Fp4Stage &st, const uint8_t *wp, const uint8_t *sp,
+                                               int kb, int ks0, int kstep1) {
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        int ks = ks0 + u;
+        if (ks < kstep1) {
+            st.w[u] = ldg16_stream(wp + (size_t)ks * 64);
+            st.s[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+        }
+    }
+}
+
 template <bool EXACT>
-__device__ __forceinline__ v4f stream_fp4_rows(const uint8_t *__restrict__ w_rows,
-                                               const uint8_t *__restrict__ s_rows,
-                                               const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                               const __bf16 *x_lds, int k, int kstep0,
-                                               int ksteps, int lane) {
+__device__ __forceinline__ v4f fp4_compute_stage(const Fp4Stage &st, v4f acc,
+                                                 const uint8_t *xq_lds, const uint8_t *xs_lds,
+                                                 const __bf16 *x_lds, int kb, int ks0,
+                                                 int kstep1) {
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        int ks = ks0 + u;
+        if (ks >= kstep1) continue;
+        if (EXACT) {
+            v8bf wq[4], xb[4];
+            cvt_fp4x32(st.w[u], e8m0_to_f32(st.s[u] & 0xFF), wq);
+            const v8bf *xp = (const v8bf *)(x_lds + ks * 128 + kb * 32);
+#pragma unroll
+            for (int j = 0; j < 4; j++) xb[j] = xp[j];
+            acc = mfma_bf16_k128(wq, xb, acc);
+        } else {
+            const uint8_t *xp = xq_lds + ks * 128 + kb * 16;
+            v8i b = frag_from(*(const uint4 *)xp, *(const uint4 *)(xp + 64));
+            int sx = xs_lds[ks * 4 + kb];
+            acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(st.w[u]), b, acc, (int)st.s[u], sx);
+        }
+    }
+    return acc;
+}
+
+struct Fp4Rows {
+    const uint8_t *wp, *sp;
+    int kb;
+};
+
+__device__ __forceinline__ Fp4Rows fp4_rows(const uint8_t *w_rows, const uint8_t *s_rows, int k,
+                                            int lane) {
     const int r = lane & 15, kb = lane >> 4;
-    const uint8_t *wp = w_rows + (size_t)r * (k / 2) + kb * 16;
-    const uint8_t *sp = s_rows + (size_t)r * (k / 32);
+    return Fp4Rows{w_rows + (size_t)r * (k / 2) + kb * 16, s_rows + (size_t)r * (k / 32), kb};
+}
+
+// Continue streaming after the caller loaded `first` = steps [kstep0, kstep0+kU).
+template <bool EXACT>
+__device__ __forceinline__ v4f stream_fp4_rows(const Fp4Rows &rows, Fp4Stage &first,
+                                               const uint8_t *xq_lds, const uint8_t *xs_lds,
+                                               const __bf16 *x_lds, int kstep0, int kstep1) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ks0 = kstep0; ks0 < ksteps; ks0 += kU) {
-        uint4 wf[kU];
-        uint32_t ws_[kU];
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            int ks = ks0 + u;
-            if (ks < ksteps) {
-                wf[u] = ldg16_stream(wp + (size_t)ks * 64);
-                ws_[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kU; u++) {
-            int ks = ks0 + u;
-            if (ks >= ksteps) continue;
-            if (EXACT) {
-                v8bf wq[4], xb[4];
-                cvt_fp4x32(wf[u], e8m0_to_f32(ws_[u] & 0xFF), wq);
-                const v8bf *xp = (const v8bf *)(x_lds + ks * 128 + kb * 32);
-#pragma unroll
-                for (int j = 0; j < 4; j++) xb[j] = xp[j];
-                acc = mfma_bf16_k128(wq, xb, acc);
-            } else {
-                const uint8_t *xp = xq_lds + ks * 128 + kb * 16;
-                v8i b = frag_from(*(const uint4 *)xp, *(const uint4 *)(xp + 64));
-                int sx = xs_lds[ks * 4 + kb];
-                acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(wf[u]), b, acc, (int)ws_[u], sx);
-            }
-        }
+    Fp4Stage other;
+    for (int ks0 = kstep0; ks0 < kstep1; ks0 += 2 * kU) {
+        if (ks0 + kU < kstep1) fp4_load_stage(other, rows.wp, rows.sp, rows.kb, ks0 + kU, kstep1);
+        acc = fp4_compute_stage<EXACT>(first, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0, kstep1);
+        if (ks0 + 2 * kU < kstep1)
+            fp4_load_stage(first, rows.wp, rows.sp, rows.kb, ks0 + 2 * kU, kstep1);
+        if (ks0 + kU < kstep1)
+            acc = fp4_compute_stage<EXACT>(other, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0 + kU,
+                                           kstep1);
     }
     return acc;
 }
@@ -109,10 +152,40 @@ __device__ __forceinline__ void fp8_to_bf16_lds(const uint8_t *q, const uint8_t 
     }
 }
 
+// Quantise f32 x[dim] per 1x32 block (the act_quant_fp8_emit rule) straight
+// into LDS: exact bf16 values (EXACT) or e4m3 bytes + UE8M0 scales (native).
+// Each 32-value block is held by 8 lanes x 4 values.
 template <bool EXACT>
+__device__ __forceinline__ void quant_x_to_lds(const float *x, int dim, __bf16 *x_l,
+                                               uint8_t *xq_l, uint8_t *xs_l, int t, int nthr) {
+    for (int i = t * 4; i < dim; i += nthr * 4) {  // dim % 1024 == 0 is not required:
+        float4 v = *(const float4 *)(x + i);        // blocks never straddle a thread
+        float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                           fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        if (amax < 1e-4f) amax = 1e-4f;
+        const int e = log2_ceil(amax / 448.0f);
+        const float sc = __builtin_ldexpf(1.0f, e);
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t q[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) q[j] = f32_to_e4m3(rclamp(f[j] / sc, -448.0f, 448.0f));
+        if (EXACT) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) x_l[i + j] = (__bf16)(e4m3_to_f32(q[j]) * sc);
+        } else {
+            *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+            if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)(e + 127);
+        }
+    }
+}
+
+template <bool EXACT, bool XF32>
 __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
-    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs, const int32_t *__restrict__ idx,
-    const float *__restrict__ topk_w, const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
+    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs, const float *__restrict__ xf,
+    const int32_t *__restrict__ idx, const float *__restrict__ topk_w,
+    const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
     uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -120,14 +193,27 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     __bf16 *x_l = (__bf16 *)lds;
     uint8_t *xq_l = lds;
     uint8_t *xs_l = lds + dim;
-    __shared__ float part[kGluKSplit][2][32];
+    __shared__ float gu[2][32];
     const int slot = blockIdx.y;
     const int e = idx[slot];
     if (e < 0 || e >= n_experts) return;  // whole workgroup
     const int tile = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
-    if (EXACT) {
+    // wave -> (matrix, 16-row half of the 32-row tile), whole K
+    const int mat = w >> 1, half = w & 1;
+    const int row0 = tile * 32 + half * 16;
+    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
+    const Fp4Rows rows = fp4_rows((mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2),
+                                  (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32),
+                                  dim, lane);
+    const int ksteps = dim / 128;
+    Fp4Stage first;
+    fp4_load_stage(first, rows.wp, rows.sp, rows.kb, 0, ksteps);  // in flight during the prologue
+
+    if (XF32) {
+        quant_x_to_lds<EXACT>(xf, dim, x_l, xq_l, xs_l, t, kDecThreads);
+    } else if (EXACT) {
         fp8_to_bf16_lds(xq, xs, x_l, dim, t, kDecThreads);
     } else {
         for (int i = t * 16; i < dim; i += kDecThreads * 16)
@@ -136,32 +222,18 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     }
     __syncthreads();
 
-    // wave -> (matrix, 16-row half of the tile, K quarter)
-    const int unit = w & 3, ksp = w >> 2;
-    const int mat = unit >> 1, half = unit & 1;
-    const int ksteps = dim / 128;
-    const int k0 = ksp * ksteps / kGluKSplit, k1 = (ksp + 1) * ksteps / kGluKSplit;
-    const int row0 = tile * 32 + half * 16;
-    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
-    const uint8_t *W = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2);
-    const uint8_t *S = (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32);
-    v4f acc = stream_fp4_rows<EXACT>(W, S, xq_l, xs_l, x_l, dim, k0, k1, lane);
+    v4f acc = stream_fp4_rows<EXACT>(rows, first, xq_l, xs_l, x_l, 0, ksteps);
     // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
     if ((lane & 15) == 0) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) part[ksp][mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
+        for (int v = 0; v < 4; v++) gu[mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
     }
     __syncthreads();
     if (w != 0) return;
     // lanes 0-31 own the tile's 32 values; lanes 32-63 mirror them so the
     // half-wave reduction stays uniform, and do not store
     const int n = lane & 31;
-    float g = part[0][0][n], u = part[0][1][n];
-#pragma unroll
-    for (int q = 1; q < kGluKSplit; q++) {
-        g = g + part[q][0][n];
-        u = u + part[q][1][n];
-    }
+    float g = gu[0][n], u = gu[1][n];
     if (limit > 0.0f) {
         u = rclamp(u, -limit, limit);
         g = fminf(g, limit);
@@ -178,57 +250,70 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
 }
 
 template <bool EXACT>
-__global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
+__global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs, const int32_t *__restrict__ idx,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
     int inter, int n_experts, int top_k) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int32_t sorted_e[kMaxTopkDec];
-    __shared__ int32_t n_valid;
-    __shared__ float part[kMaxTopkDec][kRedKSplitMax][16];
+    __shared__ float part[kMaxTopkDec][kRedWaves][16];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int row0 = blockIdx.x * 16;
-    if (t == 0) {
-        int cnt = 0;
-        for (int s = 0; s < top_k; s++) {
-            int e = idx[s];
-            if (e < 0 || e >= n_experts) continue;
-            sorted_e[pick_rank(idx, top_k, n_experts, s)] = e;
-            cnt++;
-        }
-        n_valid = cnt;
+    // every wave ranks the (<= 16) picks itself: no barrier before the loads
+    int nv = 0;
+    for (int sidx = 0; sidx < top_k; sidx++) {
+        int e = idx[sidx];
+        nv += (e >= 0 && e < n_experts);
     }
+    // work units (pick, K part): a wave streams 16 rows of one expert's w2
+    // over 1/ksplit of inter; with 8 picks every wave owns one whole expert
+    const int ksteps = inter / 128;
+    int ksplit = kRedWaves / (nv > 0 ? nv : 1);
+    ksplit = ksplit < 1 ? 1 : ksplit;
+    if (ksplit > ksteps) ksplit = ksteps;
+    const int nunits = nv * ksplit;
+    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
+
     // EXACT: picks as bf16 (2 * top_k * inter bytes); native: e4m3 + scales
     __bf16 *h_l = (__bf16 *)lds;
     uint8_t *hq_l = lds;
     uint8_t *hs_l = lds + (size_t)top_k * inter;
-    __syncthreads();
-    const int nv = n_valid;
+
+    Fp4Rows rows{nullptr, nullptr, 0};
+    Fp4Stage first;
+    int unit = w, p = 0, ksp = 0, k0 = 0, k1 = 0;
+    if (unit < nunits) {
+        p = unit / ksplit;
+        ksp = unit % ksplit;
+        k0 = ksp * ksteps / ksplit;
+        k1 = (ksp + 1) * ksteps / ksplit;
+        const int e = expert_of_rank(idx, top_k, n_experts, p);
+        rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
+                        s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
+        fp4_load_stage(first, rows.wp, rows.sp, rows.kb, k0, k1);  // before the prologue
+    }
     if (EXACT) {
-        fp8_to_bf16_lds(hq, hs, h_l, nv * inter, t, kDecThreads);
+        fp8_to_bf16_lds(hq, hs, h_l, nv * inter, t, kRedThreads);
     } else {
-        for (int i = t * 16; i < nv * inter; i += kDecThreads * 16)
+        for (int i = t * 16; i < nv * inter; i += kRedThreads * 16)
             *(uint4 *)(hq_l + i) = *(const uint4 *)(hq + i);
-        for (int i = t; i < nv * (inter / 32); i += kDecThreads) hs_l[i] = hs[i];
+        for (int i = t; i < nv * (inter / 32); i += kRedThreads) hs_l[i] = hs[i];
     }
     __syncthreads();
 
-    // work units (pick, K part): every wave streams 16 rows of one expert's
-    // w2 over 1/ksplit of inter
-    const int ksteps = inter / 128;
-    int ksplit = (kDecThreads / 64) / (nv > 0 ? nv : 1);
-    ksplit = ksplit < 1 ? 1 : (ksplit > kRedKSplitMax ? kRedKSplitMax : ksplit);
-    if (ksplit > ksteps) ksplit = ksteps;
-    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
-    for (int unit = w; unit < nv * ksplit; unit += kDecThreads / 64) {
-        const int p = unit / ksplit, ksp = unit % ksplit;
-        const int e = sorted_e[p];
-        const uint8_t *W = w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2);
-        const uint8_t *S = s2 + (size_t)e * smat + (size_t)row0 * (inter / 32);
-        v4f acc = stream_fp4_rows<EXACT>(W, S, hq_l + (size_t)p * inter,
+    for (; unit < nunits; unit += kRedWaves) {
+        if (unit != w) {  // further units (fewer waves than units)
+            p = unit / ksplit;
+            ksp = unit % ksplit;
+            k0 = ksp * ksteps / ksplit;
+            k1 = (ksp + 1) * ksteps / ksplit;
+            const int e = expert_of_rank(idx, top_k, n_experts, p);
+            rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
+                            s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
+            fp4_load_stage(first, rows.wp, rows.sp, rows.kb, k0, k1);
+        }
+        v4f acc = stream_fp4_rows<EXACT>(rows, first, hq_l + (size_t)p * inter,
                                          hs_l + (size_t)p * (inter / 32),
-                                         h_l + (size_t)p * inter, inter, ksp * ksteps / ksplit,
-                                         (ksp + 1) * ksteps / ksplit, lane);
+                                         h_l + (size_t)p * inter, k0, k1);
         if ((lane & 15) == 0) {
 #pragma unroll
             for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
@@ -238,9 +323,9 @@ __global__ __launch_bounds__(kDecThreads) void expert_reduce_kernel(
     if (t < 16) {
         // one f32 add per expert, ascending expert id (moe.rs:76-84)
         float acc = 0.0f;
-        for (int p = 0; p < nv; p++) {
-            float pe = part[p][0][t];
-            for (int q = 1; q < ksplit; q++) pe = pe + part[p][q][t];
+        for (int q = 0; q < nv; q++) {
+            float pe = part[q][0][t];
+            for (int r = 1; r < ksplit; r++) pe = pe + part[q][r][t];
             acc = acc + pe;
         }
         y[row0 + t] = acc;
@@ -264,6 +349,53 @@ using namespace ws;
 
 extern "C" {
 
+}  // extern "C"
+
+namespace ws {
+
+static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf,
+                      const int32_t *topk_idx, const float *topk_w, const uint8_t *w1,
+                      const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, uint8_t *hq,
+                      uint8_t *hs, int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                      float swiglu_limit, hipStream_t stream) {
+    dim3 grid((unsigned)(inter / 32), (unsigned)top_k);
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
+#define WS_GLU(EX, XF)                                                                        \
+    hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF>), grid, dim3(kDecThreads), lds, stream, \
+                       xq, xs, xf, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim,         \
+                       (int)inter, (int)n_experts, (int)top_k, swiglu_limit)
+    if (exact) {
+        if (xf) WS_GLU(true, true); else WS_GLU(true, false);
+    } else {
+        if (xf) WS_GLU(false, true); else WS_GLU(false, false);
+    }
+#undef WS_GLU
+    return launch_status();
+}
+
+static int reduce_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
+                         const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
+                         int64_t inter, int64_t n_experts, int64_t top_k, hipStream_t stream) {
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    size_t lds = exact ? (size_t)top_k * inter * 2
+                       : (size_t)top_k * inter + (size_t)top_k * (inter / 32);
+    dim3 grid((unsigned)(dim / 16));
+    if (exact)
+        hipLaunchKernelGGL(expert_reduce_kernel<true>, grid, dim3(kRedThreads), lds, stream, hq,
+                           hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
+                           (int)top_k);
+    else
+        hipLaunchKernelGGL(expert_reduce_kernel<false>, grid, dim3(kRedThreads), lds, stream, hq,
+                           hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
+                           (int)top_k);
+    return launch_status();
+}
+
+}  // namespace ws
+
+extern "C" {
+
 int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *topk_idx,
                         const float *topk_w, const uint8_t *w1, const uint8_t *s1,
                         const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
@@ -276,18 +408,24 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
     if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 3) ||
         ((uintptr_t)s3 & 3))
         return WS_ERR_INVALID_ARG;
-    dim3 grid((unsigned)(inter / 32), (unsigned)top_k);
-    const bool exact = math_mode() == WS_MATH_EXACT;
-    size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
-    if (exact)
-        hipLaunchKernelGGL(expert_glu_quant_kernel<true>, grid, dim3(kDecThreads), lds, stream, xq,
-                           xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
-                           (int)n_experts, (int)top_k, swiglu_limit);
-    else
-        hipLaunchKernelGGL(expert_glu_quant_kernel<false>, grid, dim3(kDecThreads), lds, stream, xq,
-                           xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,
-                           (int)n_experts, (int)top_k, swiglu_limit);
-    return launch_status();
+    return glu_launch(xq, xs, nullptr, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                      n_experts, top_k, swiglu_limit, stream);
+}
+
+int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *topk_w,
+                          const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
+                          const uint8_t *s3, uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter,
+                          int64_t n_experts, int64_t top_k, float swiglu_limit,
+                          ws_stream_t stream) {
+    if (!x || !topk_idx || !topk_w || !w1 || !s1 || !w3 || !s3 || !hq || !hs)
+        return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 3) ||
+        ((uintptr_t)s3 & 3))
+        return WS_ERR_INVALID_ARG;
+    return glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                      n_experts, top_k, swiglu_limit, stream);
 }
 
 int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
@@ -297,25 +435,14 @@ int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_i
     int rc = check_decode_shapes(dim, inter, n_experts, top_k);
     if (rc) return rc;
     if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 3)) return WS_ERR_INVALID_ARG;
-    const bool exact = math_mode() == WS_MATH_EXACT;
-    size_t lds = exact ? (size_t)top_k * inter * 2 : (size_t)top_k * inter + (size_t)top_k * (inter / 32);
-    if (exact)
-        hipLaunchKernelGGL(expert_reduce_kernel<true>, dim3((unsigned)(dim / 16)), dim3(kDecThreads),
-                           lds, stream, hq, hs, topk_idx, w2, s2, y, (int)dim, (int)inter,
-                           (int)n_experts, (int)top_k);
-    else
-        hipLaunchKernelGGL(expert_reduce_kernel<false>, dim3((unsigned)(dim / 16)),
-                           dim3(kDecThreads), lds, stream, hq, hs, topk_idx, w2, s2, y, (int)dim,
-                           (int)inter, (int)n_experts, (int)top_k);
-    return launch_status();
+    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k) {
     if (dim <= 0 || inter <= 0 || top_k <= 0) return 0;
-    return align256(dim) + align256(dim / 32) + align256(top_k * inter) +
-           align256(top_k * (inter / 32));
+    return align256(top_k * inter) + align256(top_k * (inter / 32));
 }
 
 int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, const uint8_t *w1,
@@ -328,20 +455,17 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, 
     if (rc) return rc;
     if (workspace_bytes < ws_moe_decode_workspace_size(dim, inter, top_k) || !aligned16(workspace))
         return WS_ERR_INVALID_ARG;
-    uint8_t *p = (uint8_t *)workspace;
-    uint8_t *xq = p;
-    p += align256(dim);
-    uint8_t *xs = p;
-    p += align256(dim / 32);
-    uint8_t *hq = p;
-    p += align256(top_k * inter);
-    uint8_t *hs = p;
-    rc = ws_emit8(x, xq, xs, dim, stream);
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || !aligned16(w2) ||
+        ((uintptr_t)s1 & 3) || ((uintptr_t)s3 & 3) || ((uintptr_t)s2 & 3) || !topk_idx ||
+        !topk_w || !w1 || !s1 || !w3 || !s3 || !w2 || !s2 || !y)
+        return WS_ERR_INVALID_ARG;
+    // the gate/up kernel quantises x itself (the act_quant_fp8_emit rule)
+    uint8_t *hq = (uint8_t *)workspace;
+    uint8_t *hs = hq + align256(top_k * inter);
+    rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                    n_experts, top_k, swiglu_limit, stream);
     if (rc) return rc;
-    rc = ws_expert_glu_quant(xq, xs, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                             n_experts, top_k, swiglu_limit, stream);
-    if (rc) return rc;
-    return ws_expert_reduce(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
 }
 
 }  // extern "C"

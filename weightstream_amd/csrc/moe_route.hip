@@ -101,23 +101,26 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-// One workgroup per token row: scores, top-k selection, weights.
-__global__ __launch_bounds__(kTopkThreads) void topk_kernel(
+// One wave per token row: scores, top-k selection, weights. Each lane keeps
+// CPL candidates (expert e = lane + 64 c) as 64-bit keys (total-order key of
+// score+bias, then the complemented index so that ties pick the lower index);
+// a round is a lane-local max and a 6-step wave max, with no barrier.
+template <int CPL>
+__global__ __launch_bounds__(64) void topk_kernel(
     const float *__restrict__ logits, const float *__restrict__ bias, float *__restrict__ scores_out,
     int32_t *__restrict__ out_idx, float *__restrict__ out_w, int n_experts, int top_k,
     int score_func, float gate_temp, int norm, float route_scale) {
     __shared__ float sc[kMaxExperts];
-    __shared__ uint64_t wave_best[kTopkThreads / 64];
-    __shared__ int32_t picked[kMaxTopk];
+    __shared__ float ssum;
     const int m = blockIdx.x;
-    const int t = threadIdx.x;
+    const int lane = threadIdx.x;
     const float *lg = logits + (size_t)m * n_experts;
 
-    for (int e = t; e < n_experts; e += kTopkThreads) sc[e] = score_fn(lg[e], score_func, gate_temp);
-    __syncthreads();
+    for (int e = lane; e < n_experts; e += 64) sc[e] = score_fn(lg[e], score_func, gate_temp);
     if (score_func == WS_SCORE_SOFTMAX) {
         // num.rs:46-62: max, exp(x - max) in place with a sequential sum, divide
-        if (t == 0) {
+        __syncthreads();
+        if (lane == 0) {
             float mx = -__builtin_inff();
             for (int e = 0; e < n_experts; e++)
                 if (sc[e] > mx) mx = sc[e];
@@ -126,43 +129,37 @@ __global__ __launch_bounds__(kTopkThreads) void topk_kernel(
                 sc[e] = ws_expf(sc[e] - mx);
                 s = s + sc[e];
             }
-            wave_best[0] = (uint64_t)__float_as_uint(s);
+            ssum = s;
         }
         __syncthreads();
-        float s = __uint_as_float((uint32_t)wave_best[0]);
-        for (int e = t; e < n_experts; e += kTopkThreads) sc[e] = sc[e] / s;
-        __syncthreads();
+        const float s = ssum;
+        for (int e = lane; e < n_experts; e += 64) sc[e] = sc[e] / s;
     }
+    __syncthreads();
     if (scores_out)
-        for (int e = t; e < n_experts; e += kTopkThreads) scores_out[(size_t)m * n_experts + e] = sc[e];
+        for (int e = lane; e < n_experts; e += 64) scores_out[(size_t)m * n_experts + e] = sc[e];
 
-    // candidate keys: (total-order key of score+bias) << 32 | (~index)
-    uint64_t cand[kMaxExperts / kTopkThreads];
+    uint64_t cand[CPL];
 #pragma unroll
-    for (int c = 0; c < kMaxExperts / kTopkThreads; c++) {
-        int e = t + c * kTopkThreads;
+    for (int c = 0; c < CPL; c++) {
+        int e = lane + 64 * c;
         cand[c] = e < n_experts
                       ? ((uint64_t)total_key_u(sc[e] + bias[e]) << 32) | (uint32_t)(~(uint32_t)e)
                       : 0ull;
     }
+    int picked[kMaxTopk];
     for (int k = 0; k < top_k; k++) {
-        uint64_t best = 0;
+        uint64_t best = cand[0];
 #pragma unroll
-        for (int c = 0; c < kMaxExperts / kTopkThreads; c++) best = cand[c] > best ? cand[c] : best;
+        for (int c = 1; c < CPL; c++) best = cand[c] > best ? cand[c] : best;
         best = wave_max_u64(best);
-        if ((t & 63) == 0) wave_best[t >> 6] = best;
-        __syncthreads();
-        best = wave_best[0];
+        const int e = (int)(~(uint32_t)best);
+        picked[k] = e;
 #pragma unroll
-        for (int wv = 1; wv < kTopkThreads / 64; wv++) best = wave_best[wv] > best ? wave_best[wv] : best;
-        int e = (int)(~(uint32_t)best);
-        if (t == 0) picked[k] = e;
-#pragma unroll
-        for (int c = 0; c < kMaxExperts / kTopkThreads; c++)
-            if (t + c * kTopkThreads == e) cand[c] = 0ull;
-        __syncthreads();
+        for (int c = 0; c < CPL; c++)
+            if (lane + 64 * c == e) cand[c] = 0ull;
     }
-    if (t == 0) {
+    if (lane == 0) {
         float w[kMaxTopk];
         for (int k = 0; k < top_k; k++) w[k] = sc[picked[k]];
         // norm 1: moe.rs:61 (only when top_k > 1); norm 2: moe_select's
@@ -256,9 +253,16 @@ static int topk_launch(const float *logits, const float *bias, float *scores_out
     if (n_experts > kMaxExperts || top_k > kMaxTopk || top_k > n_experts || m > (1 << 30))
         return WS_ERR_SHAPE;
     if (score_func < 0 || score_func > kScoreIdentity) return WS_ERR_INVALID_ARG;
-    hipLaunchKernelGGL(topk_kernel, dim3((unsigned)m), dim3(kTopkThreads), 0, stream, logits, bias,
-                       scores_out, idx, w, (int)n_experts, (int)top_k, score_func, gate_temp, norm,
-                       route_scale);
+#define WS_TOPK(C)                                                                            \
+    hipLaunchKernelGGL(topk_kernel<C>, dim3((unsigned)m), dim3(64), 0, stream, logits, bias,      \
+                       scores_out, idx, w, (int)n_experts, (int)top_k, score_func, gate_temp,    \
+                       norm, route_scale)
+    if (n_experts <= 128) WS_TOPK(2);
+    else if (n_experts <= 256) WS_TOPK(4);
+    else if (n_experts <= 384) WS_TOPK(6);
+    else if (n_experts <= 512) WS_TOPK(8);
+    else WS_TOPK(16);
+#undef WS_TOPK
     return launch_status();
 }
 

@@ -206,6 +206,14 @@ def expert_glu_quant(act_x, act_x_s, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slo
           n_experts, top_k, swiglu_limit, _s(stream))
 
 
+def expert_glu_quant_x(x, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slots, s_slots, n, k,
+                       n_experts, top_k, swiglu_limit=10.0, stream=None):
+    """expert_glu_quant with the FP8 activation quantisation of f32 x fused in."""
+    _call("ws_expert_glu_quant_x", _ptr(x), _ptr(topk_idx), _ptr(topk_w), _ptr(w1), _ptr(w1_s),
+          _ptr(w3), _ptr(w3_s), _ptr(q_slots), _ptr(s_slots), k, n, n_experts, top_k,
+          swiglu_limit, _s(stream))
+
+
 def expert_reduce(act_slots, act_s_slots, w2, w2_s, gate_idx, y, dim, inter, n_experts, top_k,
                   stream=None):
     _call("ws_expert_reduce", _ptr(act_slots), _ptr(act_s_slots), _ptr(gate_idx), _ptr(w2),
