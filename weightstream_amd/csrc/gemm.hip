@@ -94,31 +94,31 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
     const float *saf = (const float *)SA;
     const float *sbf = (const float *)SB;
 
+    // steps past k1 re-load step k1-1 and are not used: unconditional loads
+    // keep a whole stage in flight behind one wait
     auto load = [&](GemmStage<WM, WN, U> &st, int ks0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            int ks = ks0 + u;
-            if (ks < k1) {
+            int ks = min(ks0 + u, k1 - 1);
 #pragma unroll
-                for (int i = 0; i < WM; i++) {
-                    const uint8_t *p = arow[i] + (size_t)ks * 128;
-                    st.a[u][i][0] = ldg16(p);
-                    st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
-                    if (SMODE == kUe8m0)
-                        st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
-                }
+            for (int i = 0; i < WM; i++) {
+                const uint8_t *p = arow[i] + (size_t)ks * 128;
+                st.a[u][i][0] = ldg16(p);
+                st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
+                if (SMODE == kUe8m0)
+                    st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * kb);
+            }
 #pragma unroll
-                for (int j = 0; j < WN; j++) {
-                    if (BFP4) {
-                        st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
-                    } else {
-                        const uint8_t *p = brow[j] + (size_t)ks * 128;
-                        st.b[u][j][0] = ldg16_stream(p);
-                        st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
-                    }
-                    if (SMODE == kUe8m0)
-                        st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
+            for (int j = 0; j < WN; j++) {
+                if (BFP4) {
+                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                } else {
+                    const uint8_t *p = brow[j] + (size_t)ks * 128;
+                    st.b[u][j][0] = ldg16_stream(p);
+                    st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
                 }
+                if (SMODE == kUe8m0)
+                    st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
             }
         }
     };

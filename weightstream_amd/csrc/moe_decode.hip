@@ -27,9 +27,11 @@
 
 namespace ws {
 
-constexpr int kDecThreads = 256;   // glu: 4 waves = (w1|w3) x (rows 0-15|16-31)
-constexpr int kRedWaves = 8;       // reduce: 8 waves over (expert, K part) units
-constexpr int kRedThreads = 64 * kRedWaves;
+constexpr int kGluStreamWaves = 4;  // glu: (w1|w3) x (rows 0-15|16-31), + 1 helper wave
+constexpr int kDecThreads = 64 * (kGluStreamWaves + 1);
+constexpr int kRedWaves = 8;        // reduce: 8 streaming waves over (expert, K part) units
+constexpr int kRedHelpers = 2;      // + 2 helper waves preparing the picks in LDS
+constexpr int kRedThreads = 64 * (kRedWaves + kRedHelpers);
 constexpr int kMaxTopkDec = 16;
 constexpr int kU = 8;  // 128-K steps per register stage (two stages in flight)
 
@@ -69,15 +71,16 @@ struct Fp4Stage {
     uint32_t s[kU];
 };
 
+// Steps past kstep1 re-load step kstep1-1 (never used): the loads stay
+// unconditional, so the compiler can keep a whole stage in flight and wait
+// for it with one counter check instead of branching around each load.
 __device__ __forceinline__ void fp4_load_stage(Fp4Stage &st, const uint8_t *wp, const uint8_t *sp,
                                                int kb, int ks0, int kstep1) {
 #pragma unroll
     for (int u = 0; u < kU; u++) {
-        int ks = ks0 + u;
-        if (ks < kstep1) {
-            st.w[u] = ldg16_stream(wp + (size_t)ks * 64);
-            st.s[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
-        }
+        int ks = min(ks0 + u, kstep1 - 1);
+        st.w[u] = ldg16_stream(wp + (size_t)ks * 64);
+        st.s[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
     }
 }
 
@@ -118,65 +121,120 @@ __device__ __forceinline__ Fp4Rows fp4_rows(const uint8_t *w_rows, const uint8_t
     return Fp4Rows{w_rows + (size_t)r * (k / 2) + kb * 16, s_rows + (size_t)r * (k / 32), kb};
 }
 
-// Continue streaming after the caller loaded `first` = steps [kstep0, kstep0+kU).
+// Stream steps [kstep0, kstep1) given the first two stages already in flight
+// (s0 = steps kstep0.., s1 = kstep0+kU..): while one stage is multiplied the
+// other one's loads are outstanding.
 template <bool EXACT>
-__device__ __forceinline__ v4f stream_fp4_rows(const Fp4Rows &rows, Fp4Stage &first,
+__device__ __forceinline__ v4f stream_fp4_rows(const Fp4Rows &rows, Fp4Stage &s0, Fp4Stage &s1,
                                                const uint8_t *xq_lds, const uint8_t *xs_lds,
                                                const __bf16 *x_lds, int kstep0, int kstep1) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    Fp4Stage other;
     for (int ks0 = kstep0; ks0 < kstep1; ks0 += 2 * kU) {
-        if (ks0 + kU < kstep1) fp4_load_stage(other, rows.wp, rows.sp, rows.kb, ks0 + kU, kstep1);
-        acc = fp4_compute_stage<EXACT>(first, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0, kstep1);
+        acc = fp4_compute_stage<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0, kstep1);
         if (ks0 + 2 * kU < kstep1)
-            fp4_load_stage(first, rows.wp, rows.sp, rows.kb, ks0 + 2 * kU, kstep1);
+            fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, ks0 + 2 * kU, kstep1);
         if (ks0 + kU < kstep1)
-            acc = fp4_compute_stage<EXACT>(other, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0 + kU,
+            acc = fp4_compute_stage<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0 + kU,
                                            kstep1);
+        if (ks0 + 3 * kU < kstep1)
+            fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, ks0 + 3 * kU, kstep1);
     }
     return acc;
 }
 
-// n e4m3 values + their UE8M0 scales (global) -> exact bf16 values in LDS.
-// n % 8 == 0; every thread converts 8 values (one 8-byte chunk of one block).
-__device__ __forceinline__ void fp8_to_bf16_lds(const uint8_t *q, const uint8_t *s, __bf16 *dst,
-                                                int n, int t, int nthreads) {
-    for (int i = t * 8; i < n; i += nthreads * 8) {
-        uint2 v = *(const uint2 *)(q + i);
-        float sc = e8m0_to_f32(s[i / 32]);
-        u32x4v o = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, sc, false),
-                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.x, sc, true),
-                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, sc, false),
-                       __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v.y, sc, true));
-        *(u32x4v *)(dst + i) = o;
+// ---- LDS preparation by helper waves -------------------------------------
+// A helper wave fills LDS with the operand every streaming wave multiplies
+// (the token, or the picks' hidden states). Streaming waves issue their weight
+// loads first and meet the helper at an LDS-only barrier, so their loads stay
+// in flight while the helper works (load counters are per wave).
+
+// Barrier that orders LDS only: global loads issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+constexpr int kHelperRounds = 16;  // 16-byte loads per lane and batch
+
+// f32 token x[n] -> FP8 1x32 quantisation (the act_quant_fp8_emit rule) into
+// LDS: exact bf16 values (EXACT) or e4m3 bytes + UE8M0 scales. One helper
+// wave; a 32-value block is 8 lanes x 4 values of one round.
+template <bool EXACT>
+__device__ __forceinline__ void helper_quant_x(const float *x, int n, __bf16 *x_l, uint8_t *xq_l,
+                                               uint8_t *xs_l, int lane) {
+    for (int base = 0; base < n; base += kHelperRounds * 256) {
+        float4 v[kHelperRounds];
+#pragma unroll
+        for (int j = 0; j < kHelperRounds; j++)
+            v[j] = *(const float4 *)(x + min(base + (j * 64 + lane) * 4, n - 4));
+#pragma unroll
+        for (int j = 0; j < kHelperRounds; j++) {
+            const int i = base + (j * 64 + lane) * 4;
+            if (base + j * 256 >= n) break;  // uniform
+            float amax = fmaxf(fmaxf(__builtin_fabsf(v[j].x), __builtin_fabsf(v[j].y)),
+                               fmaxf(__builtin_fabsf(v[j].z), __builtin_fabsf(v[j].w)));
+#pragma unroll
+            for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+            if (amax < 1e-4f) amax = 1e-4f;
+            const int e = log2_ceil(amax / 448.0f);
+            const float sc = __builtin_ldexpf(1.0f, e);
+            const float f[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            uint32_t q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] / sc, -448.0f, 448.0f));
+            if (EXACT) {
+                u32x4v o;
+                const float d[4] = {e4m3_to_f32(q[0]) * sc, e4m3_to_f32(q[1]) * sc,
+                                    e4m3_to_f32(q[2]) * sc, e4m3_to_f32(q[3]) * sc};
+                // exact: every value has at most 4 significant bits
+                *(uint2 *)(x_l + i) = uint2{(__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xFFFF0000u),
+                                            (__float_as_uint(d[2]) >> 16) | (__float_as_uint(d[3]) & 0xFFFF0000u)};
+                (void)o;
+            } else {
+                *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+                if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)(e + 127);
+            }
+        }
     }
 }
 
-// Quantise f32 x[dim] per 1x32 block (the act_quant_fp8_emit rule) straight
-// into LDS: exact bf16 values (EXACT) or e4m3 bytes + UE8M0 scales (native).
-// Each 32-value block is held by 8 lanes x 4 values.
+// n e4m3 bytes + UE8M0 scales -> exact bf16 values in LDS (EXACT) or a plain
+// byte copy (native); `hw` helper waves, helper index `hi`.
 template <bool EXACT>
-__device__ __forceinline__ void quant_x_to_lds(const float *x, int dim, __bf16 *x_l,
-                                               uint8_t *xq_l, uint8_t *xs_l, int t, int nthr) {
-    for (int i = t * 4; i < dim; i += nthr * 4) {  // dim % 1024 == 0 is not required:
-        float4 v = *(const float4 *)(x + i);        // blocks never straddle a thread
-        float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
-                           fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+__device__ __forceinline__ void helper_fp8_to_lds(const uint8_t *q, const uint8_t *s, int n,
+                                                  __bf16 *dst, uint8_t *q_l, uint8_t *s_l, int hi,
+                                                  int hw, int lane) {
+    const int stride = hw * 64 * 16;
+    for (int base = hi * 64 * 16; base < n; base += kHelperRounds * stride) {
+        uint4 v[kHelperRounds];
+        uint32_t sc[kHelperRounds];
 #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-        if (amax < 1e-4f) amax = 1e-4f;
-        const int e = log2_ceil(amax / 448.0f);
-        const float sc = __builtin_ldexpf(1.0f, e);
-        const float f[4] = {v.x, v.y, v.z, v.w};
-        uint32_t q[4];
+        for (int j = 0; j < kHelperRounds; j++) {
+            const int i = min(base + j * stride + lane * 16, n - 16);
+            v[j] = *(const uint4 *)(q + i);
+            sc[j] = s[i / 32];
+        }
 #pragma unroll
-        for (int j = 0; j < 4; j++) q[j] = f32_to_e4m3(rclamp(f[j] / sc, -448.0f, 448.0f));
-        if (EXACT) {
+        for (int j = 0; j < kHelperRounds; j++) {
+            const int i = base + j * stride + lane * 16;
+            if (base + j * stride >= n) break;  // uniform: n % (64*16) == 0 not assumed below
+            if (i >= n) continue;
+            if (EXACT) {
+                const float f = e8m0_to_f32(sc[j]);
+                const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) x_l[i + j] = (__bf16)(e4m3_to_f32(q[j]) * sc);
-        } else {
-            *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-            if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)(e + 127);
+                for (int c = 0; c < 2; c++) {
+                    u32x4v o = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, false),
+                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, true),
+                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, false),
+                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, true));
+                    *(u32x4v *)(dst + i + 8 * c) = o;
+                }
+            } else {
+                *(uint4 *)(q_l + i) = v[j];
+                if ((i & 31) == 0) s_l[i / 32] = (uint8_t)sc[j];
+            }
         }
     }
 }
@@ -199,34 +257,33 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     if (e < 0 || e >= n_experts) return;  // whole workgroup
     const int tile = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-
-    // wave -> (matrix, 16-row half of the 32-row tile), whole K
-    const int mat = w >> 1, half = w & 1;
-    const int row0 = tile * 32 + half * 16;
-    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
-    const Fp4Rows rows = fp4_rows((mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2),
-                                  (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32),
-                                  dim, lane);
     const int ksteps = dim / 128;
-    Fp4Stage first;
-    fp4_load_stage(first, rows.wp, rows.sp, rows.kb, 0, ksteps);  // in flight during the prologue
 
-    if (XF32) {
-        quant_x_to_lds<EXACT>(xf, dim, x_l, xq_l, xs_l, t, kDecThreads);
-    } else if (EXACT) {
-        fp8_to_bf16_lds(xq, xs, x_l, dim, t, kDecThreads);
+    // streaming waves 0-3 -> (matrix, 16-row half of the 32-row tile), whole K;
+    // wave 4 prepares the token in LDS
+    const int mat = (w >> 1) & 1, half = w & 1;
+    Fp4Rows rows{nullptr, nullptr, 0};
+    Fp4Stage st0, st1;
+    if (w < kGluStreamWaves) {
+        const int row0 = tile * 32 + half * 16;
+        const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
+        rows = fp4_rows((mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2),
+                        (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32), dim, lane);
+        fp4_load_stage(st0, rows.wp, rows.sp, rows.kb, 0, ksteps);
+        fp4_load_stage(st1, rows.wp, rows.sp, rows.kb, kU, ksteps);
     } else {
-        for (int i = t * 16; i < dim; i += kDecThreads * 16)
-            *(uint4 *)(xq_l + i) = *(const uint4 *)(xq + i);
-        for (int i = t; i < dim / 32; i += kDecThreads) xs_l[i] = xs[i];
+        if (XF32) helper_quant_x<EXACT>(xf, dim, x_l, xq_l, xs_l, lane);
+        else helper_fp8_to_lds<EXACT>(xq, xs, dim, x_l, xq_l, xs_l, 0, 1, lane);
     }
-    __syncthreads();
+    lds_barrier();
 
-    v4f acc = stream_fp4_rows<EXACT>(rows, first, xq_l, xs_l, x_l, 0, ksteps);
-    // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
-    if ((lane & 15) == 0) {
+    if (w < kGluStreamWaves) {
+        v4f acc = stream_fp4_rows<EXACT>(rows, st0, st1, xq_l, xs_l, x_l, 0, ksteps);
+        // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
+        if ((lane & 15) == 0) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) gu[mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
+            for (int v = 0; v < 4; v++) gu[mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
+        }
     }
     __syncthreads();
     if (w != 0) return;
@@ -279,29 +336,10 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     uint8_t *hs_l = lds + (size_t)top_k * inter;
 
     Fp4Rows rows{nullptr, nullptr, 0};
-    Fp4Stage first;
+    Fp4Stage s0, s1;
     int unit = w, p = 0, ksp = 0, k0 = 0, k1 = 0;
-    if (unit < nunits) {
-        p = unit / ksplit;
-        ksp = unit % ksplit;
-        k0 = ksp * ksteps / ksplit;
-        k1 = (ksp + 1) * ksteps / ksplit;
-        const int e = expert_of_rank(idx, top_k, n_experts, p);
-        rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
-                        s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
-        fp4_load_stage(first, rows.wp, rows.sp, rows.kb, k0, k1);  // before the prologue
-    }
-    if (EXACT) {
-        fp8_to_bf16_lds(hq, hs, h_l, nv * inter, t, kRedThreads);
-    } else {
-        for (int i = t * 16; i < nv * inter; i += kRedThreads * 16)
-            *(uint4 *)(hq_l + i) = *(const uint4 *)(hq + i);
-        for (int i = t; i < nv * (inter / 32); i += kRedThreads) hs_l[i] = hs[i];
-    }
-    __syncthreads();
-
-    for (; unit < nunits; unit += kRedWaves) {
-        if (unit != w) {  // further units (fewer waves than units)
+    if (w < kRedWaves) {
+        if (unit < nunits) {
             p = unit / ksplit;
             ksp = unit % ksplit;
             k0 = ksp * ksteps / ksplit;
@@ -309,14 +347,35 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
             const int e = expert_of_rank(idx, top_k, n_experts, p);
             rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
                             s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
-            fp4_load_stage(first, rows.wp, rows.sp, rows.kb, k0, k1);
+            fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, k0, k1);
+            fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, k0 + kU, k1);
         }
-        v4f acc = stream_fp4_rows<EXACT>(rows, first, hq_l + (size_t)p * inter,
-                                         hs_l + (size_t)p * (inter / 32),
-                                         h_l + (size_t)p * inter, k0, k1);
-        if ((lane & 15) == 0) {
+    } else {
+        helper_fp8_to_lds<EXACT>(hq, hs, nv * inter, h_l, hq_l, hs_l, w - kRedWaves,
+                                 kRedHelpers, lane);
+    }
+    lds_barrier();
+
+    if (w < kRedWaves) {
+        for (; unit < nunits; unit += kRedWaves) {
+            if (unit != w) {  // further units (fewer waves than units)
+                p = unit / ksplit;
+                ksp = unit % ksplit;
+                k0 = ksp * ksteps / ksplit;
+                k1 = (ksp + 1) * ksteps / ksplit;
+                const int e = expert_of_rank(idx, top_k, n_experts, p);
+                rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
+                                s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
+                fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, k0, k1);
+                fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, k0 + kU, k1);
+            }
+            v4f acc = stream_fp4_rows<EXACT>(rows, s0, s1, hq_l + (size_t)p * inter,
+                                             hs_l + (size_t)p * (inter / 32),
+                                             h_l + (size_t)p * inter, k0, k1);
+            if ((lane & 15) == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
+                for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
+            }
         }
     }
     __syncthreads();
@@ -335,9 +394,8 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
 static int check_decode_shapes(int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k) {
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || top_k > kMaxTopkDec) return WS_ERR_SHAPE;
-    // LDS holds the token / the picks as bf16 (2 bytes per value)
-    if (dim > 32768 || inter > 32768 || top_k * inter > 32768 || n_experts > (1 << 20))
-        return WS_ERR_SHAPE;
+    // LDS holds the token and the picks as bf16 (2 bytes per value)
+    if (dim > 32768 || top_k * inter > 32768 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
     return WS_OK;
 }
 

@@ -26,9 +26,9 @@ constexpr int kScaleOne = 127;  // UE8M0 byte of 1.0
 // UE8M0 byte -> f32 (weightstream-core quant.rs:41-48): 2^(b-127) built from
 // bits, exact for every byte including b=0 (2^-127, subnormal).
 __device__ __forceinline__ float e8m0_to_f32(uint32_t b) {
-    if (b == 0xFF) return __builtin_nanf("");
-    if (b == 0) return __uint_as_float(0x00400000u);
-    return __uint_as_float(b << 23);
+    uint32_t bits = b ? (b << 23) : 0x00400000u;   // selects, no branch
+    bits = (b == 0xFF) ? 0x7FC00000u : bits;
+    return __uint_as_float(bits);
 }
 
 // quant.rs:60-73 log2_ceil via the exponent field.
