@@ -65,7 +65,15 @@ def make_experts(L, torch, gen, dev):
     return w1, s1, w3, s3, w2, s2
 
 
-def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
+def pack_experts(L, raw):
+    """Upload-time relayout into the fragment-major layout (ws_prepack_fp4)."""
+    w1, s1, w3, s3, w2, s2 = raw
+    out = (L.prepack_fp4_new(w1, s1, E * INTER, DIM) + L.prepack_fp4_new(w3, s3, E * INTER, DIM)
+           + L.prepack_fp4_new(w2, s2, E * DIM, INTER))
+    return out
+
+
+def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
     logits = torch.randn((n_tokens, E), device=dev, generator=gen)
     bias = torch.randn((E,), device=dev, generator=gen) * 0.1
     x = torch.randn((n_tokens, DIM), device=dev, generator=gen)
@@ -77,7 +85,7 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
     def step(t, stream):
         L.moe_topk(logits[t], bias, None, idx[t], wts[t], 1, E, TOPK, L.SCORE_SIGMOID, 1.0, True,
                    1.0, stream=stream)
-        L.moe_decode(x[t], idx[t], wts[t], *slabs, y[t], DIM, INTER, E, TOPK, ws, stream=stream)
+        L.moe_decode(x[t], idx[t], wts[t], *packed, y[t], DIM, INTER, E, TOPK, ws, stream=stream)
 
     # eager pass: results for the parity check and the per-kernel timing inputs
     s = torch.cuda.current_stream()
@@ -86,25 +94,26 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
     torch.cuda.synchronize()
     y_eager = y.clone()
 
+    # the timed region is one replay of a graph holding exactly `steps` decode
+    # steps (token t uses buffer t % n_tokens); warmup is `warmup` eager steps
+    # plus one untimed replay (first-replay upload)
     g = torch.cuda.CUDAGraph()
     cs = torch.cuda.Stream()
     with torch.cuda.stream(cs):
         with torch.cuda.graph(g, stream=cs):
-            for t in range(n_tokens):
-                step(t, cs)
+            for t in range(steps):
+                step(t % n_tokens, cs)
     torch.cuda.synchronize()
-    reps_w = max(1, math.ceil(warmup / n_tokens))
-    for _ in range(reps_w):
-        g.replay()
+    for t in range(warmup):
+        step(t % n_tokens, s)
+    g.replay()
     torch.cuda.synchronize()
     if not torch.equal(y, y_eager):
         raise RuntimeError("graph replay differs from the eager pass")
-    reps = max(1, math.ceil(steps / n_tokens))
-    done = reps * n_tokens
+    done = steps
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms_per_step = dt * 1e3 / done
@@ -112,7 +121,7 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen):
     gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
 
     # per-kernel durations with events on the launch stream
-    w1, s1, w3, s3, w2, s2 = slabs
+    w1, s1, w3, s3, w2, s2 = packed
     xq = torch.empty((n_tokens, DIM), dtype=torch.uint8, device=dev)
     xs = torch.empty((n_tokens, DIM // 32), dtype=torch.uint8, device=dev)
     hq = torch.empty((n_tokens, TOPK, INTER), dtype=torch.uint8, device=dev)
@@ -281,13 +290,15 @@ def main():
     gen.manual_seed(0)
     t0 = time.time()
     slabs = make_experts(L, torch, gen, dev)
-    log("experts generated in %.1fs" % (time.time() - t0))
+    packed = pack_experts(L, slabs)
+    torch.cuda.synchronize()
+    log("experts generated and packed in %.1fs" % (time.time() - t0))
     gen_state = gen.get_state()
     L.set_math_mode(L.MATH_NATIVE)
-    native = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, slabs, gen)
+    native = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, slabs, gen, packed)
     L.set_math_mode(L.MATH_EXACT)
     gen.set_state(gen_state)
-    res = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, slabs, gen)
+    res = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, slabs, gen, packed)
     k = res["kernels"]["expert_glu_quant_kernel"]
     roof = {"kernel": "expert_glu_quant_kernel", "bound": "hbm", "achieved": k["GB/s"],
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["GB/s"] / PEAK_HBM_GBS,

@@ -168,9 +168,27 @@ int ws_swiglu(const float *gate, const float *up, float *out, int64_t n, float r
               ws_stream_t stream);
 
 /* ---------------------------------------------------------------------
+ * Packed FP4 expert weights. The routed-expert entry points below read FP4
+ * weight slabs in a fragment-major layout: 16-row bands, each 128-K step of a
+ * band one contiguous 1 KB (MFMA lane order), scales grouped per lane and 8
+ * steps. ws_prepack_fp4 converts the on-disk layout (packed e2m1 [rows,
+ * cols/2], UE8M0 [rows, cols/32]; quant.rs:189-215) at upload, as the
+ * reference engine re-tiles its expert slabs (engine.rs:842-884
+ * pack_expert_scales / tile_major_expert, launch.rs:383-428 tensor maps).
+ * rows % 16 == 0, cols % 128 == 0. Weight bytes keep their size
+ * (rows*cols/2); scales take ws_packed_fp4_scale_bytes(rows, cols) bytes.
+ * An expert slab [E, rows, cols] is E packed matrices back to back: pack
+ * each expert (or pass rows = E*rows when every expert has `rows` % 16 == 0:
+ * bands never straddle experts).
+ * ------------------------------------------------------------------- */
+size_t ws_packed_fp4_scale_bytes(int64_t rows, int64_t cols);
+int ws_prepack_fp4(const uint8_t *w, const uint8_t *s, int64_t rows, int64_t cols, uint8_t *pw,
+                   uint8_t *ps, ws_stream_t stream);
+
+/* ---------------------------------------------------------------------
  * Routed experts, M = 1 decode (moe.rs:75-84,162-208; moe_grouped.cu:61-224).
- * Expert slabs: w1/w3 packed e2m1 [E, inter, dim/2] + UE8M0 [E, inter, dim/32];
- * w2 [E, dim, inter/2] + [E, dim, inter/32]. topk_idx/topk_w as ws_moe_topk
+ * Expert slabs (packed, see ws_prepack_fp4): w1/w3 [E, inter, dim] and
+ * w2 [E, dim, inter]. topk_idx/topk_w as ws_moe_topk
  * writes them (top-k order); kernels sort the picks by ascending expert id.
  * ------------------------------------------------------------------- */
 /* Fused expert_glu + expert_quant (moe_grouped.cu:61,128): for each pick p

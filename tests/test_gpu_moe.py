@@ -27,10 +27,19 @@ def _init():
 
 
 def _slabs(gen, E, dim, inter):
+    """Raw (on-disk layout) expert slabs; the kernels read _packed(raw)."""
     w1, s1 = rand_fp4_weights(gen, E * inter, dim)
     w3, s3 = rand_fp4_weights(gen, E * inter, dim)
     w2, s2 = rand_fp4_weights(gen, E * dim, inter)
     return w1, s1, w3, s3, w2, s2
+
+
+def _packed(raw, E, dim, inter):
+    w1, s1, w3, s3, w2, s2 = raw
+    p1 = L.prepack_fp4_new(w1, s1, E * inter, dim)
+    p3 = L.prepack_fp4_new(w3, s3, E * inter, dim)
+    p2 = L.prepack_fp4_new(w2, s2, E * dim, inter)
+    return p1 + p3 + p2
 
 
 def _host_experts(slabs, experts, E, dim, inter):
@@ -49,10 +58,10 @@ def _host_experts(slabs, experts, E, dim, inter):
     return out
 
 
-def _run_decode(x, idx, w, slabs, dim, inter, E, k, limit=10.0):
+def _run_decode(x, idx, w, packed, dim, inter, E, k, limit=10.0):
     ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
     y = torch.empty(dim, dtype=torch.float32, device=DEV)
-    L.moe_decode(x, idx, w, *slabs, y, dim, inter, E, k, ws, swiglu_limit=limit)
+    L.moe_decode(x, idx, w, *packed, y, dim, inter, E, k, ws, swiglu_limit=limit)
     return y
 
 
@@ -70,7 +79,7 @@ def test_moe_decode_matches_oracle(E, dim, inter, k):
     w = torch.empty(k, dtype=torch.float32, device=DEV)
     L.moe_topk(dev(logits), dev(bias), None, idx, w, 1, E, k, O.SCORE_SIGMOID, 1.0, True, 1.0)
     x = rng.standard_normal(dim).astype(np.float32)
-    y = _run_decode(dev(x), idx, w, slabs, dim, inter, E, k)
+    y = _run_decode(dev(x), idx, w, _packed(slabs, E, dim, inter), dim, inter, E, k)
     hi, hw = host(idx), host(w)
     ri, rw = O.route(O.score(logits, O.SCORE_SIGMOID), bias, k)
     assert np.array_equal(hi, ri) and np.array_equal(hw.view(np.uint32), rw.view(np.uint32))
@@ -92,16 +101,17 @@ def test_moe_decode_split_entry_points_and_order():
     ids = np.array([20, 3, 31, 0, 7], np.int32)
     wts = np.array([0.3, 0.1, 0.25, 0.15, 0.2], np.float32)
     announce("moe_decode split entry points")
-    y1 = _run_decode(dev(x), dev(ids), dev(wts), slabs, dim, inter, E, k)
+    packed = _packed(slabs, E, dim, inter)
+    y1 = _run_decode(dev(x), dev(ids), dev(wts), packed, dim, inter, E, k)
     perm = np.array([3, 0, 4, 1, 2])
-    y2 = _run_decode(dev(x), dev(ids[perm]), dev(wts[perm]), slabs, dim, inter, E, k)
+    y2 = _run_decode(dev(x), dev(ids[perm]), dev(wts[perm]), packed, dim, inter, E, k)
     assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
     xq = torch.empty(dim, dtype=torch.uint8, device=DEV)
     xs = torch.empty(dim // 32, dtype=torch.uint8, device=DEV)
     L.emit8(dev(x), xq, xs, dim)
     hq = torch.empty((k, inter), dtype=torch.uint8, device=DEV)
     hs = torch.empty((k, inter // 32), dtype=torch.uint8, device=DEV)
-    w1, s1, w3, s3, w2, s2 = slabs
+    w1, s1, w3, s3, w2, s2 = packed
     L.expert_glu_quant(xq, xs, dev(ids), dev(wts), w1, s1, w3, s3, hq, hs, inter, dim, E, k)
     y3 = torch.empty(dim, dtype=torch.float32, device=DEV)
     L.expert_reduce(hq, hs, w2, s2, dev(ids), y3, dim, inter, E, k)
@@ -140,7 +150,8 @@ def test_moe_decode_closed_form_of_reference_gpu_test():
     x = torch.full((dim,), 0.01, dtype=torch.float32, device=DEV)
     idx = torch.tensor([1, 0], dtype=torch.int32, device=DEV)
     w = torch.tensor([1.0, 1.0], dtype=torch.float32, device=DEV)
-    y = host(_run_decode(x, idx, w, (w1, s1, w1, s1, w2, s2), dim, inter, E, k))
+    packed = _packed((w1, s1, w1, s1, w2, s2), E, dim, inter)
+    y = host(_run_decode(x, idx, w, packed, dim, inter, E, k))
     g = dim * 0.5 * 0.009765625                      # 20.0 -> clamped to 10
     assert g > 10
     h = np.float32(np.float32(O.silu(10.0)) * np.float32(10.0))
@@ -157,11 +168,32 @@ def test_moe_decode_invalid_picks_are_skipped():
     E, dim, inter, k = 8, 1024, 256, 3
     gen = torch.Generator(device=DEV)
     gen.manual_seed(720)
-    slabs = _slabs(gen, E, dim, inter)
+    packed = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
     x = dev(rng.standard_normal(dim).astype(np.float32))
     announce("moe_decode invalid picks")
     ya = _run_decode(x, dev(np.array([2, -1, 5], np.int32)), dev(np.array([.5, .9, .5], np.float32)),
-                     slabs, dim, inter, E, k)
+                     packed, dim, inter, E, k)
     yb = _run_decode(x, dev(np.array([5, 2], np.int32)), dev(np.array([.5, .5], np.float32)),
-                     slabs, dim, inter, E, 2)
+                     packed, dim, inter, E, 2)
     assert np.array_equal(host(ya).view(np.uint32), host(yb).view(np.uint32))
+
+
+def test_prepack_fp4_layout():
+    """ws_prepack_fp4 against a numpy restatement of the packed layout:
+    band rt, step ks, lane l -> row 16rt + l%16, K [128ks + 32(l/16), +32)."""
+    rng = np.random.default_rng(730)
+    for rows, cols in [(32, 256), (48, 1152)]:   # 1152/128 = 9 steps: a padded scale group
+        w = rng.integers(0, 256, (rows, cols // 2)).astype(np.uint8)
+        s = rng.integers(100, 140, (rows, cols // 32)).astype(np.uint8)
+        announce("prepack_fp4 %dx%d" % (rows, cols))
+        pw, ps = L.prepack_fp4_new(dev(w), dev(s), rows, cols)
+        pw, ps = host(pw), host(ps)
+        ksn, ks8 = cols // 128, (cols // 128 + 7) // 8
+        assert ps.size == (rows // 16) * ks8 * 64 * 8
+        for rt in range(rows // 16):
+            for ks in range(ksn):
+                for lane in range(64):
+                    r, g = 16 * rt + lane % 16, lane // 16
+                    off = ((rt * ksn + ks) * 64 + lane) * 16
+                    assert np.array_equal(pw[off:off + 16], w[r, ks * 64 + g * 16:ks * 64 + g * 16 + 16])
+                    assert ps[((rt * ks8 + ks // 8) * 64 + lane) * 8 + ks % 8] == s[r, ks * 4 + g]

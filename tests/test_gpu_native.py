@@ -61,7 +61,10 @@ def test_native_moe_decode():
     announce("native moe_decode")
     ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
     y = torch.empty(dim, dtype=torch.float32, device=DEV)
-    L.moe_decode(dev(x), dev(ids), dev(wts), w1, s1, w3, s3, w2, s2, y, dim, inter, E, k, ws)
+    p1 = L.prepack_fp4_new(w1, s1, E * inter, dim)
+    p3 = L.prepack_fp4_new(w3, s3, E * inter, dim)
+    p2 = L.prepack_fp4_new(w2, s2, E * dim, inter)
+    L.moe_decode(dev(x), dev(ids), dev(wts), *p1, *p3, *p2, y, dim, inter, E, k, ws)
     H = [t.view(E, -1).cpu().numpy() for t in (w1, s1, w3, s3, w2, s2)]
     want = O.moe_routed(*H, dim, inter, x, ids, wts)
     _check(host(y), want, "moe_decode")

@@ -68,10 +68,19 @@ def test_dispatch_bit_exact(m, E, k):
 
 
 def _slabs(gen, E, dim, inter):
+    """Raw (on-disk layout) expert slabs; the kernels read _packed(raw)."""
     w1, s1 = rand_fp4_weights(gen, E * inter, dim)
     w3, s3 = rand_fp4_weights(gen, E * inter, dim)
     w2, s2 = rand_fp4_weights(gen, E * dim, inter)
     return w1, s1, w3, s3, w2, s2
+
+
+def _packed(raw, E, dim, inter):
+    w1, s1, w3, s3, w2, s2 = raw
+    p1 = L.prepack_fp4_new(w1, s1, E * inter, dim)
+    p3 = L.prepack_fp4_new(w3, s3, E * inter, dim)
+    p2 = L.prepack_fp4_new(w2, s2, E * dim, inter)
+    return p1 + p3 + p2
 
 
 def _host_experts(slabs, experts, E, dim, inter):
@@ -104,7 +113,7 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
     ws = torch.empty(L.moe_prefill_workspace_size(m, dim, inter, k, E), dtype=torch.uint8,
                      device=DEV)
     y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
-    L.moe_prefill(dev(x), idx, w, *slabs, y, m, dim, inter, E, k, ws)
+    L.moe_prefill(dev(x), idx, w, *_packed(slabs, E, dim, inter), y, m, dim, inter, E, k, ws)
     gi, gw, gy = host(idx), host(w), host(y)
     rows = np.linspace(0, m - 1, check).astype(int)
     H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
@@ -118,7 +127,7 @@ def test_prefill_of_one_token_matches_decode():
     E, dim, inter, k = 32, 1024, 512, 4
     gen = torch.Generator(device=DEV)
     gen.manual_seed(950)
-    slabs = _slabs(gen, E, dim, inter)
+    slabs = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
     x = dev(rng.standard_normal((1, dim)).astype(np.float32))
     idx = dev(np.array([[9, 2, 30, 17]], np.int32))
     w = dev(np.array([[0.4, 0.3, 0.2, 0.1]], np.float32))

@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libweightstream_hip.so")
 
-SOURCES = ["common.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip"]
+SOURCES = ["common.hip", "pack.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

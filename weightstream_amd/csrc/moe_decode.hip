@@ -24,16 +24,17 @@
 //    rows; per-expert results meet in LDS and are added in ascending expert id,
 //    one f32 add per expert like the reference's acc_f32 chain.
 #include "ws_internal.hpp"
+#include "ws_pack.hpp"
 
 namespace ws {
 
-constexpr int kGluStreamWaves = 4;  // glu: (w1|w3) x (rows 0-15|16-31), + 1 helper wave
+constexpr int kGluKParts = 2;       // glu: (w1|w3) x (rows 0-15|16-31) x K half,
+constexpr int kGluStreamWaves = 4 * kGluKParts;  // + 1 helper wave
 constexpr int kDecThreads = 64 * (kGluStreamWaves + 1);
 constexpr int kRedWaves = 8;        // reduce: 8 streaming waves over (expert, K part) units
 constexpr int kRedHelpers = 2;      // + 2 helper waves preparing the picks in LDS
 constexpr int kRedThreads = 64 * (kRedWaves + kRedHelpers);
 constexpr int kMaxTopkDec = 16;
-constexpr int kU = 8;  // 128-K steps per register stage (two stages in flight)
 
 // rank of pick `slot` among valid picks ordered by (expert id, slot)
 __device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_experts, int slot) {
@@ -56,46 +57,22 @@ __device__ __forceinline__ int expert_of_rank(const int32_t *idx, int top_k, int
     return 0;
 }
 
-// Stream a 16-row FP4 weight tile against the token held in LDS and return the
-// 16x16 MFMA accumulator (all columns equal). w_rows / s_rows point at row 0
-// of the tile and its scale row; row strides k/2 bytes and k/32 bytes; the
-// 128-K steps [kstep0, kstep1) are streamed.
-// EXACT: the token is bf16 in LDS (x_lds), the weights are dequantised to
-// bf16 in registers, bf16 MFMA. Native: the token is e4m3 + UE8M0 in LDS
-// (xq_lds, xs_lds) and feeds the scaled FP4 x FP8 MFMA.
-// Loads run in two register stages of kU steps: stage n+1 is in flight while
-// stage n is multiplied, and the caller may issue the first stage (`first`)
-// before it prepares the token in LDS, hiding that work behind the loads.
-struct Fp4Stage {
-    uint4 w[kU];
-    uint32_t s[kU];
-};
-
-// Steps past kstep1 re-load step kstep1-1 (never used): the loads stay
-// unconditional, so the compiler can keep a whole stage in flight and wait
-// for it with one counter check instead of branching around each load.
-__device__ __forceinline__ void fp4_load_stage(Fp4Stage &st, const uint8_t *wp, const uint8_t *sp,
-                                               int kb, int ks0, int kstep1) {
-#pragma unroll
-    for (int u = 0; u < kU; u++) {
-        int ks = min(ks0 + u, kstep1 - 1);
-        st.w[u] = ldg16_stream(wp + (size_t)ks * 64);
-        st.s[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
-    }
-}
-
+// Multiply one register stage of a packed 16-row FP4 band with the operand in
+// LDS: EXACT -> bf16 values (x_lds); native -> e4m3 bytes + UE8M0 scales
+// (xq_lds, xs_lds). Returns the updated 16x16 accumulator (row i of the band
+// in D[i][*]).
 template <bool EXACT>
-__device__ __forceinline__ v4f fp4_compute_stage(const Fp4Stage &st, v4f acc,
-                                                 const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                                 const __bf16 *x_lds, int kb, int ks0,
-                                                 int kstep1) {
+__device__ __forceinline__ v4f fp4_compute(const Fp4Stage &st, v4f acc, const uint8_t *xq_lds,
+                                           const uint8_t *xs_lds, const __bf16 *x_lds, int kb,
+                                           int ks0, int kend) {
 #pragma unroll
     for (int u = 0; u < kU; u++) {
-        int ks = ks0 + u;
-        if (ks >= kstep1) continue;
+        const int ks = ks0 + u;
+        if (ks >= kend) continue;  // uniform
+        const uint32_t sw = stage_scale(st, u);
         if (EXACT) {
             v8bf wq[4], xb[4];
-            cvt_fp4x32(st.w[u], e8m0_to_f32(st.s[u] & 0xFF), wq);
+            cvt_fp4x32(st.w[u], e8m0_to_f32(sw), wq);
             const v8bf *xp = (const v8bf *)(x_lds + ks * 128 + kb * 32);
 #pragma unroll
             for (int j = 0; j < 4; j++) xb[j] = xp[j];
@@ -103,43 +80,35 @@ __device__ __forceinline__ v4f fp4_compute_stage(const Fp4Stage &st, v4f acc,
         } else {
             const uint8_t *xp = xq_lds + ks * 128 + kb * 16;
             v8i b = frag_from(*(const uint4 *)xp, *(const uint4 *)(xp + 64));
-            int sx = xs_lds[ks * 4 + kb];
-            acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(st.w[u]), b, acc, (int)st.s[u], sx);
+            acc = mfma_scaled<kFmtFp4, kFmtFp8>(frag_from4(st.w[u]), b, acc, (int)sw,
+                                                (int)xs_lds[ks * 4 + kb]);
         }
     }
     return acc;
 }
 
-struct Fp4Rows {
-    const uint8_t *wp, *sp;
-    int kb;
-};
-
-__device__ __forceinline__ Fp4Rows fp4_rows(const uint8_t *w_rows, const uint8_t *s_rows, int k,
-                                            int lane) {
-    const int r = lane & 15, kb = lane >> 4;
-    return Fp4Rows{w_rows + (size_t)r * (k / 2) + kb * 16, s_rows + (size_t)r * (k / 32), kb};
-}
-
-// Stream steps [kstep0, kstep1) given the first two stages already in flight
-// (s0 = steps kstep0.., s1 = kstep0+kU..): while one stage is multiplied the
-// other one's loads are outstanding.
+// Stream band steps [k0, k1) (k0 % 8 == 0) given the first two stages already
+// in flight (s0 = k0.., s1 = k0+kU..): one stage is multiplied while the
+// other's loads are outstanding.
 template <bool EXACT>
-__device__ __forceinline__ v4f stream_fp4_rows(const Fp4Rows &rows, Fp4Stage &s0, Fp4Stage &s1,
-                                               const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                               const __bf16 *x_lds, int kstep0, int kstep1) {
+__device__ __forceinline__ v4f fp4_stream(const Fp4Band &b, Fp4Stage &s0, Fp4Stage &s1,
+                                          const uint8_t *xq_lds, const uint8_t *xs_lds,
+                                          const __bf16 *x_lds, int kb, int k0, int k1) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ks0 = kstep0; ks0 < kstep1; ks0 += 2 * kU) {
-        acc = fp4_compute_stage<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0, kstep1);
-        if (ks0 + 2 * kU < kstep1)
-            fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, ks0 + 2 * kU, kstep1);
-        if (ks0 + kU < kstep1)
-            acc = fp4_compute_stage<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, rows.kb, ks0 + kU,
-                                           kstep1);
-        if (ks0 + 3 * kU < kstep1)
-            fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, ks0 + 3 * kU, kstep1);
+    for (int ks0 = k0; ks0 < k1; ks0 += 2 * kU) {
+        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        if (ks0 + 2 * kU < k1) fp4_load(s0, b, ks0 + 2 * kU, k1);
+        if (ks0 + kU < k1) acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
+        if (ks0 + 3 * kU < k1) fp4_load(s1, b, ks0 + 3 * kU, k1);
     }
     return acc;
+}
+
+// K range [k0, k1) of part `part` of `parts`, in whole 8-step stages
+__device__ __forceinline__ void k_part(int ksteps, int part, int parts, int &k0, int &k1) {
+    const int stages = (ksteps + kU - 1) / kU;
+    k0 = min(ksteps, part * stages / parts * kU);
+    k1 = min(ksteps, (part + 1) * stages / parts * kU);
 }
 
 // ---- LDS preparation by helper waves -------------------------------------
@@ -251,7 +220,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     __bf16 *x_l = (__bf16 *)lds;
     uint8_t *xq_l = lds;
     uint8_t *xs_l = lds + dim;
-    __shared__ float gu[2][32];
+    __shared__ float gu[kGluKParts][2][32];
     const int slot = blockIdx.y;
     const int e = idx[slot];
     if (e < 0 || e >= n_experts) return;  // whole workgroup
@@ -259,18 +228,20 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int ksteps = dim / 128;
 
-    // streaming waves 0-3 -> (matrix, 16-row half of the 32-row tile), whole K;
-    // wave 4 prepares the token in LDS
-    const int mat = (w >> 1) & 1, half = w & 1;
-    Fp4Rows rows{nullptr, nullptr, 0};
+    // streaming waves -> (matrix, 16-row half of the 32-row tile, K half);
+    // the last wave prepares the token in LDS
+    const int mat = (w >> 1) & 1, half = w & 1, kpart = w >> 2;
+    Fp4Band band{nullptr, nullptr, 0};
     Fp4Stage st0, st1;
+    int k0 = 0, k1 = 0;
     if (w < kGluStreamWaves) {
-        const int row0 = tile * 32 + half * 16;
-        const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
-        rows = fp4_rows((mat ? w3 : w1) + (size_t)e * wmat + (size_t)row0 * (dim / 2),
-                        (mat ? s3 : s1) + (size_t)e * smat + (size_t)row0 * (dim / 32), dim, lane);
-        fp4_load_stage(st0, rows.wp, rows.sp, rows.kb, 0, ksteps);
-        fp4_load_stage(st1, rows.wp, rows.sp, rows.kb, kU, ksteps);
+        k_part(ksteps, kpart, kGluKParts, k0, k1);
+        const size_t wmat = (size_t)inter * (dim / 2);
+        const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
+        band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat, (mat ? s3 : s1) + (size_t)e * smat,
+                        tile * 2 + half, dim, lane);
+        fp4_load(st0, band, k0, k1);
+        fp4_load(st1, band, k0 + kU, k1);
     } else {
         if (XF32) helper_quant_x<EXACT>(xf, dim, x_l, xq_l, xs_l, lane);
         else helper_fp8_to_lds<EXACT>(xq, xs, dim, x_l, xq_l, xs_l, 0, 1, lane);
@@ -278,11 +249,11 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     lds_barrier();
 
     if (w < kGluStreamWaves) {
-        v4f acc = stream_fp4_rows<EXACT>(rows, st0, st1, xq_l, xs_l, x_l, 0, ksteps);
+        v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1);
         // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
         if ((lane & 15) == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) gu[mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
+            for (int v = 0; v < 4; v++) gu[kpart][mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
         }
     }
     __syncthreads();
@@ -290,7 +261,12 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     // lanes 0-31 own the tile's 32 values; lanes 32-63 mirror them so the
     // half-wave reduction stays uniform, and do not store
     const int n = lane & 31;
-    float g = gu[0][n], u = gu[1][n];
+    float g = gu[0][0][n], u = gu[0][1][n];
+#pragma unroll
+    for (int q = 1; q < kGluKParts; q++) {
+        g = g + gu[q][0][n];
+        u = u + gu[q][1][n];
+    }
     if (limit > 0.0f) {
         u = rclamp(u, -limit, limit);
         g = fminf(g, limit);
@@ -326,29 +302,29 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int ksteps = inter / 128;
     int ksplit = kRedWaves / (nv > 0 ? nv : 1);
     ksplit = ksplit < 1 ? 1 : ksplit;
-    if (ksplit > ksteps) ksplit = ksteps;
+    const int stages = (ksteps + kU - 1) / kU;
+    if (ksplit > stages) ksplit = stages;
     const int nunits = nv * ksplit;
-    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
+    const size_t wmat = (size_t)dim * (inter / 2);
+    const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
 
     // EXACT: picks as bf16 (2 * top_k * inter bytes); native: e4m3 + scales
     __bf16 *h_l = (__bf16 *)lds;
     uint8_t *hq_l = lds;
     uint8_t *hs_l = lds + (size_t)top_k * inter;
 
-    Fp4Rows rows{nullptr, nullptr, 0};
+    Fp4Band band{nullptr, nullptr, 0};
     Fp4Stage s0, s1;
     int unit = w, p = 0, ksp = 0, k0 = 0, k1 = 0;
     if (w < kRedWaves) {
         if (unit < nunits) {
             p = unit / ksplit;
             ksp = unit % ksplit;
-            k0 = ksp * ksteps / ksplit;
-            k1 = (ksp + 1) * ksteps / ksplit;
+            k_part(ksteps, ksp, ksplit, k0, k1);
             const int e = expert_of_rank(idx, top_k, n_experts, p);
-            rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
-                            s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
-            fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, k0, k1);
-            fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, k0 + kU, k1);
+            band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter, lane);
+            fp4_load(s0, band, k0, k1);
+            fp4_load(s1, band, k0 + kU, k1);
         }
     } else {
         helper_fp8_to_lds<EXACT>(hq, hs, nv * inter, h_l, hq_l, hs_l, w - kRedWaves,
@@ -361,17 +337,16 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
             if (unit != w) {  // further units (fewer waves than units)
                 p = unit / ksplit;
                 ksp = unit % ksplit;
-                k0 = ksp * ksteps / ksplit;
-                k1 = (ksp + 1) * ksteps / ksplit;
+                k_part(ksteps, ksp, ksplit, k0, k1);
                 const int e = expert_of_rank(idx, top_k, n_experts, p);
-                rows = fp4_rows(w2 + (size_t)e * wmat + (size_t)row0 * (inter / 2),
-                                s2 + (size_t)e * smat + (size_t)row0 * (inter / 32), inter, lane);
-                fp4_load_stage(s0, rows.wp, rows.sp, rows.kb, k0, k1);
-                fp4_load_stage(s1, rows.wp, rows.sp, rows.kb, k0 + kU, k1);
+                band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter,
+                                lane);
+                fp4_load(s0, band, k0, k1);
+                fp4_load(s1, band, k0 + kU, k1);
             }
-            v4f acc = stream_fp4_rows<EXACT>(rows, s0, s1, hq_l + (size_t)p * inter,
-                                             hs_l + (size_t)p * (inter / 32),
-                                             h_l + (size_t)p * inter, k0, k1);
+            v4f acc = fp4_stream<EXACT>(band, s0, s1, hq_l + (size_t)p * inter,
+                                        hs_l + (size_t)p * (inter / 32), h_l + (size_t)p * inter,
+                                        lane >> 4, k0, k1);
             if ((lane & 15) == 0) {
 #pragma unroll
                 for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];

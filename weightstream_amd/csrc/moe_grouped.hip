@@ -21,6 +21,7 @@
 // Because slots ascend with expert id, the combine sums each token's expert
 // outputs in ascending expert id, the reference CPU order.
 #include "ws_internal.hpp"
+#include "ws_pack.hpp"
 
 namespace ws {
 
@@ -160,10 +161,10 @@ __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
         arow[i] = xq + (size_t)tok * dim + (EXACT ? kb * 32 : kb * 16);
         srow[i] = xs + (size_t)tok * (dim / 32);
     }
-    const int n = nt * kTile + half * 16 + r;
-    const size_t wmat = (size_t)inter * (dim / 2), smat = (size_t)inter * (dim / 32);
-    const uint8_t *bp = (mat ? w3 : w1) + (size_t)e * wmat + (size_t)n * (dim / 2) + kb * 16;
-    const uint8_t *sp = (mat ? s3 : s1) + (size_t)e * smat + (size_t)n * (dim / 32);
+    const size_t wmat = (size_t)inter * (dim / 2);
+    const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
+    const Fp4Band band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat,
+                                  (mat ? s3 : s1) + (size_t)e * smat, nt * 2 + half, dim, lane);
 
     v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     const int ksteps = dim / 128;
@@ -173,10 +174,11 @@ __global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
         uint32_t sb[U], sa[U][2];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            int ks = ks0 + u;
-            if (ks < ksteps) {
-                bf[u] = ldg16_stream(bp + (size_t)ks * 64);
-                sb[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+            // steps past the end re-load the last one (unused): no branches
+            int ks = min(ks0 + u, ksteps - 1);
+            {
+                bf[u] = ldg16_stream(band.w + (size_t)ks * 1024);
+                sb[u] = band.s[(size_t)(ks / 8) * 512 + ks % 8];
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     af[u][i][0] = ldg16(arow[i] + ks * 128);
@@ -247,9 +249,10 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
     const int r = lane & 15, kb = lane >> 4;
     const int slot0 = tile * kTile;
     const int n = blockIdx.x * 64 + w * 16 + r;
-    const size_t wmat = (size_t)dim * (inter / 2), smat = (size_t)dim * (inter / 32);
-    const uint8_t *bp = w2 + (size_t)e * wmat + (size_t)n * (inter / 2) + kb * 16;
-    const uint8_t *sp = s2 + (size_t)e * smat + (size_t)n * (inter / 32);
+    const size_t wmat = (size_t)dim * (inter / 2);
+    const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
+    const Fp4Band band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat,
+                                  blockIdx.x * 4 + w, inter, lane);
     const uint8_t *arow[2];
     const uint8_t *srow[2];
 #pragma unroll
@@ -265,10 +268,11 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
         uint32_t sb[U], sa[U][2];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            int ks = ks0 + u;
-            if (ks < ksteps) {
-                bf[u] = ldg16_stream(bp + (size_t)ks * 64);
-                sb[u] = *(const uint32_t *)(sp + ks * 4) >> (8 * kb);
+            // steps past the end re-load the last one (unused): no branches
+            int ks = min(ks0 + u, ksteps - 1);
+            {
+                bf[u] = ldg16_stream(band.w + (size_t)ks * 1024);
+                sb[u] = band.s[(size_t)(ks / 8) * 512 + ks % 8];
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
                     af[u][i][0] = ldg16(arow[i] + ks * 128);

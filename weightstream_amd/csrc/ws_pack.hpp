@@ -1,0 +1,63 @@
+// Fragment-major ("packed") layout of FP4 weight matrices, and the streaming
+// primitives of the kernels that read it.
+//
+// A [R, K] e2m1 matrix (R % 16 == 0, K % 128 == 0) with one UE8M0 scale per
+// row and 32 K is stored as 16-row bands; band rt, 128-K step ks and MFMA lane
+// l (row 16rt + l%16, K [128ks + 32(l/16), +32)) own 16 weight bytes at
+//     ((rt * KS + ks) * 64 + l) * 16,          KS = K / 128,
+// so a wave reads one contiguous 1 KB per step and walks a band's K as one
+// contiguous run. The scale bytes of 8 consecutive steps of a lane are
+// contiguous:
+//     (((rt * KS8 + ks / 8) * 64 + l) * 8 + ks % 8,   KS8 = ceil(KS / 8).
+// Expert slabs [E, R, K] concatenate E packed matrices. ws_prepack_fp4 builds
+// the layout from the on-disk one (weightstream-core quant.rs:189-215) at
+// upload, as the reference engine re-tiles its expert slabs
+// (weightstream-gpu engine.rs:868 tile_major_expert).
+#pragma once
+
+#include "ws_device.hpp"
+
+namespace ws {
+
+constexpr int kU = 8;  // 128-K steps per register stage
+
+__host__ __device__ constexpr int64_t packed_fp4_scale_bytes(int64_t rows, int64_t cols) {
+    return (rows / 16) * ((cols / 128 + 7) / 8) * 64 * 8;
+}
+
+struct Fp4Band {
+    const uint8_t *w;  // this lane's 16 bytes of step 0
+    const uint8_t *s;  // this lane's scale byte of step 0 (8-step group 0)
+    int ks_total;
+};
+
+// Band `rt` of a packed [R, K] matrix at (w, s), for lane `lane`.
+__device__ __forceinline__ Fp4Band fp4_band(const uint8_t *w, const uint8_t *s, int rt, int k,
+                                           int lane) {
+    const int ks = k / 128, ks8 = (ks + 7) / 8;
+    return Fp4Band{w + ((size_t)rt * ks * 64 + lane) * 16, s + ((size_t)rt * ks8 * 64 + lane) * 8,
+                   ks};
+}
+
+struct Fp4Stage {
+    uint4 w[kU];
+    uint2 s;  // scale bytes of the kU steps
+};
+
+// Steps [ks0, ks0 + kU) of the band; steps past `kend` re-load step kend-1
+// (never used), keeping the loads unconditional so that one counter wait
+// covers a whole stage. ks0 % 8 == 0.
+__device__ __forceinline__ void fp4_load(Fp4Stage &st, const Fp4Band &b, int ks0, int kend) {
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        int ks = min(ks0 + u, kend - 1);
+        st.w[u] = ldg16_stream(b.w + (size_t)ks * 1024);
+    }
+    st.s = *(const uint2 *)(b.s + (size_t)(ks0 / 8) * 512);
+}
+
+__device__ __forceinline__ uint32_t stage_scale(const Fp4Stage &st, int u) {
+    return ((u < 4 ? st.s.x : st.s.y) >> (8 * (u & 3))) & 0xFF;
+}
+
+}  // namespace ws

@@ -121,6 +121,23 @@ def weight_quant_fp8(w, q, s, rows, cols, stream=None):
     _call("ws_weight_quant_fp8", _ptr(w), _ptr(q), _ptr(s), rows, cols, _s(stream))
 
 
+def packed_fp4_scale_bytes(rows, cols):
+    return int(_lib.load().ws_packed_fp4_scale_bytes(rows, cols))
+
+
+def prepack_fp4(w, s, rows, cols, pw, ps, stream=None):
+    """On-disk FP4 layout -> the fragment-major layout the expert kernels read."""
+    _call("ws_prepack_fp4", _ptr(w), _ptr(s), rows, cols, _ptr(pw), _ptr(ps), _s(stream))
+
+
+def prepack_fp4_new(w, s, rows, cols, stream=None):
+    """Allocate and fill the packed copy of (w, s); returns (pw, ps)."""
+    pw = torch.empty(rows * cols // 2, dtype=torch.uint8, device=w.device)
+    ps = torch.empty(packed_fp4_scale_bytes(rows, cols), dtype=torch.uint8, device=w.device)
+    prepack_fp4(w, s, rows, cols, pw, ps, stream=stream)
+    return pw, ps
+
+
 # ---- GEMMs (launch.rs:344-377, 717-804) -------------------------------------
 def fp8_gemm(a, sa, b, sb, out, m, n, k, stream=None):
     _call("ws_fp8_gemm", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k, _s(stream))
