@@ -190,6 +190,8 @@ int ws_prepack_fp4(const uint8_t *w, const uint8_t *s, int64_t rows, int64_t col
  * Expert slabs (packed, see ws_prepack_fp4): w1/w3 [E, inter, dim] and
  * w2 [E, dim, inter]. topk_idx/topk_w as ws_moe_topk
  * writes them (top-k order); kernels sort the picks by ascending expert id.
+ * Shapes: dim % 128 == 0, inter % 128 == 0, dim <= 16384, top_k <= 16,
+ * top_k * inter <= 32768; WS_ERR_SHAPE otherwise.
  * ------------------------------------------------------------------- */
 /* Fused expert_glu + expert_quant (moe_grouped.cu:61,128): for each pick p
  * (rank r by ascending expert id) h = silu(min(w1.x,L)) * clamp(w3.x,+-L) * w_p,
@@ -201,7 +203,7 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
                         int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
                         float swiglu_limit, ws_stream_t stream);
 /* As ws_expert_glu_quant with the activation quantisation (act_quant_fp8_emit,
- * actquant.cu:47) fused in: x is the f32 token [dim]. */
+ * actquant.cu:47) fused in: x is the f32 token [dim], dim <= 8192. */
 int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *topk_w,
                           const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
                           const uint8_t *s3, uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter,
@@ -213,7 +215,8 @@ int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_i
                      const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
                      int64_t inter, int64_t n_experts, int64_t top_k, ws_stream_t stream);
 /* Whole routed MoE for one token from f32 x: glu_quant_x -> reduce (two
- * kernels; hq/hs of the picks live in the workspace).
+ * kernels; hq/hs of the picks live in the workspace; for dim > 8192 the
+ * token is quantised into the workspace by a third kernel first).
  * workspace >= ws_moe_decode_workspace_size(dim, inter, top_k) bytes. */
 size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k);
 int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,

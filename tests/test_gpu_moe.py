@@ -66,7 +66,8 @@ def _run_decode(x, idx, w, packed, dim, inter, E, k, limit=10.0):
 
 
 @pytest.mark.parametrize("E,dim,inter,k", [(16, 1024, 512, 4), (64, 2048, 768, 6),
-                                           (384, 4096, 2048, 8)])
+                                           (384, 4096, 2048, 8), (8, 128, 128, 3),
+                                           (8, 10240, 256, 2)])
 def test_moe_decode_matches_oracle(E, dim, inter, k):
     rng = np.random.default_rng(700 + E)
     gen = torch.Generator(device=DEV)

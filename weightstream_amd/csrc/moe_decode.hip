@@ -15,22 +15,26 @@
 // registers (v_cvt_scalef32_pk_bf16_fp4 applies the UE8M0 scale) and keeps
 // the token as exact bf16 in LDS; native mode feeds the scaled FP4 x FP8 MFMA.
 //
-//  glu_quant: grid (inter/32, top_k), 16 waves: a wave streams 16 rows of w1 or
-//    w3 of the 32-row tile over a quarter of K (8 KB at the BASELINE shape, all
-//    loads in flight at once); the quarters are added in LDS in fixed order,
-//    then the epilogue applies SwiGLU x routing weight and quantises the 32
-//    values (one FP8 1x32 block) straight to e4m3 + UE8M0.
-//  reduce: grid (dim/16), 16 waves over (expert, K part) units for 16 output
-//    rows; per-expert results meet in LDS and are added in ascending expert id,
-//    one f32 add per expert like the reference's acc_f32 chain.
+//  glu_quant: 8 streaming waves per workgroup. A wave streams one packed
+//    16-row band of w1 or w3 (double-buffered 8 KB register stages) and,
+//    while its first stages are in flight, quantises 1/8 of the token into
+//    LDS; the waves meet at an LDS-only barrier. At the BASELINE shape a workgroup owns two 32-row tiles
+//    and every wave walks the whole K (256 workgroups: one resident round);
+//    smaller problems give a workgroup one tile with K split in halves. The
+//    epilogue applies SwiGLU x routing weight and quantises each 32-value
+//    tile (one FP8 1x32 block) straight to e4m3 + UE8M0.
+//  reduce: grid (dim/16), 8 streaming waves over (expert, K part) units for
+//    16 output rows + 2 helper waves that decode the picks' hidden states
+//    into LDS; per-expert results meet in LDS and are added in ascending
+//    expert id, one f32 add per expert like the reference's acc_f32 chain.
 #include "ws_internal.hpp"
 #include "ws_pack.hpp"
 
 namespace ws {
 
 constexpr int kGluKParts = 2;       // glu: (w1|w3) x (rows 0-15|16-31) x K half,
-constexpr int kGluStreamWaves = 4 * kGluKParts;  // + 1 helper wave
-constexpr int kDecThreads = 64 * (kGluStreamWaves + 1);
+constexpr int kGluStreamWaves = 4 * kGluKParts;
+constexpr int kDecThreads = 64 * kGluStreamWaves;
 constexpr int kRedWaves = 8;        // reduce: 8 streaming waves over (expert, K part) units
 constexpr int kRedHelpers = 2;      // + 2 helper waves preparing the picks in LDS
 constexpr int kRedThreads = 64 * (kRedWaves + kRedHelpers);
@@ -89,17 +93,31 @@ __device__ __forceinline__ v4f fp4_compute(const Fp4Stage &st, v4f acc, const ui
 
 // Stream band steps [k0, k1) (k0 % 8 == 0) given the first two stages already
 // in flight (s0 = k0.., s1 = k0+kU..): one stage is multiplied while the
-// other's loads are outstanding.
+// other's loads are outstanding. The steady-state loop reloads both stages
+// unconditionally, so its body is straight-line and each wait covers only the
+// stage about to be used; the last two or three stages are the tail.
 template <bool EXACT>
 __device__ __forceinline__ v4f fp4_stream(const Fp4Band &b, Fp4Stage &s0, Fp4Stage &s1,
                                           const uint8_t *xq_lds, const uint8_t *xs_lds,
                                           const __bf16 *x_lds, int kb, int k0, int k1) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int ks0 = k0; ks0 < k1; ks0 += 2 * kU) {
+    const int nst = (k1 - k0 + kU - 1) / kU;
+    int i = 0, ks0 = k0;
+    for (; i + 3 < nst; i += 2, ks0 += 2 * kU) {
         acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
-        if (ks0 + 2 * kU < k1) fp4_load(s0, b, ks0 + 2 * kU, k1);
-        if (ks0 + kU < k1) acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
-        if (ks0 + 3 * kU < k1) fp4_load(s1, b, ks0 + 3 * kU, k1);
+        fp4_load(s0, b, ks0 + 2 * kU, k1);
+        acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
+        fp4_load(s1, b, ks0 + 3 * kU, k1);
+    }
+    const int rest = nst - i;
+    if (rest == 3) {
+        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        fp4_load(s0, b, ks0 + 2 * kU, k1);
+        acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
+        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0 + 2 * kU, k1);
+    } else {
+        if (rest >= 1) acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        if (rest == 2) acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
     }
     return acc;
 }
@@ -117,6 +135,11 @@ __device__ __forceinline__ void k_part(int ksteps, int part, int parts, int &k0,
 // loads first and meet the helper at an LDS-only barrier, so their loads stay
 // in flight while the helper works (load counters are per wave).
 
+// Compiler-only barrier: memory accesses are not moved across it, so loads
+// issued before it leave the wave first (load counters then return them in
+// issue order and a wait for them does not cover later loads).
+__device__ __forceinline__ void mem_order() { __asm__ volatile("" ::: "memory"); }
+
 // Barrier that orders LDS only: global loads issued before it stay in flight.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -126,44 +149,105 @@ __device__ __forceinline__ void lds_barrier() {
 
 constexpr int kHelperRounds = 16;  // 16-byte loads per lane and batch
 
-// f32 token x[n] -> FP8 1x32 quantisation (the act_quant_fp8_emit rule) into
-// LDS: exact bf16 values (EXACT) or e4m3 bytes + UE8M0 scales. One helper
-// wave; a 32-value block is 8 lanes x 4 values of one round.
+// ---- the token, split over the streaming waves ----------------------------
+// Each of the `parts` streaming waves converts its share of the token into
+// LDS. It issues the share's loads before its weight loads (loads return in
+// order, so the conversion waits for the token bytes only) and converts while
+// its weight stages are in flight. All rounds of a share are loaded up front
+// (straight-line code: a wait for them never covers a weight load): 4 rounds
+// of 256 f32 values (dim <= 8192) or 2 rounds of 1 KB e4m3 (dim <= 16384).
+constexpr int kXRF = 4, kXRQ = 2;
+constexpr int kMaxDimF32 = kGluStreamWaves * kXRF * 256;
+constexpr int kMaxDimFp8 = kGluStreamWaves * kXRQ * 1024;
+
+struct TokenRegs {
+    float4 f[kXRF];   // f32 token: 4 values of one 1x32 block per lane and round
+    uint4 q[kXRQ];    // e4m3 token: 16 bytes per lane and round
+    uint32_t s[kXRQ];
+};
+
+// f32 token, blocks [b0, b1) of 32 values: round r covers 8 blocks, a block
+// is 8 lanes x 4 values. Loads are clamped into the share (or block 0).
+__device__ __forceinline__ void tok_load_f32(TokenRegs &tr, const float *x, int b0, int b1,
+                                             int lane) {
+#pragma unroll
+    for (int j = 0; j < kXRF; j++) {
+        const int blk = max(min(b0 + j * 8 + (lane >> 3), b1 - 1), 0);
+        tr.f[j] = *(const float4 *)(x + (size_t)blk * 32 + (lane & 7) * 4);
+    }
+}
+
+// FP8 1x32 quantisation of the loaded rounds (the act_quant_fp8_emit rule,
+// weightstream-ref actquant.rs:21-45) into LDS: exact bf16 values (EXACT) or
+// e4m3 bytes + UE8M0 scales.
 template <bool EXACT>
-__device__ __forceinline__ void helper_quant_x(const float *x, int n, __bf16 *x_l, uint8_t *xq_l,
-                                               uint8_t *xs_l, int lane) {
-    for (int base = 0; base < n; base += kHelperRounds * 256) {
-        float4 v[kHelperRounds];
+__device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b1, int lane,
+                                              __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l) {
 #pragma unroll
-        for (int j = 0; j < kHelperRounds; j++)
-            v[j] = *(const float4 *)(x + min(base + (j * 64 + lane) * 4, n - 4));
+    for (int j = 0; j < kXRF; j++) {
+        if (j * 8 >= b1 - b0) break;  // uniform
+        const int blk = b0 + j * 8 + (lane >> 3);
+        const float4 v = tr.f[j];
+        float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                           fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
 #pragma unroll
-        for (int j = 0; j < kHelperRounds; j++) {
-            const int i = base + (j * 64 + lane) * 4;
-            if (base + j * 256 >= n) break;  // uniform
-            float amax = fmaxf(fmaxf(__builtin_fabsf(v[j].x), __builtin_fabsf(v[j].y)),
-                               fmaxf(__builtin_fabsf(v[j].z), __builtin_fabsf(v[j].w)));
+        for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+        if (amax < 1e-4f) amax = 1e-4f;
+        const int e = log2_ceil(amax / 448.0f);
+        // x / 2^e == x * 2^-e exactly (2^-e is a normal f32 here)
+        const float inv = __builtin_ldexpf(1.0f, -e), sc = __builtin_ldexpf(1.0f, e);
+        const float f[4] = {v.x, v.y, v.z, v.w};
+        uint32_t q[4];
 #pragma unroll
-            for (int off = 1; off < 8; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-            if (amax < 1e-4f) amax = 1e-4f;
-            const int e = log2_ceil(amax / 448.0f);
-            const float sc = __builtin_ldexpf(1.0f, e);
-            const float f[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-            uint32_t q[4];
+        for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] * inv, -448.0f, 448.0f));
+        if (blk >= b1) continue;
+        const int i = blk * 32 + (lane & 7) * 4;
+        if (EXACT) {
+            // exact: every value has at most 4 significant bits
+            const float d[4] = {e4m3_to_f32(q[0]) * sc, e4m3_to_f32(q[1]) * sc,
+                                e4m3_to_f32(q[2]) * sc, e4m3_to_f32(q[3]) * sc};
+            *(uint2 *)(x_l + i) =
+                uint2{(__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xFFFF0000u),
+                      (__float_as_uint(d[2]) >> 16) | (__float_as_uint(d[3]) & 0xFFFF0000u)};
+        } else {
+            *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+            if ((lane & 7) == 0) xs_l[blk] = (uint8_t)(e + 127);
+        }
+    }
+}
+
+// e4m3 token bytes [c0, c1) (16-byte multiples): 16 bytes per lane and round.
+__device__ __forceinline__ void tok_load_fp8(TokenRegs &tr, const uint8_t *q, const uint8_t *s,
+                                             int c0, int c1, int lane) {
 #pragma unroll
-            for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] / sc, -448.0f, 448.0f));
-            if (EXACT) {
-                u32x4v o;
-                const float d[4] = {e4m3_to_f32(q[0]) * sc, e4m3_to_f32(q[1]) * sc,
-                                    e4m3_to_f32(q[2]) * sc, e4m3_to_f32(q[3]) * sc};
-                // exact: every value has at most 4 significant bits
-                *(uint2 *)(x_l + i) = uint2{(__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xFFFF0000u),
-                                            (__float_as_uint(d[2]) >> 16) | (__float_as_uint(d[3]) & 0xFFFF0000u)};
-                (void)o;
-            } else {
-                *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-                if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)(e + 127);
+    for (int j = 0; j < kXRQ; j++) {
+        const int i = max(min(c0 + j * 1024 + lane * 16, c1 - 16), 0);
+        tr.q[j] = *(const uint4 *)(q + i);
+        tr.s[j] = s[i / 32];
+    }
+}
+
+template <bool EXACT>
+__device__ __forceinline__ void tok_store_fp8(const TokenRegs &tr, int c0, int c1, int lane,
+                                              __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l) {
+#pragma unroll
+    for (int j = 0; j < kXRQ; j++) {
+        const int i = c0 + j * 1024 + lane * 16;
+        if (i >= c1) continue;
+        if (EXACT) {
+            const float f = e8m0_to_f32(tr.s[j]);
+            const uint32_t wd[4] = {tr.q[j].x, tr.q[j].y, tr.q[j].z, tr.q[j].w};
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                u32x4v o = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, false),
+                               __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, true),
+                               __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, false),
+                               __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, true));
+                *(u32x4v *)(x_l + i + 8 * c) = o;
             }
+        } else {
+            *(uint4 *)(xq_l + i) = tr.q[j];
+            if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)tr.s[j];
         }
     }
 }
@@ -210,11 +294,12 @@ __device__ __forceinline__ void helper_fp8_to_lds(const uint8_t *q, const uint8_
 
 template <bool EXACT, bool XF32>
 __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
-    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs, const float *__restrict__ xf,
+    const uint8_t *xq, const uint8_t *xs, const float *xf,
     const int32_t *__restrict__ idx, const float *__restrict__ topk_w,
     const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
-    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
+    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit,
+    int tpw) {
     extern __shared__ __align__(16) uint8_t lds[];
     // EXACT: bf16 token (2*dim bytes); native: e4m3 token + scales
     __bf16 *x_l = (__bf16 *)lds;
@@ -224,46 +309,58 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const int slot = blockIdx.y;
     const int e = idx[slot];
     if (e < 0 || e >= n_experts) return;  // whole workgroup
-    const int tile = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int ksteps = dim / 128;
 
-    // streaming waves -> (matrix, 16-row half of the 32-row tile, K half);
-    // the last wave prepares the token in LDS
-    const int mat = (w >> 1) & 1, half = w & 1, kpart = w >> 2;
-    Fp4Band band{nullptr, nullptr, 0};
+    // waves -> (matrix, 16-row half of a 32-row tile, sub): with tpw == 2
+    // the workgroup owns tiles 2x, 2x+1 and `sub` picks the tile (a wave
+    // streams the whole K); with tpw == 1 it owns tile x and `sub` picks the
+    // K half. Every wave also converts 1/8 of the token into LDS.
+    const int mat = (w >> 1) & 1, half = w & 1, sub = w >> 2;
+    const int kparts = tpw == 2 ? 1 : kGluKParts;
+    // token share: blocks [tb0, tb1) (f32) or bytes [tc0, tc1) (e4m3)
+    const int nblk = dim / 32;
+    const int tb0 = w * nblk / kGluStreamWaves, tb1 = (w + 1) * nblk / kGluStreamWaves;
+    const int tc0 = tb0 * 32, tc1 = tb1 * 32;
+    TokenRegs tr;
+    if (XF32) tok_load_f32(tr, xf, tb0, tb1, lane);
+    else tok_load_fp8(tr, xq, xs, tc0, tc1, lane);
+    mem_order();
+
+    const int tile = blockIdx.x * tpw + (tpw == 2 ? sub : 0);
+    int k0, k1;
+    k_part(ksteps, tpw == 2 ? 0 : sub, kparts, k0, k1);
+    const size_t wmat = (size_t)inter * (dim / 2);
+    const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
+    const Fp4Band band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat,
+                                  (mat ? s3 : s1) + (size_t)e * smat, tile * 2 + half, dim, lane);
     Fp4Stage st0, st1;
-    int k0 = 0, k1 = 0;
-    if (w < kGluStreamWaves) {
-        k_part(ksteps, kpart, kGluKParts, k0, k1);
-        const size_t wmat = (size_t)inter * (dim / 2);
-        const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
-        band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat, (mat ? s3 : s1) + (size_t)e * smat,
-                        tile * 2 + half, dim, lane);
-        fp4_load(st0, band, k0, k1);
-        fp4_load(st1, band, k0 + kU, k1);
-    } else {
-        if (XF32) helper_quant_x<EXACT>(xf, dim, x_l, xq_l, xs_l, lane);
-        else helper_fp8_to_lds<EXACT>(xq, xs, dim, x_l, xq_l, xs_l, 0, 1, lane);
-    }
+    fp4_load(st0, band, k0, k1);
+    mem_order();
+    fp4_load(st1, band, k0 + kU, k1);
+    mem_order();
+
+    if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
+    else tok_store_fp8<EXACT>(tr, tc0, tc1, lane, x_l, xq_l, xs_l);
     lds_barrier();
 
-    if (w < kGluStreamWaves) {
+    {
         v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1);
         // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
         if ((lane & 15) == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; v++) gu[kpart][mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
+            for (int v = 0; v < 4; v++) gu[sub][mat][half * 16 + 4 * (lane >> 4) + v] = acc[v];
         }
     }
     __syncthreads();
-    if (w != 0) return;
-    // lanes 0-31 own the tile's 32 values; lanes 32-63 mirror them so the
-    // half-wave reduction stays uniform, and do not store
+    if (w >= tpw) return;
+    // wave w finishes tile blockIdx.x * tpw + w; lanes 0-31 own its 32 values,
+    // lanes 32-63 mirror them so the half-wave reduction stays uniform, and do
+    // not store. K halves (tpw == 1) are added in fixed order.
+    const int otile = blockIdx.x * tpw + w;
     const int n = lane & 31;
-    float g = gu[0][0][n], u = gu[0][1][n];
-#pragma unroll
-    for (int q = 1; q < kGluKParts; q++) {
+    float g = gu[w][0][n], u = gu[w][1][n];
+    for (int q = 1; q < kparts; q++) {
         g = g + gu[q][0][n];
         u = u + gu[q][1][n];
     }
@@ -277,8 +374,8 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     uint32_t qb = quant_fp8_block32(h, &sb);
     if (lane < 32) {
         const int rank = pick_rank(idx, top_k, n_experts, slot);
-        hq[(size_t)rank * inter + tile * 32 + n] = (uint8_t)qb;
-        if (n == 0) hs[(size_t)rank * (inter / 32) + tile] = (uint8_t)sb;
+        hq[(size_t)rank * inter + otile * 32 + n] = (uint8_t)qb;
+        if (n == 0) hs[(size_t)rank * (inter / 32) + otile] = (uint8_t)sb;
     }
 }
 
@@ -370,7 +467,8 @@ static int check_decode_shapes(int64_t dim, int64_t inter, int64_t n_experts, in
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || top_k > kMaxTopkDec) return WS_ERR_SHAPE;
     // LDS holds the token and the picks as bf16 (2 bytes per value)
-    if (dim > 32768 || top_k * inter > 32768 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
+    // the gate/up kernel holds a wave's share of the token in registers
+    if (dim > kMaxDimFp8 || top_k * inter > 32768 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
     return WS_OK;
 }
 
@@ -391,13 +489,16 @@ static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf,
                       const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, uint8_t *hq,
                       uint8_t *hs, int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
                       float swiglu_limit, hipStream_t stream) {
-    dim3 grid((unsigned)(inter / 32), (unsigned)top_k);
+    // two tiles per workgroup when that still gives every CU a workgroup:
+    // one resident round of 9-wave workgroups, each wave streaming whole K rows
+    const int tpw = (inter / 32) * top_k >= 512 ? 2 : 1;
+    dim3 grid((unsigned)(inter / 32 / tpw), (unsigned)top_k);
     const bool exact = math_mode() == WS_MATH_EXACT;
     size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
 #define WS_GLU(EX, XF)                                                                        \
     hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF>), grid, dim3(kDecThreads), lds, stream, \
                        xq, xs, xf, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim,         \
-                       (int)inter, (int)n_experts, (int)top_k, swiglu_limit)
+                       (int)inter, (int)n_experts, (int)top_k, swiglu_limit, tpw)
     if (exact) {
         if (xf) WS_GLU(true, true); else WS_GLU(true, false);
     } else {
@@ -438,8 +539,8 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
         return WS_ERR_INVALID_ARG;
     int rc = check_decode_shapes(dim, inter, n_experts, top_k);
     if (rc) return rc;
-    if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 3) ||
-        ((uintptr_t)s3 & 3))
+    if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
+        ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
     return glu_launch(xq, xs, nullptr, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
                       n_experts, top_k, swiglu_limit, stream);
@@ -454,8 +555,9 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
         return WS_ERR_INVALID_ARG;
     int rc = check_decode_shapes(dim, inter, n_experts, top_k);
     if (rc) return rc;
-    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 3) ||
-        ((uintptr_t)s3 & 3))
+    if (dim > kMaxDimF32) return WS_ERR_SHAPE;
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
+        ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
     return glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
                       n_experts, top_k, swiglu_limit, stream);
@@ -467,7 +569,7 @@ int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_i
     if (!hq || !hs || !topk_idx || !w2 || !s2 || !y) return WS_ERR_INVALID_ARG;
     int rc = check_decode_shapes(dim, inter, n_experts, top_k);
     if (rc) return rc;
-    if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 3)) return WS_ERR_INVALID_ARG;
+    if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 7)) return WS_ERR_INVALID_ARG;
     return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
 }
 
@@ -475,7 +577,10 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 size_t ws_moe_decode_workspace_size(int64_t dim, int64_t inter, int64_t top_k) {
     if (dim <= 0 || inter <= 0 || top_k <= 0) return 0;
-    return align256(top_k * inter) + align256(top_k * (inter / 32));
+    // hq, hs; for dim > kMaxDimF32 also the e4m3 token and its scales
+    size_t n = align256(top_k * inter) + align256(top_k * (inter / 32));
+    if (dim > kMaxDimF32) n += align256(dim) + align256(dim / 32);
+    return n;
 }
 
 int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, const uint8_t *w1,
@@ -489,14 +594,23 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, 
     if (workspace_bytes < ws_moe_decode_workspace_size(dim, inter, top_k) || !aligned16(workspace))
         return WS_ERR_INVALID_ARG;
     if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || !aligned16(w2) ||
-        ((uintptr_t)s1 & 3) || ((uintptr_t)s3 & 3) || ((uintptr_t)s2 & 3) || !topk_idx ||
+        ((uintptr_t)s1 & 7) || ((uintptr_t)s3 & 7) || ((uintptr_t)s2 & 7) || !topk_idx ||
         !topk_w || !w1 || !s1 || !w3 || !s3 || !w2 || !s2 || !y)
         return WS_ERR_INVALID_ARG;
-    // the gate/up kernel quantises x itself (the act_quant_fp8_emit rule)
     uint8_t *hq = (uint8_t *)workspace;
     uint8_t *hs = hq + align256(top_k * inter);
-    rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                    n_experts, top_k, swiglu_limit, stream);
+    if (dim <= kMaxDimF32) {
+        // the gate/up kernel quantises x itself (the act_quant_fp8_emit rule)
+        rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                        n_experts, top_k, swiglu_limit, stream);
+    } else {
+        uint8_t *xq = hs + align256(top_k * (inter / 32));
+        uint8_t *xs = xq + align256(dim);
+        rc = ws_emit8(x, xq, xs, dim, stream);
+        if (rc) return rc;
+        rc = glu_launch(xq, xs, nullptr, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
+                        n_experts, top_k, swiglu_limit, stream);
+    }
     if (rc) return rc;
     return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
 }

@@ -44,16 +44,18 @@ struct Fp4Stage {
     uint2 s;  // scale bytes of the kU steps
 };
 
-// Steps [ks0, ks0 + kU) of the band; steps past `kend` re-load step kend-1
-// (never used), keeping the loads unconditional so that one counter wait
-// covers a whole stage. ks0 % 8 == 0.
+// Steps [ks0, ks0 + kU) of the band; steps at or past `kend` re-load step
+// max(kend - 1, 0) (never used), keeping the loads unconditional so that one
+// counter wait covers a whole stage. An empty range (kend == 0, or a stage past
+// the end) thus still reads inside the band. ks0 % 8 == 0, kend <= ks_total.
 __device__ __forceinline__ void fp4_load(Fp4Stage &st, const Fp4Band &b, int ks0, int kend) {
+    const int last = kend > 0 ? kend - 1 : 0;
 #pragma unroll
     for (int u = 0; u < kU; u++) {
-        int ks = min(ks0 + u, kend - 1);
+        int ks = min(ks0 + u, last);
         st.w[u] = ldg16_stream(b.w + (size_t)ks * 1024);
     }
-    st.s = *(const uint2 *)(b.s + (size_t)(ks0 / 8) * 512);
+    st.s = *(const uint2 *)(b.s + (size_t)(min(ks0, last) / 8) * 512);
 }
 
 __device__ __forceinline__ uint32_t stage_scale(const Fp4Stage &st, int u) {
