@@ -20,7 +20,9 @@ def _init():
 
 def test_device_expf_equals_glibc_on_every_input():
     """All 2^32 inputs: the device digest equals glibc's, and 2^24 inputs
-    spread over the whole range are compared value by value."""
+    spread over the whole range are compared value by value. The probe also
+    evaluates the lane-table variant used by the routing kernels and marks
+    any input where the two differ."""
     lib = L._lib.load()
     chunk = 1 << 28
     out = torch.empty(chunk, dtype=torch.int32, device=DEV)
@@ -30,6 +32,8 @@ def test_device_expf_equals_glibc_on_every_input():
         announce("expf probe chunk %d" % c)
         L._lib.check("ws_expf_probe", lib.ws_expf_probe(lo, chunk, out.data_ptr(),
                                                          torch.cuda.current_stream().cuda_stream))
+        # the lane-table variant (routing kernels) agrees with ws_expf
+        assert int((out == 0x7FBADBAD).sum().item()) == 0
         r = out.to(torch.int64) & 0xFFFFFFFF
         # canonical NaN, as the host digest does
         nan = ((r & 0x7F800000) == 0x7F800000) & ((r & 0x7FFFFF) != 0)
@@ -80,6 +84,11 @@ def _rows_with_ties(rng, m, E, score_func):
     bias[5] = np.float32(s0[9] + bias[9] - s0[5])
     logits[1, 40] = logits[1, 41]                  # equal logits, equal scores
     bias[40] = bias[41]
+    if E > 71:
+        # row 2: four exact ties at the very top, on different lanes (10, 20)
+        # and on one lane (7, 71 = 7 + 64): picked by ascending index
+        logits[2, [7, 10, 20, 71]] = 6.0
+        bias[[7, 10, 20, 71]] = 0.25
     return logits, bias
 
 
@@ -96,6 +105,8 @@ def test_topk_bit_exact(score_func, E, k):
     sc = torch.empty((m, E), dtype=torch.float32, device=DEV)
     L.moe_topk(dev(logits), dev(bias), sc, idx, w, m, E, k, score_func, temp, True, rscale)
     gi, gw, gs = host(idx), host(w), host(sc)
+    if E > 71 and score_func == O.SCORE_SIGMOID:
+        assert list(gi[2][:4]) == [7, 10, 20, 71][:k]
     for r in range(m):
         s = O.score(logits[r], score_func, temp)
         assert np.array_equal(gs[r].view(np.uint32), s.view(np.uint32))

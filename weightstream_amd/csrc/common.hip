@@ -119,11 +119,14 @@ __global__ __launch_bounds__(256) void weight_quant_fp8_kernel(const float *w, u
     if (t == 0) s[(size_t)rb * (cols / 32) + cb] = (uint8_t)(e + 127);
 }
 
+// ws_expf on inputs lo .. lo+n-1; the lane-table variant (ws_expf_lanes) is
+// evaluated beside it and any difference is reported as 0x7fbadbad.
 __global__ __launch_bounds__(256) void expf_probe_kernel(uint32_t lo, uint32_t n, uint32_t *out) {
-    uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    float r = ws_expf(__uint_as_float(lo + i));
-    out[i] = __float_as_uint(r);
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const float x = __uint_as_float(lo + min(i, n - 1));
+    const uint32_t a = __float_as_uint(ws_expf(x));
+    const uint32_t b = __float_as_uint(ws_expf_lanes(x, ws_lane_exp2f_tab(threadIdx.x & 63)));
+    if (i < n) out[i] = a == b ? a : 0x7fbadbadu;
 }
 
 // ---- swiglu_limit10 (moe.cu:143), elementwise in moe.rs:187-201 order ----

@@ -24,8 +24,8 @@
 //    epilogue applies SwiGLU x routing weight and quantises each 32-value
 //    tile (one FP8 1x32 block) straight to e4m3 + UE8M0.
 //  reduce: grid (dim/16), 8 streaming waves over (expert, K part) units for
-//    16 output rows + 2 helper waves that decode the picks' hidden states
-//    into LDS; per-expert results meet in LDS and are added in ascending
+//    16 output rows; each also decodes 1/8 of the picks' hidden states into
+//    LDS; per-expert results meet in LDS and are added in ascending
 //    expert id, one f32 add per expert like the reference's acc_f32 chain.
 #include "ws_internal.hpp"
 #include "ws_pack.hpp"
@@ -36,29 +36,45 @@ constexpr int kGluKParts = 2;       // glu: (w1|w3) x (rows 0-15|16-31) x K half
 constexpr int kGluStreamWaves = 4 * kGluKParts;
 constexpr int kDecThreads = 64 * kGluStreamWaves;
 constexpr int kRedWaves = 8;        // reduce: 8 streaming waves over (expert, K part) units
-constexpr int kRedHelpers = 2;      // + 2 helper waves preparing the picks in LDS
-constexpr int kRedThreads = 64 * (kRedWaves + kRedHelpers);
+constexpr int kRedThreads = 64 * kRedWaves;
 constexpr int kMaxTopkDec = 16;
+constexpr int kMaxPickBytes = 32768;  // top_k * inter: the picks in LDS as bf16
+constexpr int kRedShareRounds = kMaxPickBytes / kRedWaves / 1024;
 
-// rank of pick `slot` among valid picks ordered by (expert id, slot)
-__device__ __forceinline__ int pick_rank(const int32_t *idx, int top_k, int n_experts, int slot) {
-    int e = idx[slot];
+// The picks as the whole wave sees them: lane j < top_k holds pick j (its
+// expert id and its rank among the valid picks ordered by (expert id, slot)).
+// One vector load and top_k lane reads; no memory round trip per pick.
+struct WavePicks {
+    int e;     // expert id of the lane's pick (-1 for lanes >= top_k)
+    int rank;  // rank of the lane's pick, -1 if invalid (outside [0, E))
+    int nv;    // number of valid picks
+};
+
+__device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, int n_experts,
+                                                int lane) {
+    WavePicks wp;
+    wp.e = lane < top_k ? idx[lane] : -1;
+    const bool valid = lane < top_k && wp.e >= 0 && wp.e < n_experts;
     int rank = 0;
-    for (int j = 0; j < top_k; j++) {
-        int f = idx[j];
-        if (f < 0 || f >= n_experts) continue;
-        if (f < e || (f == e && j < slot)) rank++;
+    for (int i = 0; i < top_k; i++) {
+        const int ei = __builtin_amdgcn_readlane(wp.e, i);
+        const bool vi = ei >= 0 && ei < n_experts;
+        rank += (vi && (ei < wp.e || (ei == wp.e && i < lane))) ? 1 : 0;
     }
-    return rank;
+    wp.rank = valid ? rank : -1;
+    wp.nv = __popcll(__ballot(valid));
+    return wp;
 }
 
-// expert id of the pick with rank p (ascending expert id, then slot)
-__device__ __forceinline__ int expert_of_rank(const int32_t *idx, int top_k, int n_experts, int p) {
-    for (int sidx = 0; sidx < top_k; sidx++) {
-        int e = idx[sidx];
-        if (e >= 0 && e < n_experts && pick_rank(idx, top_k, n_experts, sidx) == p) return e;
-    }
-    return 0;
+// expert id of the valid pick with rank p (0 if there is none)
+__device__ __forceinline__ int wave_expert_of_rank(const WavePicks &wp, int p) {
+    const unsigned long long m = __ballot(wp.rank == p);
+    return m ? __builtin_amdgcn_readlane(wp.e, __ffsll((long long)m) - 1) : 0;
+}
+
+// rank of pick `slot` (uniform)
+__device__ __forceinline__ int wave_rank_of_slot(const WavePicks &wp, int slot) {
+    return __builtin_amdgcn_readlane(wp.rank, slot);
 }
 
 // Multiply one register stage of a packed 16-row FP4 band with the operand in
@@ -129,11 +145,11 @@ __device__ __forceinline__ void k_part(int ksteps, int part, int parts, int &k0,
     k1 = min(ksteps, (part + 1) * stages / parts * kU);
 }
 
-// ---- LDS preparation by helper waves -------------------------------------
-// A helper wave fills LDS with the operand every streaming wave multiplies
-// (the token, or the picks' hidden states). Streaming waves issue their weight
-// loads first and meet the helper at an LDS-only barrier, so their loads stay
-// in flight while the helper works (load counters are per wave).
+// ---- operand preparation in LDS ------------------------------------------
+// Every streaming wave converts a share of the operand all waves multiply (the
+// token, or the picks' hidden states) into LDS. It issues the share's loads
+// before its weight loads, converts while the weight stages are in flight,
+// and the waves meet at an LDS-only barrier that leaves those loads in flight.
 
 // Compiler-only barrier: memory accesses are not moved across it, so loads
 // issued before it leave the wave first (load counters then return them in
@@ -147,8 +163,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-constexpr int kHelperRounds = 16;  // 16-byte loads per lane and batch
-
 // ---- the token, split over the streaming waves ----------------------------
 // Each of the `parts` streaming waves converts its share of the token into
 // LDS. It issues the share's loads before its weight loads (loads return in
@@ -160,10 +174,16 @@ constexpr int kXRF = 4, kXRQ = 2;
 constexpr int kMaxDimF32 = kGluStreamWaves * kXRF * 256;
 constexpr int kMaxDimFp8 = kGluStreamWaves * kXRQ * 1024;
 
+// e4m3 bytes + their UE8M0 scale bytes, 16 bytes per lane and round
+template <int R>
+struct Fp8Share {
+    uint4 q[R];
+    uint32_t s[R];
+};
+
 struct TokenRegs {
     float4 f[kXRF];   // f32 token: 4 values of one 1x32 block per lane and round
-    uint4 q[kXRQ];    // e4m3 token: 16 bytes per lane and round
-    uint32_t s[kXRQ];
+    Fp8Share<kXRQ> b; // e4m3 token
 };
 
 // f32 token, blocks [b0, b1) of 32 values: round r covers 8 blocks, a block
@@ -216,22 +236,25 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
     }
 }
 
-// e4m3 token bytes [c0, c1) (16-byte multiples): 16 bytes per lane and round.
-__device__ __forceinline__ void tok_load_fp8(TokenRegs &tr, const uint8_t *q, const uint8_t *s,
-                                             int c0, int c1, int lane) {
+// e4m3 bytes [c0, c1) (16-byte multiples, c1 - c0 <= R KB) with one scale
+// byte per 32: 16 bytes per lane and round.
+template <int R>
+__device__ __forceinline__ void share_load_fp8(Fp8Share<R> &tr, const uint8_t *q, const uint8_t *s,
+                                               int c0, int c1, int lane) {
 #pragma unroll
-    for (int j = 0; j < kXRQ; j++) {
+    for (int j = 0; j < R; j++) {
         const int i = max(min(c0 + j * 1024 + lane * 16, c1 - 16), 0);
         tr.q[j] = *(const uint4 *)(q + i);
         tr.s[j] = s[i / 32];
     }
 }
 
-template <bool EXACT>
-__device__ __forceinline__ void tok_store_fp8(const TokenRegs &tr, int c0, int c1, int lane,
-                                              __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l) {
+// ... into LDS: exact bf16 values (EXACT) or the bytes and scales as they are
+template <bool EXACT, int R>
+__device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, int c1, int lane,
+                                                __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l) {
 #pragma unroll
-    for (int j = 0; j < kXRQ; j++) {
+    for (int j = 0; j < R; j++) {
         const int i = c0 + j * 1024 + lane * 16;
         if (i >= c1) continue;
         if (EXACT) {
@@ -248,46 +271,6 @@ __device__ __forceinline__ void tok_store_fp8(const TokenRegs &tr, int c0, int c
         } else {
             *(uint4 *)(xq_l + i) = tr.q[j];
             if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)tr.s[j];
-        }
-    }
-}
-
-// n e4m3 bytes + UE8M0 scales -> exact bf16 values in LDS (EXACT) or a plain
-// byte copy (native); `hw` helper waves, helper index `hi`.
-template <bool EXACT>
-__device__ __forceinline__ void helper_fp8_to_lds(const uint8_t *q, const uint8_t *s, int n,
-                                                  __bf16 *dst, uint8_t *q_l, uint8_t *s_l, int hi,
-                                                  int hw, int lane) {
-    const int stride = hw * 64 * 16;
-    for (int base = hi * 64 * 16; base < n; base += kHelperRounds * stride) {
-        uint4 v[kHelperRounds];
-        uint32_t sc[kHelperRounds];
-#pragma unroll
-        for (int j = 0; j < kHelperRounds; j++) {
-            const int i = min(base + j * stride + lane * 16, n - 16);
-            v[j] = *(const uint4 *)(q + i);
-            sc[j] = s[i / 32];
-        }
-#pragma unroll
-        for (int j = 0; j < kHelperRounds; j++) {
-            const int i = base + j * stride + lane * 16;
-            if (base + j * stride >= n) break;  // uniform: n % (64*16) == 0 not assumed below
-            if (i >= n) continue;
-            if (EXACT) {
-                const float f = e8m0_to_f32(sc[j]);
-                const uint32_t wd[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
-#pragma unroll
-                for (int c = 0; c < 2; c++) {
-                    u32x4v o = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, false),
-                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c], f, true),
-                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, false),
-                                   __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wd[2 * c + 1], f, true));
-                    *(u32x4v *)(dst + i + 8 * c) = o;
-                }
-            } else {
-                *(uint4 *)(q_l + i) = v[j];
-                if ((i & 31) == 0) s_l[i / 32] = (uint8_t)sc[j];
-            }
         }
     }
 }
@@ -324,7 +307,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const int tc0 = tb0 * 32, tc1 = tb1 * 32;
     TokenRegs tr;
     if (XF32) tok_load_f32(tr, xf, tb0, tb1, lane);
-    else tok_load_fp8(tr, xq, xs, tc0, tc1, lane);
+    else share_load_fp8(tr.b, xq, xs, tc0, tc1, lane);
     mem_order();
 
     const int tile = blockIdx.x * tpw + (tpw == 2 ? sub : 0);
@@ -341,7 +324,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     mem_order();
 
     if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
-    else tok_store_fp8<EXACT>(tr, tc0, tc1, lane, x_l, xq_l, xs_l);
+    else share_store_fp8<EXACT>(tr.b, tc0, tc1, lane, x_l, xq_l, xs_l);
     lds_barrier();
 
     {
@@ -372,8 +355,8 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     float h = ws_silu(g) * u * rw;
     uint32_t sb;
     uint32_t qb = quant_fp8_block32(h, &sb);
+    const int rank = wave_rank_of_slot(wave_picks(idx, top_k, n_experts, lane), slot);
     if (lane < 32) {
-        const int rank = pick_rank(idx, top_k, n_experts, slot);
         hq[(size_t)rank * inter + otile * 32 + n] = (uint8_t)qb;
         if (n == 0) hs[(size_t)rank * (inter / 32) + otile] = (uint8_t)sb;
     }
@@ -381,7 +364,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
 
 template <bool EXACT>
 __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
-    const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs, const int32_t *__restrict__ idx,
+    const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ idx,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
     int inter, int n_experts, int top_k) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -389,13 +372,20 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int row0 = blockIdx.x * 16;
     // every wave ranks the (<= 16) picks itself: no barrier before the loads
-    int nv = 0;
-    for (int sidx = 0; sidx < top_k; sidx++) {
-        int e = idx[sidx];
-        nv += (e >= 0 && e < n_experts);
-    }
+    const WavePicks wp = wave_picks(idx, top_k, n_experts, lane);
+    const int nv = wp.nv;
+    // the picks' hidden states (nv rows of inter e4m3 bytes, ascending expert
+    // id): every wave converts 1/8 of them into LDS; their loads go first
+    const int tot = nv * inter;
+    const int c0 = w * (tot / kRedWaves), c1 = c0 + tot / kRedWaves;
+    Fp8Share<kRedShareRounds> hr;
+    share_load_fp8(hr, hq, hs, c0, c1, lane);
+    mem_order();
+
     // work units (pick, K part): a wave streams 16 rows of one expert's w2
-    // over 1/ksplit of inter; with 8 picks every wave owns one whole expert
+    // over 1/ksplit of inter; with 8 picks every wave owns one whole expert.
+    // A wave without a unit streams nothing (its clamped loads re-read one
+    // 1 KB step).
     const int ksteps = inter / 128;
     int ksplit = kRedWaves / (nv > 0 ? nv : 1);
     ksplit = ksplit < 1 ? 1 : ksplit;
@@ -404,50 +394,49 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int nunits = nv * ksplit;
     const size_t wmat = (size_t)dim * (inter / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
+    const bool has = w < nunits;
+    int p = has ? w / ksplit : 0, ksp = has ? w % ksplit : 0, k0 = 0, k1 = 0;
+    if (has) k_part(ksteps, ksp, ksplit, k0, k1);
+    const int e0 = wave_expert_of_rank(wp, p);
+    Fp4Band band = fp4_band(w2 + (size_t)e0 * wmat, s2 + (size_t)e0 * smat, blockIdx.x, inter,
+                            lane);
+    Fp4Stage s0, s1;
+    fp4_load(s0, band, k0, k1);
+    mem_order();
+    fp4_load(s1, band, k0 + kU, k1);
+    mem_order();
 
     // EXACT: picks as bf16 (2 * top_k * inter bytes); native: e4m3 + scales
     __bf16 *h_l = (__bf16 *)lds;
     uint8_t *hq_l = lds;
     uint8_t *hs_l = lds + (size_t)top_k * inter;
-
-    Fp4Band band{nullptr, nullptr, 0};
-    Fp4Stage s0, s1;
-    int unit = w, p = 0, ksp = 0, k0 = 0, k1 = 0;
-    if (w < kRedWaves) {
-        if (unit < nunits) {
-            p = unit / ksplit;
-            ksp = unit % ksplit;
-            k_part(ksteps, ksp, ksplit, k0, k1);
-            const int e = expert_of_rank(idx, top_k, n_experts, p);
-            band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter, lane);
-            fp4_load(s0, band, k0, k1);
-            fp4_load(s1, band, k0 + kU, k1);
-        }
-    } else {
-        helper_fp8_to_lds<EXACT>(hq, hs, nv * inter, h_l, hq_l, hs_l, w - kRedWaves,
-                                 kRedHelpers, lane);
-    }
+    share_store_fp8<EXACT>(hr, c0, c1, lane, h_l, hq_l, hs_l);
     lds_barrier();
 
-    if (w < kRedWaves) {
-        for (; unit < nunits; unit += kRedWaves) {
-            if (unit != w) {  // further units (fewer waves than units)
-                p = unit / ksplit;
-                ksp = unit % ksplit;
-                k_part(ksteps, ksp, ksplit, k0, k1);
-                const int e = expert_of_rank(idx, top_k, n_experts, p);
-                band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter,
-                                lane);
-                fp4_load(s0, band, k0, k1);
-                fp4_load(s1, band, k0 + kU, k1);
-            }
-            v4f acc = fp4_stream<EXACT>(band, s0, s1, hq_l + (size_t)p * inter,
-                                        hs_l + (size_t)p * (inter / 32), h_l + (size_t)p * inter,
-                                        lane >> 4, k0, k1);
-            if ((lane & 15) == 0) {
+    if (has) {
+        v4f acc = fp4_stream<EXACT>(band, s0, s1, hq_l + (size_t)p * inter,
+                                    hs_l + (size_t)p * (inter / 32), h_l + (size_t)p * inter,
+                                    lane >> 4, k0, k1);
+        if ((lane & 15) == 0) {
 #pragma unroll
-                for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
-            }
+            for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
+        }
+    }
+    // more units than waves (more than 8 picks)
+    for (int unit = w + kRedWaves; unit < nunits; unit += kRedWaves) {
+        p = unit / ksplit;
+        ksp = unit % ksplit;
+        k_part(ksteps, ksp, ksplit, k0, k1);
+        const int e = wave_expert_of_rank(wp, p);
+        band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter, lane);
+        fp4_load(s0, band, k0, k1);
+        fp4_load(s1, band, k0 + kU, k1);
+        v4f acc = fp4_stream<EXACT>(band, s0, s1, hq_l + (size_t)p * inter,
+                                    hs_l + (size_t)p * (inter / 32), h_l + (size_t)p * inter,
+                                    lane >> 4, k0, k1);
+        if ((lane & 15) == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) part[p][ksp][4 * (lane >> 4) + v] = acc[v];
         }
     }
     __syncthreads();
@@ -468,7 +457,7 @@ static int check_decode_shapes(int64_t dim, int64_t inter, int64_t n_experts, in
     if (dim % 128 || inter % 128 || top_k > kMaxTopkDec) return WS_ERR_SHAPE;
     // LDS holds the token and the picks as bf16 (2 bytes per value)
     // the gate/up kernel holds a wave's share of the token in registers
-    if (dim > kMaxDimFp8 || top_k * inter > 32768 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
+    if (dim > kMaxDimFp8 || top_k * inter > kMaxPickBytes || n_experts > (1 << 20)) return WS_ERR_SHAPE;
     return WS_OK;
 }
 

@@ -101,78 +101,151 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return v;
 }
 
-// One wave per token row: scores, top-k selection, weights. Each lane keeps
-// CPL candidates (expert e = lane + 64 c) as 64-bit keys (total-order key of
-// score+bias, then the complemented index so that ties pick the lower index);
-// a round is a lane-local max and a 6-step wave max, with no barrier.
+// Wave max with DPP lane moves (no LDS permutes): quad swaps, half-row and
+// row mirrors, then row broadcasts 15 and 31 carry the maximum to lane 63.
+#define WS_DPP_MAX(v, ctrl, rmask)                                                           \
+    do {                                                                                    \
+        uint32_t o_ = (uint32_t)__builtin_amdgcn_update_dpp((int)(v), (int)(v), ctrl, rmask, \
+                                                            0xf, false);                    \
+        v = o_ > v ? o_ : v;                                                                \
+    } while (0)
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    WS_DPP_MAX(v, 0xB1, 0xf);   // quad_perm [1,0,3,2]
+    WS_DPP_MAX(v, 0x4E, 0xf);   // quad_perm [2,3,0,1]
+    WS_DPP_MAX(v, 0x141, 0xf);  // row_half_mirror
+    WS_DPP_MAX(v, 0x140, 0xf);  // row_mirror
+    WS_DPP_MAX(v, 0x142, 0xa);  // row_bcast:15 -> rows 1, 3
+    WS_DPP_MAX(v, 0x143, 0xc);  // row_bcast:31 -> rows 2, 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+#undef WS_DPP_MAX
+
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// One wave per token row: scores, top-k selection, weights, all in registers.
+// Each lane keeps CPL candidates (expert e = lane + 64 c) as 64-bit keys
+// (total-order key of score+bias, then the complemented index so that ties
+// pick the lower index). A round takes each lane's best key, a 32-bit wave
+// max of the score halves and a ballot; only an exact score tie across lanes
+// needs the 64-bit wave max. Lane k keeps pick k and its score.
 template <int CPL>
 __global__ __launch_bounds__(64) void topk_kernel(
     const float *__restrict__ logits, const float *__restrict__ bias, float *__restrict__ scores_out,
     int32_t *__restrict__ out_idx, float *__restrict__ out_w, int n_experts, int top_k,
     int score_func, float gate_temp, int norm, float route_scale) {
-    __shared__ float sc[kMaxExperts];
+    __shared__ float sm[kMaxExperts];
     __shared__ float ssum;
     const int m = blockIdx.x;
     const int lane = threadIdx.x;
     const float *lg = logits + (size_t)m * n_experts;
 
-    for (int e = lane; e < n_experts; e += 64) sc[e] = score_fn(lg[e], score_func, gate_temp);
+    float sc[CPL];
     if (score_func == WS_SCORE_SOFTMAX) {
         // num.rs:46-62: max, exp(x - max) in place with a sequential sum, divide
+        for (int e = lane; e < n_experts; e += 64) sm[e] = score_fn(lg[e], score_func, gate_temp);
         __syncthreads();
         if (lane == 0) {
             float mx = -__builtin_inff();
             for (int e = 0; e < n_experts; e++)
-                if (sc[e] > mx) mx = sc[e];
+                if (sm[e] > mx) mx = sm[e];
             float s = 0.0f;
             for (int e = 0; e < n_experts; e++) {
-                sc[e] = ws_expf(sc[e] - mx);
-                s = s + sc[e];
+                sm[e] = ws_expf(sm[e] - mx);
+                s = s + sm[e];
             }
             ssum = s;
         }
         __syncthreads();
         const float s = ssum;
-        for (int e = lane; e < n_experts; e += 64) sc[e] = sc[e] / s;
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+            const int e = lane + 64 * c;
+            sc[c] = e < n_experts ? sm[e] / s : 0.0f;
+        }
+    } else {
+        // logits, biases and the exp table all load at once
+        float v[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; c++) v[c] = lg[min(lane + 64 * c, n_experts - 1)];
+        const uint64_t tab = ws_lane_exp2f_tab(lane);
+        if (gate_temp != 1.0f) {
+#pragma unroll
+            for (int c = 0; c < CPL; c++) v[c] = v[c] / gate_temp;
+        }
+        // score_fn on the lane-table exp (no table loads per value)
+        if (score_func == WS_SCORE_SIGMOID) {
+#pragma unroll
+            for (int c = 0; c < CPL; c++) sc[c] = ws_sigmoid_lanes(v[c], tab);
+        } else if (score_func == WS_SCORE_SQRTSOFTPLUS) {
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const float ex = ws_expf_lanes(v[c], tab);
+                sc[c] = sqrtf(v[c] > 20.0f ? v[c] : logf(1.0f + ex));
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < CPL; c++) sc[c] = v[c];
+        }
     }
-    __syncthreads();
-    if (scores_out)
-        for (int e = lane; e < n_experts; e += 64) scores_out[(size_t)m * n_experts + e] = sc[e];
-
+    float bv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) bv[c] = bias[min(lane + 64 * c, n_experts - 1)];
     uint64_t cand[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
-        int e = lane + 64 * c;
+        const int e = lane + 64 * c;
+        if (scores_out && e < n_experts) scores_out[(size_t)m * n_experts + e] = sc[c];
         cand[c] = e < n_experts
-                      ? ((uint64_t)total_key_u(sc[e] + bias[e]) << 32) | (uint32_t)(~(uint32_t)e)
+                      ? ((uint64_t)total_key_u(sc[c] + bv[c]) << 32) | (uint32_t)(~(uint32_t)e)
                       : 0ull;
     }
-    int picked[kMaxTopk];
+    int my_pick = 0;
+    float my_w = 0.0f;
     for (int k = 0; k < top_k; k++) {
         uint64_t best = cand[0];
+        int bc = 0;
 #pragma unroll
-        for (int c = 1; c < CPL; c++) best = cand[c] > best ? cand[c] : best;
-        best = wave_max_u64(best);
-        const int e = (int)(~(uint32_t)best);
-        picked[k] = e;
+        for (int c = 1; c < CPL; c++)
+            if (cand[c] > best) {
+                best = cand[c];
+                bc = c;
+            }
+        const uint32_t hk = (uint32_t)(best >> 32);
+        const uint32_t wk = wave_max_u32(hk);
+        uint64_t bal = __ballot(hk == wk);
+        if (__popcll(bal) > 1) {
+            // equal scores on several lanes: the larger full key (lower index)
+            const uint64_t full = wave_max_u64(hk == wk ? best : 0ull);
+            bal = __ballot(hk == wk && best == full);
+        }
+        const int win = __ffsll((long long)bal) - 1;
+        float sb = sc[0];
+#pragma unroll
+        for (int c = 1; c < CPL; c++) sb = c == bc ? sc[c] : sb;
+        const int e = __builtin_amdgcn_readlane(lane + 64 * bc, win);
+        const float w = readlane_f(sb, win);
+        if (lane == k) {
+            my_pick = e;
+            my_w = w;
+        }
 #pragma unroll
         for (int c = 0; c < CPL; c++)
-            if (lane + 64 * c == e) cand[c] = 0ull;
+            if (lane == win && c == bc) cand[c] = 0ull;
     }
-    if (lane == 0) {
-        float w[kMaxTopk];
-        for (int k = 0; k < top_k; k++) w[k] = sc[picked[k]];
-        // norm 1: moe.rs:61 (only when top_k > 1); norm 2: moe_select's
-        // unconditional normalisation (moe.cu:84-88)
-        if ((norm == 1 && top_k > 1) || norm == 2) {
-            float s = -0.0f;
-            for (int k = 0; k < top_k; k++) s = s + w[k];
-            for (int k = 0; k < top_k; k++) w[k] = w[k] / (s + 1e-20f);
-        }
-        for (int k = 0; k < top_k; k++) {
-            out_idx[(size_t)m * top_k + k] = picked[k];
-            out_w[(size_t)m * top_k + k] = w[k] * route_scale;
-        }
+    // norm 1: moe.rs:61 (only when top_k > 1); norm 2: moe_select's
+    // unconditional normalisation (moe.cu:84-88). The sum runs in top-k order.
+    float wout = my_w;
+    if ((norm == 1 && top_k > 1) || norm == 2) {
+        float s = -0.0f;
+        for (int k = 0; k < top_k; k++) s = s + readlane_f(my_w, k);
+        wout = my_w / (s + 1e-20f);
+    }
+    if (lane < top_k) {
+        out_idx[(size_t)m * top_k + lane] = my_pick;
+        out_w[(size_t)m * top_k + lane] = wout * route_scale;
     }
 }
 

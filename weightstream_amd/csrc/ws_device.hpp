@@ -83,6 +83,30 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
     return (uint16_t)((bits + round) >> 16);
 }
 
+// ws_expf with the 32-entry table held in lane registers: lane l holds
+// ws_exp2f_tab[l % 32] (ws_lane_exp2f_tab) and the entry is fetched with a
+// lane permute instead of a memory load. Same arithmetic as ws_expf. Every
+// lane of the wave must take part.
+__device__ __forceinline__ uint64_t ws_lane_exp2f_tab(int lane) { return ws_exp2f_tab[lane & 31]; }
+
+__device__ __forceinline__ float ws_expf_lanes(float x, uint64_t tab) {
+    uint64_t ki = 0;
+    double r = 0.0;
+    float out = 0.0f;
+    const int special = ws_expf_reduce(x, &ki, &r, &out);
+    const int j = (int)(ki & 31);
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)tab, j, 64);
+    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(tab >> 32), j, 64);
+    const float v = ws_expf_finish(ki, r, ((uint64_t)hi << 32) | lo);
+    return special ? out : v;
+}
+
+// num.rs:71 sigmoid, 1/(1+exp(-x)), on ws_expf_lanes
+__device__ __forceinline__ float ws_sigmoid_lanes(float x, uint64_t tab) {
+WS_NO_CONTRACT
+    return 1.0f / (1.0f + ws_expf_lanes(-x, tab));
+}
+
 // Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 reduce
 // separately). Max is exact, so the order does not matter.
 __device__ __forceinline__ float half_wave_max(float v) {

@@ -68,29 +68,39 @@ WS_HD double ws_u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
 #define WS_EXPF_FMA 1
 #endif
 
-WS_HD float ws_expf(float x) {
+/* Split in two so that a caller may fetch the table entry its own way (the
+ * GPU routing kernel keeps the table in lane registers): ws_expf_reduce
+ * handles the special inputs (returns 1 with the result in *out) or computes
+ * k and r; ws_expf_finish evaluates 2^(k/N) * 2^(r/N) given the table entry
+ * ws_exp2f_tab[k % 32]. */
+WS_HD int ws_expf_reduce(float x, uint64_t *ki_out, double *r_out, float *out) {
 WS_NO_CONTRACT
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
-    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
-    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
-    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
     uint32_t ux = ws_f2u(x);
     uint32_t abstop = (ux >> 20) & 0x7ff;
     if (abstop >= (ws_f2u(88.0f) >> 20)) {
-        if (ux == 0xff800000u) return 0.0f;                 /* -inf */
-        if (abstop >= (0x7f800000u >> 20)) return x + x;      /* +inf, nan */
-        if (x > 0x1.62e42ep6f) return ws_u2f(0x7f800000u);   /* overflow */
-        if (x < -0x1.9fe368p6f) return 0.0f;                 /* underflow */
+        if (ux == 0xff800000u) { *out = 0.0f; return 1; }                 /* -inf */
+        if (abstop >= (0x7f800000u >> 20)) { *out = x + x; return 1; }      /* +inf, nan */
+        if (x > 0x1.62e42ep6f) { *out = ws_u2f(0x7f800000u); return 1; }   /* overflow */
+        if (x < -0x1.9fe368p6f) { *out = 0.0f; return 1; }                 /* underflow */
     }
     double xd = (double)x;
     double z = inv_ln2_n * xd;
     double kd = z + shift;
     uint64_t ki = ws_d2u(kd);
     kd -= shift;
-    double r = z - kd;
-    uint64_t t = ws_exp2f_tab[ki % 32];
-    t += ki << (52 - 5);
+    *r_out = z - kd;
+    *ki_out = ki;
+    return 0;
+}
+
+WS_HD float ws_expf_finish(uint64_t ki, double r, uint64_t tab) {
+WS_NO_CONTRACT
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    uint64_t t = tab + (ki << (52 - 5));
     double s = ws_u2d(t);
 #if WS_EXPF_FMA
     double zz = __builtin_fma(c0, r, c1);
@@ -105,6 +115,14 @@ WS_NO_CONTRACT
 #endif
     y = y * s;
     return (float)y;
+}
+
+WS_HD float ws_expf(float x) {
+    uint64_t ki;
+    double r;
+    float out;
+    if (ws_expf_reduce(x, &ki, &r, &out)) return out;
+    return ws_expf_finish(ki, r, ws_exp2f_tab[ki % 32]);
 }
 
 /* sigmoid and silu in the reference's exact operation order
