@@ -15,10 +15,10 @@ block GEMM TFLOP/s at M=128"):
            weights rotated over > 256 MB of copies (cold).
 
 Timing: the steps are captured once into a HIP graph (one node per kernel,
-no allocation, no memset) and replayed; wall time between two device
-synchronisations brackets exactly `--steps` steps. Per-kernel durations for
-the roofline come from HIP events recorded on the launch stream around
-individual launches.
+no allocation, no memset) holding exactly `--steps` steps and replayed once;
+wall time between two device synchronisations brackets it. Per-kernel
+durations for the roofline come from HIP events recorded on the launch stream
+around batches of back-to-back launches of that kernel alone.
 
     python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
 """
@@ -130,18 +130,22 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
         L.emit8(x[t], xq[t], xs[t], DIM, stream=s)
     torch.cuda.synchronize()
 
-    def timed(fn, reps_k):
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(reps_k)]
-        for i in range(reps_k):
-            t = i % n_tokens
-            ev[i][0].record(s)
-            fn(t)
-            ev[i][1].record(s)
-        torch.cuda.synchronize()
-        ms = [a.elapsed_time(b) for a, b in ev]
-        ms.sort()
-        return sum(ms) / len(ms), ms[len(ms) // 2]
+    def timed(fn, reps_k, batches=5):
+        """Average kernel duration: `batches` batches of reps_k back-to-back
+        launches, each bracketed by two events on the launch stream (the
+        queue stays ahead of the GPU, so a batch measures kernel time, not
+        launch latency). Returns (average, median of the batch averages)."""
+        per = []
+        for _ in range(batches):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(s)
+            for i in range(reps_k):
+                fn(i % n_tokens)
+            b.record(s)
+            torch.cuda.synchronize()
+            per.append(a.elapsed_time(b) / reps_k)
+        per_sorted = sorted(per)
+        return sum(per) / len(per), per_sorted[len(per) // 2]
 
     glu = lambda t: L.expert_glu_quant_x(x[t], idx[t], wts[t], w1, s1, w3, s3, hq[t], hs[t],
                                          INTER, DIM, E, TOPK, stream=s)
@@ -149,7 +153,7 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
                                     stream=s)
     for t in range(n_tokens):
         glu(t)
-    reps_k = max(200, n_tokens)
+    reps_k = max(100, n_tokens)
     glu_avg, glu_med = timed(glu, reps_k)
     red_avg, red_med = timed(red, reps_k)
     glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + 4 * DIM + TOPK * (INTER + INTER // 32)
@@ -243,15 +247,17 @@ def bench_gemm(L, torch, dev, reps):
                     L.fp8_gemm_f32s(aqf, asf, wq[c], wsf[c], y, M, N, K, out_bf16=True, stream=s)
             for c in range(copies):
                 run(c)
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(reps)]
-            for i in range(reps):
-                ev[i][0].record(s)
-                run(i % copies)
-                ev[i][1].record(s)
-            torch.cuda.synchronize()
-            ms = sorted(a.elapsed_time(b) for a, b in ev)
-            avg = sum(ms) / len(ms)
+            per = []
+            for _ in range(5):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(s)
+                for i in range(reps):
+                    run(i % copies)
+                b.record(s)
+                torch.cuda.synchronize()
+                per.append(a.elapsed_time(b) / reps)
+            ms = sorted(per)
+            avg = sum(per) / len(per)
             bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 2
             res[fmt] = {"avg_us": avg * 1e3, "median_us": ms[len(ms) // 2] * 1e3,
                         "TFLOP/s": flops / (avg * 1e-3) / 1e12,
@@ -315,7 +321,7 @@ def main():
         log("parity on %d tokens: routing bit-exact=%s, max rel err %.2e" % (n, route_ok, worst))
         if not route_ok or worst > 1e-3:
             raise RuntimeError("GPU results differ from the oracle")
-    gemm = None if args.no_gemm else bench_gemm(L, torch, dev, 200)
+    gemm = None if args.no_gemm else bench_gemm(L, torch, dev, 40)
 
     line = {
         "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
