@@ -207,12 +207,13 @@ def cpu_baseline_moe(res, seconds):
     return step_bytes * n / spent / 1e9, n, spent, worst, route_ok
 
 
-def bench_gemm(L, torch, dev, reps):
-    """Config 2: M=128, K=4096 FP8 block-scaled GEMM (act quant + GEMM per
-    step), cold weights (rotated over > 256 MB of copies)."""
+def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
+    """Configs 1 (M=1 GEMV, N=4096) and 2 (M=128, N in {4096, 12288, 2048}):
+    K=4096 FP8 block-scaled GEMM, both scale formats (UE8M0 1x32/32x32 and
+    f32 1x128/128x128), cold weights (rotated over > 256 MB of copies)."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(2)
-    M, K = 128, 4096
+    K = 4096
     out = {}
     x = torch.randn((M, K), device=dev, generator=gen)
     x = torch.where(torch.rand((M, K), device=dev, generator=gen) < 0.01, x * 20, x)
@@ -223,7 +224,7 @@ def bench_gemm(L, torch, dev, reps):
     L.emit8(x, aq8, as8, M * K)
     L.act_quant_f32s(x, aqf, asf, M, K)
     s = torch.cuda.current_stream()
-    for N in (4096, 12288, 2048):
+    for N in Ns:
         copies = max(2, math.ceil(400e6 / (N * K)))
         w = torch.randn((N, K), device=dev, generator=gen) * 0.02
         wq = torch.empty((copies, N, K), dtype=torch.uint8, device=dev)
@@ -268,6 +269,59 @@ def bench_gemm(L, torch, dev, reps):
         L.set_math_mode(L.MATH_EXACT)
         del wq, ws8, wsf
     return out
+
+
+def bench_prefill(L, torch, dev, packed, reps, m=132):
+    """Config 4: grouped prefill of m tokens through the same 384-expert layer,
+    router logits skewed by Zipf(1.1) popularity (log p_e added to N(0,1)
+    logits, popularity order a seeded permutation). Timed: top-k routing +
+    the whole grouped MoE (quantise, dispatch, grouped gate/up, grouped down,
+    combine). Algorithmic bytes: the touched experts' weights once."""
+    import numpy as np
+    rng = np.random.default_rng(4)
+    pop = np.log(1.0 / np.arange(1, E + 1) ** 1.1)[rng.permutation(E)].astype(np.float32)
+    batches = 4
+    logits = torch.from_numpy(
+        (rng.standard_normal((batches, m, E)).astype(np.float32) + pop)).to(dev)
+    bias = torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev)
+    x = torch.from_numpy(rng.standard_normal((batches, m, DIM)).astype(np.float32)).to(dev)
+    idx = torch.empty((batches, m, TOPK), dtype=torch.int32, device=dev)
+    wts = torch.empty((batches, m, TOPK), dtype=torch.float32, device=dev)
+    y = torch.empty((batches, m, DIM), dtype=torch.float32, device=dev)
+    ws = torch.empty(L.moe_prefill_workspace_size(m, DIM, INTER, TOPK, E), dtype=torch.uint8,
+                     device=dev)
+    s = torch.cuda.current_stream()
+
+    def step(b):
+        L.moe_topk(logits[b], bias, None, idx[b], wts[b], m, E, TOPK, L.SCORE_SIGMOID, 1.0, True,
+                   1.0, stream=s)
+        L.moe_prefill(x[b], idx[b], wts[b], *packed, y[b], m, DIM, INTER, E, TOPK, ws, stream=s)
+
+    for b in range(batches):
+        step(b)
+    torch.cuda.synchronize()
+    touched = [len(np.unique(idx[b].cpu().numpy())) for b in range(batches)]
+    per = []
+    for _ in range(3):
+        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        for i in range(reps):
+            step(i % batches)
+        e.record(s)
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(e) / reps)
+    ms = sum(per) / len(per)
+    avg_bytes = sum(touched) / batches * EXPERT_BYTES
+    flops = 2.0 * m * TOPK * 3 * DIM * INTER
+    counts = np.bincount(idx[0].cpu().numpy().ravel(), minlength=E)
+    return {"tokens": m, "avg_us": ms * 1e3, "experts_touched": touched,
+            "GB/s": avg_bytes / (ms * 1e-3) / 1e9,
+            "frac_hbm_peak": avg_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "TFLOP/s": flops / (ms * 1e-3) / 1e12,
+            "tokens_per_s": m / (ms * 1e-3),
+            "count_hist_batch0": {"0": int((counts == 0).sum()), "1-3": int(((counts >= 1) & (counts <= 3)).sum()),
+                                  "4-20": int(((counts >= 4) & (counts <= 20)).sum()),
+                                  ">20": int((counts > 20).sum())}}
 
 
 def main():
@@ -321,7 +375,16 @@ def main():
         log("parity on %d tokens: routing bit-exact=%s, max rel err %.2e" % (n, route_ok, worst))
         if not route_ok or worst > 1e-3:
             raise RuntimeError("GPU results differ from the oracle")
-    gemm = None if args.no_gemm else bench_gemm(L, torch, dev, 40)
+    prefill = bench_prefill(L, torch, dev, packed, 10)
+    L.set_math_mode(L.MATH_NATIVE)
+    prefill["native_math"] = {k: v for k, v in bench_prefill(L, torch, dev, packed, 10).items()
+                              if k in ("avg_us", "GB/s", "TFLOP/s")}
+    L.set_math_mode(L.MATH_EXACT)
+    log("prefill: %s" % prefill)
+    gemm = gemv = None
+    if not args.no_gemm:
+        gemv = bench_gemm(L, torch, dev, 100, M=1, Ns=(4096,))
+        gemm = bench_gemm(L, torch, dev, 40)
 
     line = {
         "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
@@ -348,7 +411,9 @@ def main():
         "native_math": {"value": native["gbs"], "ms_per_step": native["ms_per_step"],
                         "kernels": native["kernels"],
                         "note": "FP4xFP8 scaled MFMA; ~13-bit internal accumulation"},
+        "fp8_gemv_m1": gemv,
         "fp8_gemm_m128": gemm,
+        "moe_prefill_m132": prefill,
     }
     print(json.dumps(line), flush=True)
 

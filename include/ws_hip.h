@@ -229,7 +229,10 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,
  * Routed experts, M tokens (grouped prefill / batched decode). Replaces the
  * TileLang pipeline of engine.rs:4125-4243 (moe_dispatch_tl launch.rs:430,
  * moe_grouped_tl(_cached)(_on) :478-580, moe_swiglu_route :673,
- * moe_combine_f32 :689). Routes r = token * top_k + j.
+ * moe_combine_f32 :689). Routes r = token * top_k + j. Expert slabs are
+ * packed (ws_prepack_fp4). Shapes: dim and inter multiples of 128, dim <=
+ * 4096 (a 32-slot tile of x is staged in LDS), inter <= 2048; WS_ERR_SHAPE
+ * otherwise.
  * ------------------------------------------------------------------- */
 /* launch.rs:430-468 moe_dispatch_tl (moe_dispatch.cu:17): per-expert counts,
  * 32-padded offsets in ascending expert id (exclusive scan), psum = offset +

@@ -142,6 +142,19 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const fl
 static std::atomic<int> g_math_mode{WS_MATH_EXACT};
 int math_mode() { return g_math_mode.load(std::memory_order_relaxed); }
 
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+        n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
 }  // namespace ws
 
 using namespace ws;

@@ -247,6 +247,227 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
         }
 }
 
+// ---- K-parallel GEMM: one workgroup per 16 output columns -----------------
+// HBM-bound shapes (M <= a few hundred, e.g. M=128, K=4096): the weight matrix
+// must cross HBM exactly once, so a workgroup owns a 16-column strip of B for
+// all K and up to 16*MF*GMH rows of A. Its GMH x GK waves split the rows in
+// GMH halves and K in GK parts; a wave streams its K part in double-buffered
+// register stages of U 128-K steps (clamped, unconditional loads: one wait per
+// stage). The GK partial sums meet in LDS and are added in wave order
+// (deterministic). f32-scale mode stages the activation scales of the
+// workgroup's rows in LDS once, transposed to [step][row].
+template <int MF, int U>
+struct KpStage {
+    uint4 a[U][MF][2];
+    uint32_t sa[U][MF];
+    uint4 b[U][2];
+    uint32_t sb[U];
+    float sbf[U];
+};
+
+constexpr int kKpMaxSaPerThread = 4;  // f32 A scales staged per thread (float4 each)
+
+template <int MF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT>
+__global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A, const void *SA,
+                                                                const uint8_t *__restrict__ B,
+                                                                const void *__restrict__ SB,
+                                                                void *__restrict__ C, int M,
+                                                                int N, int K) {
+    constexpr int kRows = 16 * MF * GMH;
+    constexpr int kThreads = 64 * GMH * GK;
+    extern __shared__ __align__(16) float kp_lds[];
+    float *part = kp_lds;                      // [GK][kRows][16]
+    float *sa_l = kp_lds + GK * kRows * 16;    // [ksteps][kRows] (f32-scale mode)
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int wk = w % GK, wm = w / GK;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int mb = blockIdx.y * kRows;           // workgroup's first row
+    const int ml = wm * 16 * MF;                 // wave's first row within the workgroup
+    const int ksteps = K / 128;
+    const int k0 = wk * ksteps / GK, k1 = (wk + 1) * ksteps / GK;
+    const int kbn = K / 32, kb128 = K / 128;
+
+    // f32 activation scales of the workgroup's rows: loads first
+    float4 sav[kKpMaxSaPerThread];
+    const int nsa = kRows * ksteps;  // <= kThreads * 4 * kKpMaxSaPerThread (checked on the host)
+    if (SMODE == kF32s) {
+        const float *saf = (const float *)SA;
+#pragma unroll
+        for (int j = 0; j < kKpMaxSaPerThread; j++) {
+            // element e = row_local * ksteps + ks, four at a time (ksteps % 4 == 0)
+            const int e = min((j * kThreads + t) * 4, nsa - 4);
+            const int rl = e / ksteps, ks = e % ksteps;
+            const int row = min(mb + rl, M - 1);
+            sav[j] = *(const float4 *)(saf + (size_t)row * kb128 + ks);
+        }
+        mem_order();
+    }
+
+    const uint8_t *arow[MF];
+    const uint8_t *sarow[MF];
+#pragma unroll
+    for (int i = 0; i < MF; i++) {
+        const int row = min(mb + ml + 16 * i + r, M - 1);
+        arow[i] = A + (size_t)row * K + (EXACT ? g * 32 : g * 16);
+        sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
+    }
+    const int col = n0 + r;
+    const uint8_t *brow = BFP4 ? B + (size_t)col * (K / 2) + g * 16
+                               : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
+    const uint8_t *sbrow = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
+    const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
+
+    auto load = [&](KpStage<MF, U> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int ks = max(min(ks0 + u, k1 - 1), 0);
+#pragma unroll
+            for (int i = 0; i < MF; i++) {
+                const uint8_t *p = arow[i] + (size_t)ks * 128;
+                st.a[u][i][0] = ldg16(p);
+                st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
+                if (SMODE == kUe8m0) st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * g);
+            }
+            if (BFP4) {
+                st.b[u][0] = ldg16_stream(brow + (size_t)ks * 64);
+            } else {
+                const uint8_t *p = brow + (size_t)ks * 128;
+                st.b[u][0] = ldg16_stream(p);
+                st.b[u][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+            }
+            if (SMODE == kUe8m0) st.sb[u] = *(const uint32_t *)(sbrow + ks * 4) >> (8 * g);
+            else st.sbf[u] = sbf_row[ks];
+        }
+    };
+
+    v4f acc[MF];
+#pragma unroll
+    for (int i = 0; i < MF; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const KpStage<MF, U> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int ks = ks0 + u;
+            if (ks >= k1) continue;  // uniform
+            if (EXACT) {
+                v8bf bq[4];
+                const float sbv = SMODE == kUe8m0 ? e8m0_to_f32(st.sb[u] & 0xFF) : 1.0f;
+                if (BFP4) cvt_fp4x32(st.b[u][0], sbv, bq);
+                else cvt_fp8x32(st.b[u][0], st.b[u][1], sbv, bq);
+#pragma unroll
+                for (int i = 0; i < MF; i++) {
+                    v8bf aq[4];
+                    const float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(st.sa[u][i] & 0xFF) : 1.0f;
+                    cvt_fp8x32(st.a[u][i][0], st.a[u][i][1], sav_f, aq);
+                    if (SMODE == kUe8m0) {
+                        acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
+                    } else {
+                        const v4f p = mfma_bf16_k128(aq, bq, v4f{0.f, 0.f, 0.f, 0.f});
+                        const float4 sa4 = *(const float4 *)(sa_l + ks * kRows + ml + 16 * i + 4 * g);
+                        const float sa_v[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[i][v] = acc[i][v] + p[v] * (sa_v[v] * st.sbf[u]);
+                    }
+                }
+            } else {
+                const v8i b = BFP4 ? frag_from4(st.b[u][0]) : frag_from(st.b[u][0], st.b[u][1]);
+#pragma unroll
+                for (int i = 0; i < MF; i++) {
+                    const v8i a = frag_from(st.a[u][i][0], st.a[u][i][1]);
+                    if (SMODE == kUe8m0) {
+                        acc[i] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b, acc[i], (int)st.sa[u][i],
+                                                                      (int)st.sb[u])
+                                      : mfma_scaled<kFmtFp8, kFmtFp8>(a, b, acc[i], (int)st.sa[u][i],
+                                                                      (int)st.sb[u]);
+                    } else {
+                        const v4f p = mfma_scaled<kFmtFp8, kFmtFp8>(a, b, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                    kScaleOne, kScaleOne);
+                        const float4 sa4 = *(const float4 *)(sa_l + ks * kRows + ml + 16 * i + 4 * g);
+                        const float sa_v[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                        for (int v = 0; v < 4; v++) acc[i][v] = acc[i][v] + p[v] * (sa_v[v] * st.sbf[u]);
+                    }
+                }
+            }
+        }
+    };
+
+    KpStage<MF, U> s0, s1;
+    load(s0, k0);
+    mem_order();
+    load(s1, k0 + U);
+    mem_order();
+    if (SMODE == kF32s) {
+#pragma unroll
+        for (int j = 0; j < kKpMaxSaPerThread; j++) {
+            const int e = (j * kThreads + t) * 4;
+            if (e >= nsa) continue;
+            const int rl = e / ksteps, ks = e % ksteps;
+            const float v[4] = {sav[j].x, sav[j].y, sav[j].z, sav[j].w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) sa_l[(ks + c) * kRows + rl] = v[c];
+        }
+        lds_barrier();
+    }
+
+    // steady state: both stages reloaded unconditionally (straight-line body)
+    const int nst = (k1 - k0 + U - 1) / U;
+    int i = 0, ks0 = k0;
+    for (; i + 3 < nst; i += 2, ks0 += 2 * U) {
+        compute(s0, ks0);
+        load(s0, ks0 + 2 * U);
+        compute(s1, ks0 + U);
+        load(s1, ks0 + 3 * U);
+    }
+    const int rest = nst - i;
+    if (rest == 3) {
+        compute(s0, ks0);
+        load(s0, ks0 + 2 * U);
+        compute(s1, ks0 + U);
+        compute(s0, ks0 + 2 * U);
+    } else {
+        if (rest >= 1) compute(s0, ks0);
+        if (rest == 2) compute(s1, ks0 + U);
+    }
+
+    // D[m][n]: lane -> row 4g+v of fragment i, column r
+#pragma unroll
+    for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) part[(wk * kRows + ml + 16 * f + 4 * g + v) * 16 + r] = acc[f][v];
+    __syncthreads();
+    for (int o = t; o < kRows * 16; o += kThreads) {
+        const int rl = o >> 4, c = o & 15;
+        const int row = mb + rl;
+        if (row >= M) continue;
+        float sum = part[rl * 16 + c];
+#pragma unroll
+        for (int q = 1; q < GK; q++) sum = sum + part[(q * kRows + rl) * 16 + c];
+        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + n0 + c] = sum;
+        else ((uint16_t *)C)[(size_t)row * N + n0 + c] = f32_to_bf16(sum);
+    }
+}
+
+template <int MF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U>
+static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
+                     int m, int n, int k, hipStream_t stream) {
+    constexpr int rows = 16 * MF * GMH, threads = 64 * GMH * GK;
+    const int ksteps = k / 128;
+    if (SMODE == kF32s && (rows * ksteps > threads * 4 * kKpMaxSaPerThread || ksteps % 4 ||
+                           ((uintptr_t)sa & 15)))
+        return -1;  // caller falls back to the general kernel
+    size_t lds = (size_t)GK * rows * 16 * 4 + (SMODE == kF32s ? (size_t)ksteps * rows * 4 : 0);
+    dim3 grid((unsigned)(n / 16), (unsigned)((m + rows - 1) / rows));
+    if (math_mode() == WS_MATH_NATIVE)
+        hipLaunchKernelGGL((gemm_kp_kernel<MF, GMH, GK, BFP4, SMODE, OMODE, U, false>), grid,
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k);
+    else
+        hipLaunchKernelGGL((gemm_kp_kernel<MF, GMH, GK, BFP4, SMODE, OMODE, U, true>), grid,
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k);
+    return launch_status();
+}
+
 // Tile configurations. A config is chosen from M unless WS_GEMM_CFG forces one
 // (a tuning knob for measurements).
 struct GemmCfg {
@@ -282,7 +503,17 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         return WS_ERR_INVALID_ARG;
     int M = (int)m, N = (int)n, K = (int)k;
     int cfg = forced_cfg();
-    if (cfg < 0) cfg = (M <= 16) ? 5 : (M <= 64 ? 10 : 8);
+    if (cfg < 0) {
+        // K-parallel strips (one workgroup per 16 columns); -1: shape outside
+        // what they stage, use the general kernel
+        int rc;
+        if (M <= 16) rc = launch_kp<1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        else if (M <= 32) rc = launch_kp<2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+        else if (M <= 64) rc = launch_kp<4, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+        else rc = launch_kp<4, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+        if (rc >= 0) return rc;
+        cfg = (M <= 16) ? 5 : (M <= 64 ? 10 : 8);
+    }
     switch (cfg) {
         case 0:  // decode: 16 x 16 tile, K split over 4 waves
             return launch_cfg<1, 1, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);

@@ -151,18 +151,6 @@ __device__ __forceinline__ void k_part(int ksteps, int part, int parts, int &k0,
 // before its weight loads, converts while the weight stages are in flight,
 // and the waves meet at an LDS-only barrier that leaves those loads in flight.
 
-// Compiler-only barrier: memory accesses are not moved across it, so loads
-// issued before it leave the wave first (load counters then return them in
-// issue order and a wait for them does not cover later loads).
-__device__ __forceinline__ void mem_order() { __asm__ volatile("" ::: "memory"); }
-
-// Barrier that orders LDS only: global loads issued before it stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // ---- the token, split over the streaming waves ----------------------------
 // Each of the `parts` streaming waves converts its share of the token into
 // LDS. It issues the share's loads before its weight loads (loads return in

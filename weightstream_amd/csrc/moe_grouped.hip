@@ -130,183 +130,262 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     }
 }
 
-// ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
-// grid (inter/32, tiles), 4 waves: wave (mat = w>>1, half = w&1) computes the
-// 32 slots x 16 output columns of w1 (mat 0) or w3 (mat 1).
-template <bool EXACT>
-__global__ __launch_bounds__(256) void grouped_glu_quant_kernel(
-    const uint8_t *__restrict__ xq, const uint8_t *__restrict__ xs,
-    const int32_t *__restrict__ order, const float *__restrict__ layout_w,
-    const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ num_tiles,
-    const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
-    const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
-    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit) {
-    __shared__ float gu[2][kTile][kTile + 1];
-    const int tile = blockIdx.y;
-    if (tile >= *num_tiles) return;
-    const int e = tile_expert[tile];
-    if (e < 0 || e >= n_experts) return;
-    const int nt = blockIdx.x;
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int r = lane & 15, kb = lane >> 4;
-    const int slot0 = tile * kTile;
-    const int mat = w >> 1, half = w & 1;
+// ---- grouped expert GEMM streaming ----------------------------------------
+// Work unit = (32-slot tile, block of output columns). The grid has one
+// workgroup per CU; workgroup i takes the contiguous units
+// [i*U/G, (i+1)*U/G) of the U = used_tiles x column_blocks units (the used
+// tile count is read on the device, so every workgroup gets an equal share).
+// Within a unit each wave streams one packed 16-row FP4 band of the tile's
+// expert over its K range in two register stages (steps [k0, k0+8) and
+// [k0+8, k1)); the stages of the next unit are loaded while the current unit
+// is multiplied, so the weight stream never drains between units. The tile's
+// A rows (32 token rows of x for gate/up, 32 slot rows of hq for down; FP8 +
+// UE8M0) sit in LDS, copied with direct global->LDS loads whenever the
+// workgroup moves to a new tile.
+constexpr int kGThreads = 512;  // 8 waves
 
-    const uint8_t *arow[2];
-    const uint8_t *srow[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int route = order[slot0 + i * 16 + r];
-        int tok = route >= 0 ? route / top_k : 0;
-        arow[i] = xq + (size_t)tok * dim + (EXACT ? kb * 32 : kb * 16);
-        srow[i] = xs + (size_t)tok * (dim / 32);
+// The tile's 32 A rows into LDS, a_l[32][K] and their UE8M0 bytes
+// as_l[32][K/32], with direct global->LDS loads (global_load_lds_dwordx4 /
+// _dword: no VGPR staging). One instruction fills a contiguous 1 KB (256 B)
+// of the LDS image; lane l moves the 16 (4) bytes at image offset o, which
+// belong to row o / K (o / (K/32)). Row i of A starts at arow(i), its scales
+// at srow(i). Completion is awaited by the caller (vmcnt) before the barrier.
+template <class ARow, class SRow>
+__device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, int lane,
+                                           uint8_t *a_l, uint8_t *as_l) {
+    const int nq = kTile * K / 1024;
+    for (int c = w; c < nq; c += kGThreads / 64) {
+        const int o = c * 1024 + lane * 16;
+        const int row = o / K, col = o - row * K;
+        __builtin_amdgcn_global_load_lds((const void *)(arow(row) + col),
+                                         (__attribute__((address_space(3))) void *)(a_l + c * 1024),
+                                         16, 0, 0);
     }
+    const int ks = K / 32, nsq = (kTile * ks + 255) / 256;
+    for (int c = w; c < nsq; c += kGThreads / 64) {
+        const int o = min(c * 256 + lane * 4, kTile * ks - 4);
+        const int row = o / ks, col = o - row * ks;
+        __builtin_amdgcn_global_load_lds((const void *)(srow(row) + col),
+                                         (__attribute__((address_space(3))) void *)(as_l + c * 256),
+                                         4, 0, 0);
+    }
+}
+
+// LDS bytes of the A tile image (scales padded to whole 256-byte pieces)
+__host__ __device__ constexpr size_t g_tile_lds(int K) {
+    return (size_t)kTile * K + ((size_t)kTile * (K / 32) + 255) / 256 * 256;
+}
+
+// One stage (steps [ks0, kend), at most kU) of a band times the two 16-slot A
+// fragments in LDS (row stride K bytes, scales as_l[slot][K/32]).
+// D[m][n]: slot 4*(lane/16)+v of fragment i, band row lane%16.
+template <bool EXACT>
+__device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const uint8_t *a_l,
+                                          const uint8_t *as_l, int K, int ks0, int kend,
+                                          int lane) {
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        const int ks = ks0 + u;
+        if (ks >= kend) continue;  // uniform
+        const uint32_t sbyte = stage_scale(st, u);
+        if (EXACT) {
+            v8bf bq[4];
+            cvt_fp4x32(st.w[u], e8m0_to_f32(sbyte), bq);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int slot = i * 16 + r;
+                const uint8_t *ap = a_l + slot * K + ks * 128 + g * 32;
+                v8bf aq[4];
+                cvt_fp8x32(*(const uint4 *)ap, *(const uint4 *)(ap + 16),
+                           e8m0_to_f32(as_l[slot * (K / 32) + ks * 4 + g]), aq);
+                acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
+            }
+        } else {
+            const v8i b = frag_from4(st.w[u]);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int slot = i * 16 + r;
+                const uint8_t *ap = a_l + slot * K + ks * 128 + g * 16;
+                acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(
+                    frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64)), b, acc[i],
+                    (int)as_l[slot * (K / 32) + ks * 4 + g], (int)sbyte);
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ int g_expert(const int32_t *tile_expert, int tile, int n_experts) {
+    const int e = tile_expert[tile];
+    return e < 0 ? 0 : (e >= n_experts ? n_experts - 1 : e);
+}
+
+// ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
+// Unit = (tile, 32 intermediate columns nt). Wave w: matrix (w>>1)&1 (w1|w3),
+// 16-row half w&1, K half w>>2 (each 8-step aligned, at most 16 steps: dim
+// <= 4096). The epilogue adds the K halves, applies SwiGLU x routing weight to
+// the 32 x 32 tile and quantises each slot's 32 values (one FP8 1x32 block) to
+// hq/hs.
+template <bool EXACT>
+__global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
+    const uint8_t *xq, const uint8_t *xs, const int32_t *__restrict__ order,
+    const float *__restrict__ layout_w, const int32_t *__restrict__ tile_expert,
+    const int32_t *__restrict__ num_tiles, const uint8_t *__restrict__ w1,
+    const uint8_t *__restrict__ s1, const uint8_t *__restrict__ w3,
+    const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq, uint8_t *__restrict__ hs, int dim,
+    int inter, int n_experts, int top_k, float limit) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    uint8_t *a_l = g_lds;                           // [32][dim]
+    uint8_t *as_l = g_lds + (size_t)kTile * dim;    // [32][dim/32] (+ padding)
+    __shared__ float gu[2][2][kTile][kTile + 1];
+    __shared__ float rw_l[kTile];  // routing weight of each slot of the tile (0: padding)
+    __shared__ int pad_l[kTile];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const uint64_t tab = ws_lane_exp2f_tab(lane);
+    const int r = lane & 15, g = lane >> 4;
+    const int mat = (w >> 1) & 1, half = w & 1, kpart = w >> 2;
+    int k0, k1;
+    k_part8(dim / 128, kpart, 2, k0, k1);
+    const int km = min(k0 + kU, k1);  // stage 0: [k0, km), stage 1: [km, k1)
+    const int NT = inter / 32;
+    const int units = *num_tiles * NT;
+    const int u0 = (int)((long)blockIdx.x * units / gridDim.x);
+    const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
+    if (u0 >= u1) return;  // whole workgroup
     const size_t wmat = (size_t)inter * (dim / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
-    const Fp4Band band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat,
-                                  (mat ? s3 : s1) + (size_t)e * smat, nt * 2 + half, dim, lane);
-
-    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const int ksteps = dim / 128;
-    constexpr int U = 4;
-    for (int ks0 = 0; ks0 < ksteps; ks0 += U) {
-        uint4 bf[U], af[U][2][2];
-        uint32_t sb[U], sa[U][2];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            // steps past the end re-load the last one (unused): no branches
-            int ks = min(ks0 + u, ksteps - 1);
-            {
-                bf[u] = ldg16_stream(band.w + (size_t)ks * 1024);
-                sb[u] = band.s[(size_t)(ks / 8) * 512 + ks % 8];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    af[u][i][0] = ldg16(arow[i] + ks * 128);
-                    af[u][i][1] = ldg16(arow[i] + ks * 128 + (EXACT ? 16 : 64));
-                    sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (ks0 + u >= ksteps) continue;
-            if (EXACT) {
-                v8bf bq[4];
-                cvt_fp4x32(bf[u], e8m0_to_f32(sb[u] & 0xFF), bq);
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    v8bf aq[4];
-                    cvt_fp8x32(af[u][i][0], af[u][i][1], e8m0_to_f32(sa[u][i] & 0xFF), aq);
-                    acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
-                }
-            } else {
-                v8i b = frag_from4(bf[u]);
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-                    acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(frag_from(af[u][i][0], af[u][i][1]), b,
-                                                           acc[i], (int)sa[u][i], (int)sb[u]);
-            }
-        }
+    const uint8_t *wm = mat ? w3 : w1;
+    const uint8_t *sm = mat ? s3 : s1;
+    auto band_of = [&](int u) {
+        const int e = g_expert(tile_expert, u / NT, n_experts);
+        return fp4_band(wm + (size_t)e * wmat, sm + (size_t)e * smat, (u % NT) * 2 + half, dim,
+                        lane);
+    };
+    Fp4Stage st0, st1;
+    {
+        const Fp4Band b = band_of(u0);
+        fp4_load(st0, b, k0, km);
+        mem_order();
+        fp4_load(st1, b, km, k1);
+        mem_order();
     }
-    // D[m][n]: m = slot row 4*(lane/16)+v of fragment i, n = lane%16
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) gu[mat][i * 16 + 4 * kb + v][half * 16 + r] = acc[i][v];
-    __syncthreads();
-    // epilogue: a half-wave per slot row (32 values = one FP8 block)
-    const int col = t & 31;
-    for (int srow_i = t >> 5; srow_i < kTile; srow_i += 8) {
-        const int slot = slot0 + srow_i;
-        const bool pad = order[slot] < 0;
-        float g = gu[0][srow_i][col], u = gu[1][srow_i][col];
-        if (limit > 0.0f) {
-            u = rclamp(u, -limit, limit);
-            g = fminf(g, limit);
+    int cur_tile = -1;
+    for (int u = u0; u < u1; u++) {
+        const int tile = u / NT, nt = u % NT;
+        const int slot0 = tile * kTile;
+        if (tile != cur_tile) {  // uniform: stage the tile's token rows in LDS
+            int my_tok = 0;
+            if (lane < kTile) {
+                const int route = order[slot0 + lane];
+                my_tok = route >= 0 ? route / top_k : 0;
+                if (w == 0) {
+                    pad_l[lane] = route < 0;
+                    rw_l[lane] = layout_w[slot0 + lane];
+                }
+            }
+            g_dma_tile([&](int i) { return xq + (size_t)__shfl(my_tok, i, 64) * dim; },
+                       [&](int i) { return xs + (size_t)__shfl(my_tok, i, 64) * (dim / 32); },
+                       dim, w, lane, a_l, as_l);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+            lds_barrier();
+            cur_tile = tile;
         }
-        float h = pad ? 0.0f : ws_silu(g) * u * layout_w[slot];
-        uint32_t sbyte;
-        uint32_t q = quant_fp8_block32(h, &sbyte);
-        hq[(size_t)slot * inter + nt * kTile + col] = (uint8_t)q;
-        if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
+        const Fp4Band bn = band_of(min(u + 1, u1 - 1));
+        v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        g_compute<EXACT>(st0, acc, a_l, as_l, dim, k0, km, lane);
+        fp4_load(st0, bn, k0, km);
+        g_compute<EXACT>(st1, acc, a_l, as_l, dim, km, k1, lane);
+        fp4_load(st1, bn, km, k1);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) gu[kpart][mat][i * 16 + 4 * g + v][half * 16 + r] = acc[i][v];
+        lds_barrier();
+        // a half-wave per slot row (32 values = one FP8 block)
+        const int col = t & 31;
+        for (int srow = t >> 5; srow < kTile; srow += kGThreads / 32) {
+            const int slot = slot0 + srow;
+            const bool pad = pad_l[srow] != 0;
+            float gv = gu[0][0][srow][col] + gu[1][0][srow][col];
+            float uv = gu[0][1][srow][col] + gu[1][1][srow][col];
+            if (limit > 0.0f) {
+                uv = rclamp(uv, -limit, limit);
+                gv = fminf(gv, limit);
+            }
+            // every lane evaluates silu (the lane-table exp permutes across the wave)
+            const float sg = ws_silu_lanes(gv, tab);
+            const float h = pad ? 0.0f : sg * uv * rw_l[srow];
+            uint32_t sbyte;
+            const uint32_t q = quant_fp8_block32(h, &sbyte);
+            hq[(size_t)slot * inter + nt * kTile + col] = (uint8_t)q;
+            if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
+        }
+        lds_barrier();
     }
 }
 
 // ---- grouped down ---------------------------------------------------------
-// grid (dim/64, tiles), 4 waves: wave w computes 32 slots x 16 output columns
-// (columns nt*64 + w*16 ..) of the expert's w2; f32 out[slot, dim].
+// Unit = (tile, 128 output columns nt); wave w owns columns nt*128 + 16w ..
+// over the whole K = inter (at most 16 steps: inter <= 2048), so each output
+// is one wave's sum and is written straight from registers. f32 out[slot,
+// dim].
 template <bool EXACT>
-__global__ __launch_bounds__(256) void grouped_down_kernel(
-    const uint8_t *__restrict__ hq, const uint8_t *__restrict__ hs,
-    const int32_t *__restrict__ tile_expert, const int32_t *__restrict__ num_tiles,
-    const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
-    int dim, int inter, int n_experts) {
-    const int tile = blockIdx.y;
-    if (tile >= *num_tiles) return;
-    const int e = tile_expert[tile];
-    if (e < 0 || e >= n_experts) return;
+__global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
+    const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
+    const int32_t *__restrict__ num_tiles, const uint8_t *__restrict__ w2,
+    const uint8_t *__restrict__ s2, float *__restrict__ out, int dim, int inter, int n_experts) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    uint8_t *a_l = g_lds;                             // [32][inter]
+    uint8_t *as_l = g_lds + (size_t)kTile * inter;    // [32][inter/32] (+ padding)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int r = lane & 15, kb = lane >> 4;
-    const int slot0 = tile * kTile;
-    const int n = blockIdx.x * 64 + w * 16 + r;
+    const int r = lane & 15, g = lane >> 4;
+    const int k1 = inter / 128, km = min(kU, k1);
+    const int NT = dim / 128;
+    const int units = *num_tiles * NT;
+    const int u0 = (int)((long)blockIdx.x * units / gridDim.x);
+    const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
+    if (u0 >= u1) return;  // whole workgroup
     const size_t wmat = (size_t)dim * (inter / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
-    const Fp4Band band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat,
-                                  blockIdx.x * 4 + w, inter, lane);
-    const uint8_t *arow[2];
-    const uint8_t *srow[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        arow[i] = hq + (size_t)(slot0 + i * 16 + r) * inter + (EXACT ? kb * 32 : kb * 16);
-        srow[i] = hs + (size_t)(slot0 + i * 16 + r) * (inter / 32);
+    auto band_of = [&](int u) {
+        const int e = g_expert(tile_expert, u / NT, n_experts);
+        return fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, (u % NT) * 8 + w, inter,
+                        lane);
+    };
+    Fp4Stage s0, s1;
+    {
+        const Fp4Band b = band_of(u0);
+        fp4_load(s0, b, 0, km);
+        mem_order();
+        fp4_load(s1, b, km, k1);
+        mem_order();
     }
-    v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const int ksteps = inter / 128;
-    constexpr int U = 4;
-    for (int ks0 = 0; ks0 < ksteps; ks0 += U) {
-        uint4 bf[U], af[U][2][2];
-        uint32_t sb[U], sa[U][2];
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            // steps past the end re-load the last one (unused): no branches
-            int ks = min(ks0 + u, ksteps - 1);
-            {
-                bf[u] = ldg16_stream(band.w + (size_t)ks * 1024);
-                sb[u] = band.s[(size_t)(ks / 8) * 512 + ks % 8];
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    af[u][i][0] = ldg16(arow[i] + ks * 128);
-                    af[u][i][1] = ldg16(arow[i] + ks * 128 + (EXACT ? 16 : 64));
-                    sa[u][i] = *(const uint32_t *)(srow[i] + ks * 4) >> (8 * kb);
-                }
-            }
+    int cur_tile = -1;
+    for (int u = u0; u < u1; u++) {
+        const int tile = u / NT, nt = u % NT;
+        const int slot0 = tile * kTile;
+        if (tile != cur_tile) {  // uniform: stage the tile's hq rows in LDS
+            lds_barrier();       // every wave is done with the previous tile
+            g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
+                       [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); }, inter, w,
+                       lane, a_l, as_l);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+            lds_barrier();
+            cur_tile = tile;
         }
+        const Fp4Band bn = band_of(min(u + 1, u1 - 1));
+        v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        g_compute<EXACT>(s0, acc, a_l, as_l, inter, 0, km, lane);
+        fp4_load(s0, bn, 0, km);
+        g_compute<EXACT>(s1, acc, a_l, as_l, inter, km, k1, lane);
+        fp4_load(s1, bn, km, k1);
+        const int col = nt * 128 + w * 16 + r;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (ks0 + u >= ksteps) continue;
-            if (EXACT) {
-                v8bf bq[4];
-                cvt_fp4x32(bf[u], e8m0_to_f32(sb[u] & 0xFF), bq);
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    v8bf aq[4];
-                    cvt_fp8x32(af[u][i][0], af[u][i][1], e8m0_to_f32(sa[u][i] & 0xFF), aq);
-                    acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
-                }
-            } else {
-                v8i b = frag_from4(bf[u]);
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-                    acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(frag_from(af[u][i][0], af[u][i][1]), b,
-                                                           acc[i], (int)sa[u][i], (int)sb[u]);
-            }
-        }
+            for (int v = 0; v < 4; v++)
+                out[(size_t)(slot0 + i * 16 + 4 * g + v) * dim + col] = acc[i][v];
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int v = 0; v < 4; v++)
-            out[(size_t)(slot0 + i * 16 + 4 * kb + v) * dim + n] = acc[i][v];
 }
 
 // ---- combine: y[row] = sum of its routes' outputs in ascending slot order --
@@ -341,6 +420,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 static inline bool al4(const void *p) { return ((uintptr_t)p & 3) == 0; }
+static inline bool al8(const void *p) { return ((uintptr_t)p & 7) == 0; }
 static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static int64_t tiles_for(int64_t routes, int64_t n_experts) {
@@ -383,15 +463,17 @@ int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t
         return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || tiles > 65535 || dim > (1 << 20) || inter > (1 << 20))
         return WS_ERR_SHAPE;
-    if (!al16(xq) || !al16(w1) || !al16(w3) || !al4(xs) || !al4(s1) || !al4(s3))
+    if (!al16(xq) || !al16(w1) || !al16(w3) || !al4(xs) || !al8(s1) || !al8(s3))
         return WS_ERR_INVALID_ARG;
-    dim3 grid((unsigned)(inter / 32), (unsigned)tiles);
+    if (dim > 4096) return WS_ERR_SHAPE;  // the A tile (32 x dim bytes) lives in LDS
+    const size_t lds = g_tile_lds((int)dim);
+    dim3 grid((unsigned)cu_count());
     if (math_mode() == WS_MATH_EXACT)
-        hipLaunchKernelGGL(grouped_glu_quant_kernel<true>, grid, dim3(256), 0, stream, xq, xs, order,
+        hipLaunchKernelGGL(grouped_glu_quant_kernel<true>, grid, dim3(kGThreads), lds, stream, xq, xs, order,
                            layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs, (int)dim,
                            (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
     else
-        hipLaunchKernelGGL(grouped_glu_quant_kernel<false>, grid, dim3(256), 0, stream, xq, xs,
+        hipLaunchKernelGGL(grouped_glu_quant_kernel<false>, grid, dim3(kGThreads), lds, stream, xq, xs,
                            order, layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs,
                            (int)dim, (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
     return launch_status();
@@ -404,14 +486,16 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
     if (!hq || !hs || !tile_expert || !num_tiles || !w2 || !s2 || !out) return WS_ERR_INVALID_ARG;
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || tiles > 65535) return WS_ERR_SHAPE;
-    if (!al16(hq) || !al16(w2) || !al4(hs) || !al4(s2)) return WS_ERR_INVALID_ARG;
-    dim3 grid((unsigned)(dim / 64), (unsigned)tiles);
+    if (!al16(hq) || !al16(w2) || !al4(hs) || !al8(s2)) return WS_ERR_INVALID_ARG;
+    if (inter > 2048) return WS_ERR_SHAPE;  // one wave's K range fits two 8-step stages
+    const size_t lds = g_tile_lds((int)inter);
+    dim3 grid((unsigned)cu_count());
     if (math_mode() == WS_MATH_EXACT)
-        hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(256), 0, stream, hq, hs,
+        hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(kGThreads), lds, stream, hq, hs,
                            tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
                            (int)n_experts);
     else
-        hipLaunchKernelGGL(grouped_down_kernel<false>, grid, dim3(256), 0, stream, hq, hs,
+        hipLaunchKernelGGL(grouped_down_kernel<false>, grid, dim3(kGThreads), lds, stream, hq, hs,
                            tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
                            (int)n_experts);
     return launch_status();

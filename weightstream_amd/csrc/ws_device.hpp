@@ -83,6 +83,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
     return (uint16_t)((bits + round) >> 16);
 }
 
+// Compiler-only barrier: memory accesses are not moved across it, so loads
+// issued before it leave the wave first (load counters then return them in
+// issue order and a wait for them does not cover later loads).
+__device__ __forceinline__ void mem_order() { __asm__ volatile("" ::: "memory"); }
+
+// Barrier that orders LDS only: global loads issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ws_expf with the 32-entry table held in lane registers: lane l holds
 // ws_exp2f_tab[l % 32] (ws_lane_exp2f_tab) and the entry is fetched with a
 // lane permute instead of a memory load. Same arithmetic as ws_expf. Every
@@ -105,6 +117,12 @@ __device__ __forceinline__ float ws_expf_lanes(float x, uint64_t tab) {
 __device__ __forceinline__ float ws_sigmoid_lanes(float x, uint64_t tab) {
 WS_NO_CONTRACT
     return 1.0f / (1.0f + ws_expf_lanes(-x, tab));
+}
+
+// num.rs:79 silu, x * sigmoid(x), on ws_expf_lanes
+__device__ __forceinline__ float ws_silu_lanes(float x, uint64_t tab) {
+WS_NO_CONTRACT
+    return x * ws_sigmoid_lanes(x, tab);
 }
 
 // Max over the 32 lanes of each half-wave (lanes 0-31 and 32-63 reduce

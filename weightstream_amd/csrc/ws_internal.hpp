@@ -20,4 +20,7 @@ inline int launch_status() {
 // Math mode chosen by ws_set_math_mode (WS_MATH_EXACT by default).
 int math_mode();
 
+// Compute units of the current device (queried once per device).
+int cu_count();
+
 }  // namespace ws

@@ -58,6 +58,14 @@ __device__ __forceinline__ void fp4_load(Fp4Stage &st, const Fp4Band &b, int ks0
     st.s = *(const uint2 *)(b.s + (size_t)(min(ks0, last) / 8) * 512);
 }
 
+// K range [k0, k1) of part `part` of `parts` over `ksteps` 128-K steps, in
+// whole 8-step stages (so every stage starts on an 8-step scale group).
+__device__ __forceinline__ void k_part8(int ksteps, int part, int parts, int &k0, int &k1) {
+    const int stages = (ksteps + kU - 1) / kU;
+    k0 = min(ksteps, part * stages / parts * kU);
+    k1 = min(ksteps, (part + 1) * stages / parts * kU);
+}
+
 __device__ __forceinline__ uint32_t stage_scale(const Fp4Stage &st, int u) {
     return ((u < 4 ? st.s.x : st.s.y) >> (8 * (u & 3))) & 0xFF;
 }
