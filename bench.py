@@ -38,6 +38,11 @@ PEAK_FP8_TFLOPS = 5000.0
 FP4_MAT = INTER * DIM // 2          # packed bytes of one w1/w3/w2 matrix
 FP4_SC = INTER * DIM // 32          # UE8M0 bytes of one matrix
 EXPERT_BYTES = 3 * (FP4_MAT + FP4_SC)
+# HBM bytes per launch of the exact-math gate/up kernel at config 3, from
+# rocprofv3 FETCH_SIZE + WRITE_SIZE counter runs calibrated against a plain
+# 256 MiB copy (profiles/traffic_expert_kernels_moe_decode.md holds the runs and
+# commands; counters cannot be read from inside this process).
+GLU_TRAFFIC_BYTES = 71805786
 
 
 def log(*a):
@@ -333,6 +338,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB device-to-device 5 times (calibrates the HBM "
+                         "traffic counters against a known byte count) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the hot path is built and measured on a single "
@@ -341,6 +349,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_probe:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
+        return
     from weightstream_amd import launch as L
     L.Hip.global_()
     dev = "cuda:0"
@@ -362,7 +379,9 @@ def main():
     k = res["kernels"]["expert_glu_quant_kernel"]
     roof = {"kernel": "expert_glu_quant_kernel", "bound": "hbm", "achieved": k["GB/s"],
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["GB/s"] / PEAK_HBM_GBS,
-            "traffic": None}
+            "traffic": GLU_TRAFFIC_BYTES,
+            "algorithmic_bytes": k["bytes"], "avg_us": k["avg_us"],
+            "traffic_source": "profiles/traffic_expert_kernels_moe_decode.md"}
     cpu = None
     if not args.no_cpu:
         import multiprocessing

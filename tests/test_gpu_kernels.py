@@ -144,7 +144,8 @@ def test_fp4_gemm_matches_oracle(m, n, k):
     assert_close(host(out), want, GEMM_TOL, "fp4_gemm %dx%dx%d" % (m, n, k))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (128, 384, 4096), (20, 256, 512)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (128, 384, 4096), (20, 256, 512),
+                                   (5, 64, 1152)])  # K/128 = 9: the general kernel
 def test_fp8_gemm_f32s_matches_oracle(m, n, k):
     rng = np.random.default_rng(3000 + m + n + k)
     x = activations(rng, m, k)

@@ -468,12 +468,9 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     return launch_status();
 }
 
-// Tile configurations. A config is chosen from M unless WS_GEMM_CFG forces one
-// (a tuning knob for measurements).
-struct GemmCfg {
-    int tile_m, tile_n;
-};
-
+// General kernel configurations, used where the K-parallel kernel does not
+// stage a shape (f32 scales with K > 8192 or unaligned scale rows), or when
+// WS_GEMM_CFG forces one (0: 16 x 16 tiles, 1: 64 x 16 tiles) for measurements.
 template <int WM, int WN, int GM, int GK, bool BFP4, int SMODE, int OMODE, int U>
 static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
                       int m, int n, int k, hipStream_t stream) {
@@ -512,32 +509,12 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         else if (M <= 64) rc = launch_kp<4, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         else rc = launch_kp<4, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         if (rc >= 0) return rc;
-        cfg = (M <= 16) ? 5 : (M <= 64 ? 10 : 8);
+        cfg = (M <= 16) ? 0 : 1;
     }
     switch (cfg) {
-        case 0:  // decode: 16 x 16 tile, K split over 4 waves
-            return launch_cfg<1, 1, 1, 4, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
-        case 1:  // 64 x 16 tile
-            return launch_cfg<1, 1, 4, 1, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
-        case 2:  // 128 x 16 tile
-            return launch_cfg<2, 1, 4, 1, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
-        case 3:  // 128 x 32 tile
-            return launch_cfg<2, 2, 4, 1, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
-        case 4:  // 64 x 16 tile, K split over 2
-            return launch_cfg<1, 1, 4, 2, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
-        case 5:  // 16 x 16 tile, K split over 8 waves
+        case 0:  // 16 x 16 tile, K split over 8 waves
             return launch_cfg<1, 1, 1, 8, BFP4, SMODE, OMODE, 4>(a, sa, b, sb, out, M, N, K, stream);
-        case 6:  // 16 x 32 tile, K split over 4
-            return launch_cfg<1, 2, 1, 4, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
-        case 7:  // 16 x 16 tile, K split over 16 waves
-            return launch_cfg<1, 1, 1, 16, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-        case 8:  // 128 x 16 tile, K split over 4 (16 waves)
-            return launch_cfg<2, 1, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-        case 11:  // 128 x 16 tile, K split over 2 (8 waves)
-            return launch_cfg<2, 1, 4, 2, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
-        case 12:  // 128 x 32 tile, K split over 2 (8 waves)
-            return launch_cfg<2, 2, 4, 2, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-        case 10:  // 64 x 16 tile, K split over 4 (16 waves)
+        case 1:  // 64 x 16 tile, K split over 4 (16 waves)
             return launch_cfg<1, 1, 4, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         default:
             return WS_ERR_INVALID_ARG;

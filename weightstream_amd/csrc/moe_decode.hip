@@ -257,7 +257,7 @@ __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, i
                 *(u32x4v *)(x_l + i + 8 * c) = o;
             }
         } else {
-            *(uint4 *)(xq_l + i) = tr.q[j];
+            *(u32x4v *)(xq_l + i) = u32x4v{tr.q[j].x, tr.q[j].y, tr.q[j].z, tr.q[j].w};
             if ((i & 31) == 0) xs_l[i / 32] = (uint8_t)tr.s[j];
         }
     }
