@@ -229,6 +229,10 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
     L.emit8(x, aq8, as8, M * K)
     L.act_quant_f32s(x, aqf, asf, M, K)
     s = torch.cuda.current_stream()
+    # the production configuration: a split-K workspace registered once
+    ws = torch.empty(max(L.gemm_workspace_size(M, N, K) for N in Ns), dtype=torch.uint8,
+                     device=dev)
+    L.set_gemm_workspace(ws)
     for N in Ns:
         copies = max(2, math.ceil(400e6 / (N * K)))
         w = torch.randn((N, K), device=dev, generator=gen) * 0.02
@@ -273,6 +277,8 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
         out[str(N)] = res
         L.set_math_mode(L.MATH_EXACT)
         del wq, ws8, wsf
+    torch.cuda.synchronize()
+    L.set_gemm_workspace(None)
     return out
 
 

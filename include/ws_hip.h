@@ -98,6 +98,18 @@ int ws_weight_quant_fp8(const float *w, uint8_t *q, uint8_t *s, int64_t rows, in
  * One MFMA kernel family covers the reference's fp8_gemm (M=1 decode),
  * fp8_gemm_tile (M-batch) and the TileLang gemm_mxfp8 kernels.
  * ------------------------------------------------------------------- */
+/* Split-K workspace of the FP8/FP4 GEMMs (no counterpart in the reference,
+ * whose kernels keep the whole K of a tile in one block). Once a workspace is
+ * set for the current device, GEMMs with M > 16 split K across workgroups
+ * and a second kernel adds the f32 partials in split order (deterministic);
+ * without one they use the single-pass kernels. The workspace is shared by
+ * every GEMM call on the device: calls that may run concurrently (different
+ * streams) need it not to be set, or must be serialised.
+ * ws_gemm_workspace_size gives the bytes a shape needs; a smaller workspace
+ * makes that shape use the single-pass kernel. Workspace NULL unsets it;
+ * 256-byte aligned; `stream` is unused (kept for the launch convention). */
+size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k);
+int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream);
 /* launch.rs:717-742 fp8_gemm(_on) (fp8_gemm.cu:9): A e4m3 + sa[M,K/32],
  * B e4m3 + sb[ceil(N/32),K/32], C f32 [M,N]. */
 int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,

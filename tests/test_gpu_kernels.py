@@ -26,6 +26,20 @@ def _init():
     L.Hip.global_()
 
 
+@pytest.fixture(params=["single_pass", "split_k"])
+def gemm_path(request):
+    """Run a GEMM test with no split-K workspace (single-pass kernels) and
+    with one (M > 16 splits K across workgroups)."""
+    ws = None
+    if request.param == "split_k":
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+        L.set_gemm_workspace(ws)
+    yield request.param
+    if ws is not None:
+        torch.cuda.synchronize()
+        L.set_gemm_workspace(None)
+
+
 def _wide_range_acts(rng, n):
     x = rng.standard_normal(n).astype(np.float32)
     x *= np.repeat(10.0 ** rng.uniform(-7, 4, n // 32), 32).astype(np.float32)
@@ -111,11 +125,11 @@ GEMM_SHAPES = [(1, 4096, 4096), (1, 1024, 2048), (4, 256, 512), (16, 512, 1024),
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
-def test_fp8_gemm_matches_oracle(m, n, k):
+def test_fp8_gemm_matches_oracle(m, n, k, gemm_path):
     rng = np.random.default_rng(1000 + m + n + k)
     aq, as_, wq, ws = _quantised_case(rng, m, n, k, False)
     want = O.gemm_q(aq, as_, m, wq, ws, n, k, False)
-    announce("fp8_gemm m=%d n=%d k=%d" % (m, n, k))
+    announce("fp8_gemm %s m=%d n=%d k=%d" % (gemm_path, m, n, k))
     out = torch.empty((m, n), dtype=torch.float32, device=DEV)
     L.fp8_gemm(dev(aq), dev(as_), dev(wq), dev(ws), out, m, n, k)
     assert_close(host(out), want, GEMM_TOL, "fp8_gemm %dx%dx%d" % (m, n, k))
@@ -134,11 +148,11 @@ def test_fp8_gemm_matches_oracle(m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (8, 512, 1024), (128, 256, 2048),
                                    (33, 80, 512)])
-def test_fp4_gemm_matches_oracle(m, n, k):
+def test_fp4_gemm_matches_oracle(m, n, k, gemm_path):
     rng = np.random.default_rng(2000 + m + n + k)
     aq, as_, wq, ws = _quantised_case(rng, m, n, k, True)
     want = O.gemm_q(aq, as_, m, wq, ws, n, k, True)
-    announce("fp4_gemm m=%d n=%d k=%d" % (m, n, k))
+    announce("fp4_gemm %s m=%d n=%d k=%d" % (gemm_path, m, n, k))
     out = torch.empty((m, n), dtype=torch.float32, device=DEV)
     L.fp4_gemm(dev(aq), dev(as_), dev(wq), dev(ws), out, m, n, k)
     assert_close(host(out), want, GEMM_TOL, "fp4_gemm %dx%dx%d" % (m, n, k))
@@ -146,7 +160,7 @@ def test_fp4_gemm_matches_oracle(m, n, k):
 
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (128, 384, 4096), (20, 256, 512),
                                    (5, 64, 1152)])  # K/128 = 9: the general kernel
-def test_fp8_gemm_f32s_matches_oracle(m, n, k):
+def test_fp8_gemm_f32s_matches_oracle(m, n, k, gemm_path):
     rng = np.random.default_rng(3000 + m + n + k)
     x = activations(rng, m, k)
     wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
@@ -165,13 +179,13 @@ def test_fp8_gemm_f32s_matches_oracle(m, n, k):
 
 
 @pytest.mark.parametrize("n", [4096, 12288, 2048])
-def test_fp8_gemm_full_size_vs_fp64_dequant(n):
+def test_fp8_gemm_full_size_vs_fp64_dequant(n, gemm_path):
     """BASELINE config 2 shapes (M=128, K=4096) against an f64 matmul of the
     dequantised operands on the device (too large for the scalar oracle)."""
     m, k = 128, 4096
     gen = torch.Generator(device=DEV)
     gen.manual_seed(n)
-    announce("fp8_gemm full m=%d n=%d k=%d" % (m, n, k))
+    announce("fp8_gemm full %s m=%d n=%d k=%d" % (gemm_path, m, n, k))
     x = torch.randn((m, k), device=DEV, generator=gen)
     x = torch.where(torch.rand((m, k), device=DEV, generator=gen) < 0.01, x * 20, x)
     w = torch.randn((n, k), device=DEV, generator=gen) * 0.02
@@ -198,3 +212,25 @@ def test_gemm_rejects_bad_shapes():
         L.fp8_gemm(a, a, a, a, out, 1, 16, 100)     # K % 128 != 0
     with pytest.raises(RuntimeError, match="unsupported shape"):
         L.fp8_gemm(a, a, a, a, out, 1, 10, 128)     # N % 16 != 0
+
+
+def test_split_k_is_deterministic_and_reusable():
+    """Split-K tickets reset themselves: repeated calls (and a different shape
+    in between) give bit-identical results."""
+    rng = np.random.default_rng(4000)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    L.set_gemm_workspace(ws)
+    try:
+        outs = []
+        for m, n, k in [(128, 512, 4096), (40, 192, 2048), (128, 512, 4096), (128, 512, 4096)]:
+            aq, as_, wq, ws_ = _quantised_case(np.random.default_rng(4000 + m + n), m, n, k, False)
+            announce("split-k repeat m=%d n=%d k=%d" % (m, n, k))
+            out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+            L.fp8_gemm(dev(aq), dev(as_), dev(wq), dev(ws_), out, m, n, k)
+            outs.append(host(out))
+        assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+        assert np.array_equal(outs[0].view(np.uint32), outs[3].view(np.uint32))
+    finally:
+        torch.cuda.synchronize()
+        L.set_gemm_workspace(None)
+    del rng

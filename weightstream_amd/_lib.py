@@ -55,6 +55,8 @@ SIGNATURES = {
     "ws_weight_quant_fp8": (_i, [_p, _p, _p, _i64, _i64, _p]),
     "ws_packed_fp4_scale_bytes": (C.c_size_t, [_i64, _i64]),
     "ws_prepack_fp4": (_i, [_p, _p, _i64, _i64, _p, _p, _p]),
+    "ws_gemm_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
+    "ws_set_gemm_workspace": (_i, [_p, C.c_size_t, _p]),
     "ws_fp8_gemm": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_bf16": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),

@@ -468,6 +468,309 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     return launch_status();
 }
 
+// ---- split-K GEMM with the A block in LDS ---------------------------------
+// For M-batch shapes every CU would otherwise pull all of A through L2 (the
+// L2->CU rate, ~14 TB/s for the whole chip, bounds a 16-column strip kernel at
+// M=128, K=4096 near 9 us). Here a workgroup owns a 128 x 64 output tile and a
+// K range of at most 8 steps (1024 K): its A block (128 x <=1024 e4m3 + scales)
+// is copied into LDS once by direct global->LDS loads, and its 64 columns of W
+// stream from HBM in two register stages of four 128-K steps. The 8 waves own
+// 32 x 32 sub-tiles (2 x 2 MFMA fragments), so every A and W fragment feeds two
+// MFMA tiles. With S > 1 K ranges the splits write f32 partials to the
+// workspace and sk_reduce_kernel adds them in split order (deterministic).
+// Workgroups are numbered so that the S splits of a tile share an XCD
+// (dispatch goes round-robin over the 8 XCDs).
+constexpr int kSkBM = 128, kSkBN = 64, kSkU = 4, kSkMaxSteps = 2 * kSkU;
+constexpr int kSkThreads = 512;
+
+template <bool BFP4>
+struct SkStage {
+    uint4 b[kSkU][2][BFP4 ? 1 : 2];  // W: 2 column fragments
+    uint32_t sb[kSkU][2];            // UE8M0 weight scale of the lane's K block
+    float sbf[kSkU];                 // f32 weight scale (128-block; uniform)
+};
+
+// Copy rows of `row_bytes` (row i at src(i)) into an LDS image with a row
+// pitch of `pitch` bytes (>= row_bytes; the padding spreads rows over the LDS
+// banks), `total` = rows * pitch, with direct loads of PIECE bytes per lane
+// (16 or 4). Padding bytes get a copy of the row's last piece.
+template <int PIECE, class Src>
+__device__ __forceinline__ void sk_dma(Src src, int row_bytes, int pitch, int total, uint8_t *lds,
+                                       int w, int lane) {
+    const int per = 64 * PIECE;
+    const int n = (total + per - 1) / per;
+    for (int c = w; c < n; c += kSkThreads / 64) {
+        const int o = min(c * per + lane * PIECE, total - PIECE);
+        const int row = o / pitch, col = min(o - row * pitch, row_bytes - PIECE);
+        const void *gp = (const void *)(src(row) + col);
+        auto *lp = (__attribute__((address_space(3))) void *)(lds + c * per);
+        if constexpr (PIECE == 16) __builtin_amdgcn_global_load_lds(gp, lp, 16, 0, 0);
+        else __builtin_amdgcn_global_load_lds(gp, lp, 4, 0, 0);
+    }
+}
+
+template <bool BFP4, int SMODE, int OMODE, bool EXACT>
+__global__ __launch_bounds__(kSkThreads) void gemm_sk_kernel(
+    const uint8_t *A, const void *SA, const uint8_t *B, const void *SB,
+    void *__restrict__ C, int M, int N, int K, int S, int ntn, int tiles,
+    float *__restrict__ part) {
+    extern __shared__ __align__(16) uint8_t sk_lds[];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    // XCD-aware numbering: ids x, x+8, x+16, ... hold the tiles t = x (mod 8)
+    const int id = blockIdx.x, xcd = id & 7, q = id >> 3;
+    const int tile = xcd + 8 * (q / S), s = q % S;
+    if (tile >= tiles) return;  // whole workgroup
+    const int mb = tile / ntn, nt = tile % ntn;
+    const int m0 = mb * kSkBM, n0 = nt * kSkBN;
+    const int ksteps = K / 128, kbn = K / 32, kb128 = K / 128;
+    const int ka = s * ksteps / S, kz = (s + 1) * ksteps / S, nks = kz - ka;  // nks <= 8
+    const int kr = nks * 128;                           // A bytes per row
+    const int kp = kr + 16;                             // LDS row pitch (bank spread)
+    uint8_t *a_l = sk_lds;                              // [128][kp] e4m3
+    uint8_t *as_l = sk_lds + (size_t)kSkBM * kp;        // UE8M0 [128][nks*4] or f32 [128][nks]
+    const int wm = w & 3, wn = w >> 2;
+
+    // W columns n0 + 32 wn + 16 j + r, steps [ka, kz)
+    const uint8_t *brow[2];
+    const uint8_t *sbrow[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = min(n0 + 32 * wn + 16 * j + r, N - 1);
+        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + g * 16
+                       : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
+        sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
+    }
+    const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
+    auto load = [&](SkStage<BFP4> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < kSkU; u++) {
+            const int ks = max(min(ks0 + u, kz - 1), 0);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if (BFP4) {
+                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                } else {
+                    const uint8_t *p = brow[j] + (size_t)ks * 128;
+                    st.b[u][j][0] = ldg16_stream(p);
+                    st.b[u][j][BFP4 ? 0 : 1] = ldg16_stream(p + (EXACT ? 16 : 64));
+                }
+                if (SMODE == kUe8m0) st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
+            }
+            if (SMODE == kF32s) st.sbf[u] = sbf_row[ks];
+        }
+    };
+    // 1. the A block and its scales into LDS (rows past M repeat row M-1), issued
+    //    first so that a wait for W stage 0 also covers them
+    sk_dma<16>([&](int i) { return A + (size_t)min(m0 + i, M - 1) * K + (size_t)ka * 128; }, kr,
+               kp, kSkBM * kp, a_l, w, lane);
+    if (SMODE == kUe8m0)
+        sk_dma<4>([&](int i) {
+            return (const uint8_t *)SA + (size_t)min(m0 + i, M - 1) * kbn + ka * 4; },
+                  nks * 4, nks * 4, kSkBM * nks * 4, as_l, w, lane);
+    else
+        sk_dma<4>([&](int i) {
+            return (const uint8_t *)((const float *)SA + (size_t)min(m0 + i, M - 1) * kb128 + ka); },
+                  nks * 4, nks * 4, kSkBM * nks * 4, as_l, w, lane);
+    mem_order();
+    // 2. the two W stages
+    SkStage<BFP4> s0, s1;
+    load(s0, ka);
+    mem_order();
+    load(s1, ka + kSkU);
+    mem_order();
+    // wait until at most stage 1's weight loads are outstanding (a lower bound
+    // on the loads stage 1 issues: its scale loads only make the wait
+    // stricter): this wave's LDS copies and stage 0 have landed
+    constexpr int kStage1Loads = kSkU * 2 * (BFP4 ? 1 : 2);
+    __builtin_amdgcn_s_waitcnt((kStage1Loads & 15) | ((kStage1Loads >> 4) << 14) | (7 << 4) |
+                               (15 << 8));
+    raw_barrier();
+
+    // 3. multiply
+    v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const SkStage<BFP4> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < kSkU; u++) {
+            const int ks = ks0 + u;
+            if (ks >= kz) continue;  // uniform
+            const int kl = ks - ka;
+            if (EXACT) {
+                v8bf bq[2][4];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float sbv = SMODE == kUe8m0 ? e8m0_to_f32(st.sb[u][j] & 0xFF) : 1.0f;
+                    if (BFP4) cvt_fp4x32(st.b[u][j][0], sbv, bq[j]);
+                    else cvt_fp8x32(st.b[u][j][0], st.b[u][j][BFP4 ? 0 : 1], sbv, bq[j]);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int ml = 32 * wm + 16 * i + r;
+                    const uint8_t *ap = a_l + ml * kp + kl * 128 + g * 32;
+                    const float sav = SMODE == kUe8m0 ? e8m0_to_f32(as_l[ml * nks * 4 + kl * 4 + g])
+                                                      : 1.0f;
+                    v8bf aq[4];
+                    cvt_fp8x32(*(const uint4 *)ap, *(const uint4 *)(ap + 16), sav, aq);
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        if (SMODE == kUe8m0) {
+                            acc[i][j] = mfma_bf16_k128(aq, bq[j], acc[i][j]);
+                        } else {
+                            const v4f pr = mfma_bf16_k128(aq, bq[j], v4f{0.f, 0.f, 0.f, 0.f});
+                            const float *sar = (const float *)as_l + (32 * wm + 16 * i + 4 * g) * nks + kl;
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                acc[i][j][v] = acc[i][j][v] + pr[v] * (sar[v * nks] * st.sbf[u]);
+                        }
+                    }
+                }
+            } else {
+                v8i bf[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    bf[j] = BFP4 ? frag_from4(st.b[u][j][0])
+                                 : frag_from(st.b[u][j][0], st.b[u][j][BFP4 ? 0 : 1]);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const int ml = 32 * wm + 16 * i + r;
+                    const uint8_t *ap = a_l + ml * kp + kl * 128 + g * 16;
+                    const v8i af = frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64));
+#pragma unroll
+                    for (int j = 0; j < 2; j++) {
+                        if (SMODE == kUe8m0) {
+                            const int sa = as_l[ml * nks * 4 + kl * 4 + g];
+                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(af, bf[j], acc[i][j], sa,
+                                                                             (int)st.sb[u][j])
+                                             : mfma_scaled<kFmtFp8, kFmtFp8>(af, bf[j], acc[i][j], sa,
+                                                                             (int)st.sb[u][j]);
+                        } else {
+                            const v4f pr = mfma_scaled<kFmtFp8, kFmtFp8>(
+                                af, bf[j], v4f{0.f, 0.f, 0.f, 0.f}, kScaleOne, kScaleOne);
+                            const float *sar = (const float *)as_l + (32 * wm + 16 * i + 4 * g) * nks + kl;
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                acc[i][j][v] = acc[i][j][v] + pr[v] * (sar[v * nks] * st.sbf[u]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+    compute(s0, ka);
+    compute(s1, ka + kSkU);
+
+    // 4. store: C directly (one split) or the split's partial
+    auto store_c = [&](int row, int col, float v) {
+        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + col] = v;
+        else ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(v);
+    };
+    const size_t mpad = (size_t)((M + kSkBM - 1) / kSkBM) * kSkBM;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int col = n0 + 32 * wn + 16 * j + r;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int row = m0 + 32 * wm + 16 * i + 4 * g + v;
+                if (S == 1) {
+                    if (row < M && col < N) store_c(row, col, acc[i][j][v]);
+                } else if (col < N) {
+                    part[((size_t)s * mpad + row) * N + col] = acc[i][j][v];
+                }
+            }
+        }
+}
+
+// Sum of the S partials of every output in split order (deterministic);
+// the kernel boundary after gemm_sk_kernel makes them visible.
+template <int OMODE>
+__global__ __launch_bounds__(256) void sk_reduce_kernel(const float *__restrict__ part,
+                                                        void *__restrict__ C, int M, int N, int S,
+                                                        size_t mpad) {
+    const size_t o = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const size_t total = (size_t)M * N;
+    if (o >= total) return;
+    const size_t plane = mpad * N;
+    float4 acc = *(const float4 *)(part + o);
+    for (int q = 1; q < S; q++) {
+        const float4 v = *(const float4 *)(part + (size_t)q * plane + o);
+        acc.x = acc.x + v.x;
+        acc.y = acc.y + v.y;
+        acc.z = acc.z + v.z;
+        acc.w = acc.w + v.w;
+    }
+    if (OMODE == kOutF32) {
+        *(float4 *)((float *)C + o) = acc;
+    } else {
+        uint16_t *c = (uint16_t *)C + o;
+        *(uint2 *)c = uint2{(uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16),
+                            (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16)};
+    }
+}
+
+// Workspace for the split-K kernel, per device (ws_set_gemm_workspace).
+struct SkWorkspace {
+    uint8_t *ptr;
+    size_t bytes;
+};
+static SkWorkspace g_sk_ws[64];
+
+static SkWorkspace &sk_ws() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    return g_sk_ws[dev];
+}
+
+// Splits for (M, N, K): every split at most 8 steps, enough workgroups to
+// cover the CUs; 0 when the split-K kernel does not apply.
+static int sk_splits(int M, int N, int K, size_t ws_bytes) {
+    const int ksteps = K / 128;
+    const int tiles = ((M + kSkBM - 1) / kSkBM) * ((N + kSkBN - 1) / kSkBN);
+    int S = (ksteps + kSkMaxSteps - 1) / kSkMaxSteps;
+    const int want = (cu_count() + tiles - 1) / tiles;
+    if (want > S) S = want;
+    if (S > ksteps) S = ksteps;
+    const size_t mpad = (size_t)((M + kSkBM - 1) / kSkBM) * kSkBM;
+    if (S > 1 && (size_t)S * mpad * N * 4 > ws_bytes) return 0;
+    return S;
+}
+
+template <bool BFP4, int SMODE, int OMODE>
+static int launch_sk(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
+                     int m, int n, int k, hipStream_t stream) {
+    SkWorkspace &wsp = sk_ws();
+    if (!wsp.ptr) return -1;
+    const int S = sk_splits(m, n, k, wsp.bytes);
+    if (S <= 0) return -1;
+    const int ksteps = k / 128;
+    const int nks_max = (ksteps + S - 1) / S;
+    const int ntn = (n + kSkBN - 1) / kSkBN;
+    const int tiles = ((m + kSkBM - 1) / kSkBM) * ntn;
+    const size_t lds = (size_t)kSkBM * (nks_max * 128 + 16) + (size_t)kSkBM * nks_max * 4;
+    const unsigned grid = (unsigned)(8 * ((tiles + 7) / 8) * S);
+    float *part = (float *)wsp.ptr;
+    if (math_mode() == WS_MATH_NATIVE)
+        hipLaunchKernelGGL((gemm_sk_kernel<BFP4, SMODE, OMODE, false>), dim3(grid),
+                           dim3(kSkThreads), lds, stream, a, sa, b, sb, out, m, n, k, S, ntn,
+                           tiles, part);
+    else
+        hipLaunchKernelGGL((gemm_sk_kernel<BFP4, SMODE, OMODE, true>), dim3(grid),
+                           dim3(kSkThreads), lds, stream, a, sa, b, sb, out, m, n, k, S, ntn,
+                           tiles, part);
+    int rc = launch_status();
+    if (rc || S == 1) return rc;
+    const size_t mpad = (size_t)((m + kSkBM - 1) / kSkBM) * kSkBM;
+    const size_t quads = ((size_t)m * n + 3) / 4;
+    hipLaunchKernelGGL((sk_reduce_kernel<OMODE>), dim3((unsigned)((quads + 255) / 256)), dim3(256),
+                       0, stream, part, out, m, n, S, mpad);
+    return launch_status();
+}
+
 // General kernel configurations, used where the K-parallel kernel does not
 // stage a shape (f32 scales with K > 8192 or unaligned scale rows), or when
 // WS_GEMM_CFG forces one (0: 16 x 16 tiles, 1: 64 x 16 tiles) for measurements.
@@ -503,7 +806,15 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
     if (cfg < 0) {
         // K-parallel strips (one workgroup per 16 columns); -1: shape outside
         // what they stage, use the general kernel
-        int rc;
+        // split-K unless the 16-column strips alone fill the chip in one round
+        // (measured at M=128, K=4096: strips win at N=4096, split-K at N=2048
+        // and N=12288)
+        const int strips = N / 16, cus = cu_count();
+        const bool strips_fit = strips >= cus * 3 / 4 && strips <= cus * 3 / 2;
+        int rc = (M > 16 && !strips_fit)
+                     ? launch_sk<BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
+                     : -1;
+        if (rc >= 0) return rc;
         if (M <= 16) rc = launch_kp<1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         else if (M <= 32) rc = launch_kp<2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         else if (M <= 64) rc = launch_kp<4, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
@@ -526,6 +837,32 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
 using namespace ws;
 
 extern "C" {
+
+size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % 128) return 0;
+    const int64_t ksteps = k / 128;
+    int64_t S = (ksteps + kSkMaxSteps - 1) / kSkMaxSteps;
+    const int64_t tiles = ((m + kSkBM - 1) / kSkBM) * ((n + kSkBN - 1) / kSkBN);
+    const int64_t want = (cu_count() + tiles - 1) / tiles;
+    if (want > S) S = want;
+    if (S > ksteps) S = ksteps;
+    const int64_t mpad = (m + kSkBM - 1) / kSkBM * kSkBM;
+    return (size_t)(S > 1 ? S : 1) * mpad * n * 4;
+}
+
+int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream) {
+    (void)stream;
+    SkWorkspace &wsp = sk_ws();
+    if (!workspace || bytes == 0) {
+        wsp.ptr = nullptr;
+        wsp.bytes = 0;
+        return workspace ? WS_ERR_INVALID_ARG : WS_OK;
+    }
+    if ((uintptr_t)workspace & 255) return WS_ERR_INVALID_ARG;
+    wsp.ptr = (uint8_t *)workspace;
+    wsp.bytes = bytes;
+    return WS_OK;
+}
 
 int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                 float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {

@@ -144,19 +144,22 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
 // workgroup moves to a new tile.
 constexpr int kGThreads = 512;  // 8 waves
 
-// The tile's 32 A rows into LDS, a_l[32][K] and their UE8M0 bytes
+// The tile's 32 A rows into LDS, a_l[32][K + 16] (the 16-byte pad spreads the
+// rows of an MFMA fragment over the LDS banks) and their UE8M0 bytes
 // as_l[32][K/32], with direct global->LDS loads (global_load_lds_dwordx4 /
 // _dword: no VGPR staging). One instruction fills a contiguous 1 KB (256 B)
 // of the LDS image; lane l moves the 16 (4) bytes at image offset o, which
-// belong to row o / K (o / (K/32)). Row i of A starts at arow(i), its scales
-// at srow(i). Completion is awaited by the caller (vmcnt) before the barrier.
+// belong to row o / pitch (pad bytes repeat the row's last piece). Row i of A
+// starts at arow(i), its scales at srow(i). Completion is awaited by the
+// caller (vmcnt) before the barrier.
 template <class ARow, class SRow>
 __device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, int lane,
                                            uint8_t *a_l, uint8_t *as_l) {
-    const int nq = kTile * K / 1024;
+    const int pitch = K + 16, total = kTile * pitch;
+    const int nq = (total + 1023) / 1024;  // the last piece overhangs into the image's slack
     for (int c = w; c < nq; c += kGThreads / 64) {
-        const int o = c * 1024 + lane * 16;
-        const int row = o / K, col = o - row * K;
+        const int o = min(c * 1024 + lane * 16, total - 16);
+        const int row = o / pitch, col = min(o - row * pitch, K - 16);
         __builtin_amdgcn_global_load_lds((const void *)(arow(row) + col),
                                          (__attribute__((address_space(3))) void *)(a_l + c * 1024),
                                          16, 0, 0);
@@ -171,9 +174,13 @@ __device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, i
     }
 }
 
-// LDS bytes of the A tile image (scales padded to whole 256-byte pieces)
+// Bytes of the A image (rounded up to whole 1 KB pieces) and of the whole
+// LDS tile (scales padded to whole 256-byte pieces)
+__host__ __device__ constexpr size_t g_a_lds(int K) {
+    return ((size_t)kTile * (K + 16) + 1023) / 1024 * 1024;
+}
 __host__ __device__ constexpr size_t g_tile_lds(int K) {
-    return (size_t)kTile * K + ((size_t)kTile * (K / 32) + 255) / 256 * 256;
+    return g_a_lds(K) + ((size_t)kTile * (K / 32) + 255) / 256 * 256;
 }
 
 // One stage (steps [ks0, kend), at most kU) of a band times the two 16-slot A
@@ -195,7 +202,7 @@ __device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const 
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int slot = i * 16 + r;
-                const uint8_t *ap = a_l + slot * K + ks * 128 + g * 32;
+                const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 32;
                 v8bf aq[4];
                 cvt_fp8x32(*(const uint4 *)ap, *(const uint4 *)(ap + 16),
                            e8m0_to_f32(as_l[slot * (K / 32) + ks * 4 + g]), aq);
@@ -206,7 +213,7 @@ __device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const 
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int slot = i * 16 + r;
-                const uint8_t *ap = a_l + slot * K + ks * 128 + g * 16;
+                const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 16;
                 acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(
                     frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64)), b, acc[i],
                     (int)as_l[slot * (K / 32) + ks * 4 + g], (int)sbyte);
@@ -235,8 +242,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq, uint8_t *__restrict__ hs, int dim,
     int inter, int n_experts, int top_k, float limit) {
     extern __shared__ __align__(16) uint8_t g_lds[];
-    uint8_t *a_l = g_lds;                           // [32][dim]
-    uint8_t *as_l = g_lds + (size_t)kTile * dim;    // [32][dim/32] (+ padding)
+    uint8_t *a_l = g_lds;                           // [32][dim + 16]
+    uint8_t *as_l = g_lds + g_a_lds(dim);            // [32][dim/32] (+ padding)
     __shared__ float gu[2][2][kTile][kTile + 1];
     __shared__ float rw_l[kTile];  // routing weight of each slot of the tile (0: padding)
     __shared__ int pad_l[kTile];
@@ -335,8 +342,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const int32_t *__restrict__ num_tiles, const uint8_t *__restrict__ w2,
     const uint8_t *__restrict__ s2, float *__restrict__ out, int dim, int inter, int n_experts) {
     extern __shared__ __align__(16) uint8_t g_lds[];
-    uint8_t *a_l = g_lds;                             // [32][inter]
-    uint8_t *as_l = g_lds + (size_t)kTile * inter;    // [32][inter/32] (+ padding)
+    uint8_t *a_l = g_lds;                             // [32][inter + 16]
+    uint8_t *as_l = g_lds + g_a_lds(inter);          // [32][inter/32] (+ padding)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int k1 = inter / 128, km = min(kU, k1);

@@ -88,6 +88,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
 // issue order and a wait for them does not cover later loads).
 __device__ __forceinline__ void mem_order() { __asm__ volatile("" ::: "memory"); }
 
+// Workgroup barrier with no memory-model fences: the caller has already waited
+// (s_waitcnt) for whatever other waves will read, e.g. its own direct
+// global->LDS copies; global loads issued before it stay in flight. The
+// compiler-only barriers keep memory accesses on their side of it.
+__device__ __forceinline__ void raw_barrier() {
+    mem_order();
+    __builtin_amdgcn_s_barrier();
+    mem_order();
+}
+
 // Barrier that orders LDS only: global loads issued before it stay in flight.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");

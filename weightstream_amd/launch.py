@@ -139,6 +139,21 @@ def prepack_fp4_new(w, s, rows, cols, stream=None):
 
 
 # ---- GEMMs (launch.rs:344-377, 717-804) -------------------------------------
+def gemm_workspace_size(m, n, k):
+    """Bytes of split-K workspace the GEMMs need for (m, n, k)."""
+    return int(_lib.load().ws_gemm_workspace_size(m, n, k))
+
+
+def set_gemm_workspace(ws, stream=None):
+    """Register (a uint8 device tensor) or clear (None) the split-K workspace
+    of the current device; the caller keeps `ws` alive while it is set."""
+    if ws is None:
+        _call("ws_set_gemm_workspace", None, 0, _s(stream))
+    else:
+        _call("ws_set_gemm_workspace", _ptr(ws), ws.numel() * ws.element_size(), _s(stream))
+
+
+
 def fp8_gemm(a, sa, b, sb, out, m, n, k, stream=None):
     _call("ws_fp8_gemm", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k, _s(stream))
 
