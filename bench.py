@@ -88,9 +88,9 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
     ws = torch.empty(L.moe_decode_workspace_size(DIM, INTER, TOPK), dtype=torch.uint8, device=dev)
 
     def step(t, stream):
-        L.moe_topk(logits[t], bias, None, idx[t], wts[t], 1, E, TOPK, L.SCORE_SIGMOID, 1.0, True,
-                   1.0, stream=stream)
-        L.moe_decode(x[t], idx[t], wts[t], *packed, y[t], DIM, INTER, E, TOPK, ws, stream=stream)
+        # routing fused into the gate/up kernel (picks land in idx / wts)
+        L.moe_decode_route(logits[t], bias, L.SCORE_SIGMOID, 1.0, 1, 1.0, x[t], *packed, y[t],
+                           idx[t], wts[t], DIM, INTER, E, TOPK, ws, stream=stream)
 
     # eager pass: results for the parity check and the per-kernel timing inputs
     s = torch.cuda.current_stream()

@@ -237,6 +237,22 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w,
                   int64_t n_experts, int64_t top_k, float swiglu_limit, void *workspace,
                   size_t workspace_bytes, ws_stream_t stream);
 
+/* moe_select (launch.rs:1043, moe.cu:48) fused with the routed MoE for one
+ * token: top-k of the scores of logits[E] (score_func, gate_temp) + bias,
+ * weights normalised as ws_moe_topk's norm_topk_prob says and scaled by
+ * route_scale, written to topk_idx / topk_w [top_k] (top-k order, identical to
+ * ws_moe_topk's), then ws_moe_decode's y. The gate/up kernel computes the
+ * routing itself, so the step is two kernels. Softmax scores (a sequential
+ * sum over E) and dim > 8192 run ws_moe_topk then ws_moe_decode. Workspace as
+ * ws_moe_decode. */
+int ws_moe_decode_route(const float *logits, const float *bias, int score_func, float gate_temp,
+                        int norm_topk_prob, float route_scale, const float *x, const uint8_t *w1,
+                        const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                        const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                        int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                        float swiglu_limit, void *workspace, size_t workspace_bytes,
+                        ws_stream_t stream);
+
 /* ---------------------------------------------------------------------
  * Routed experts, M tokens (grouped prefill / batched decode). Replaces the
  * TileLang pipeline of engine.rs:4125-4243 (moe_dispatch_tl launch.rs:430,

@@ -198,3 +198,33 @@ def test_prepack_fp4_layout():
                     off = ((rt * ksn + ks) * 64 + lane) * 16
                     assert np.array_equal(pw[off:off + 16], w[r, ks * 64 + g * 16:ks * 64 + g * 16 + 16])
                     assert ps[((rt * ks8 + ks // 8) * 64 + lane) * 8 + ks % 8] == s[r, ks * 4 + g]
+
+
+@pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (64, 2048, 768, 6, 2),
+                                                 (100, 1024, 512, 4, 1), (32, 1024, 256, 4, 0)])
+def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
+    """The routing computed inside the gate/up kernel gives the same picks and
+    weights as ws_moe_topk (bit for bit) and the same y as ws_moe_decode on
+    them (bit for bit: same kernels downstream). score 0 (softmax) takes the
+    unfused path."""
+    rng = np.random.default_rng(740 + E)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(740 + E)
+    packed = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
+    logits = dev(rng.standard_normal(E).astype(np.float32))
+    bias = dev((rng.standard_normal(E) * 0.1).astype(np.float32))
+    x = dev(rng.standard_normal(dim).astype(np.float32))
+    announce("moe_decode_route E=%d dim=%d inter=%d k=%d score=%d" % (E, dim, inter, k, score))
+    idx1 = torch.full((k,), -5, dtype=torch.int32, device=DEV)
+    w1_ = torch.zeros(k, dtype=torch.float32, device=DEV)
+    L.moe_topk(logits, bias, None, idx1, w1_, 1, E, k, score, 1.0, True, 1.0)
+    y1 = _run_decode(x, idx1, w1_, packed, dim, inter, E, k)
+    ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
+    idx2 = torch.full((k,), -5, dtype=torch.int32, device=DEV)
+    w2_ = torch.zeros(k, dtype=torch.float32, device=DEV)
+    y2 = torch.empty(dim, dtype=torch.float32, device=DEV)
+    L.moe_decode_route(logits, bias, score, 1.0, 1, 1.0, x, *packed, y2, idx2, w2_, dim, inter, E,
+                       k, ws)
+    assert torch.equal(idx1, idx2)
+    assert np.array_equal(host(w1_).view(np.uint32), host(w2_).view(np.uint32))
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))

@@ -76,6 +76,8 @@ SIGNATURES = {
     "ws_expert_reduce": (_i, [_p] * 6 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
     "ws_moe_decode": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
+    "ws_moe_decode_route": (_i, [_p, _p, _i, _f, _i, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                                 _i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
     "ws_moe_dispatch": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_grouped_glu_quant": (_i, [_p] * 12 + [_i64, _i64, _i64, _i64, _i64, _f, _p]),
     "ws_moe_grouped_down": (_i, [_p] * 7 + [_i64, _i64, _i64, _i64, _p]),

@@ -29,6 +29,7 @@
 //    expert id, one f32 add per expert like the reference's acc_f32 chain.
 #include "ws_internal.hpp"
 #include "ws_pack.hpp"
+#include "ws_route.hpp"
 
 namespace ws {
 
@@ -50,10 +51,11 @@ struct WavePicks {
     int nv;    // number of valid picks
 };
 
-__device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, int n_experts,
-                                                int lane) {
+// from lane j's pick (expert id e_lane for lanes < top_k)
+__device__ __forceinline__ WavePicks wave_picks_of(int e_lane, int top_k, int n_experts,
+                                                   int lane) {
     WavePicks wp;
-    wp.e = lane < top_k ? idx[lane] : -1;
+    wp.e = lane < top_k ? e_lane : -1;
     const bool valid = lane < top_k && wp.e >= 0 && wp.e < n_experts;
     int rank = 0;
     for (int i = 0; i < top_k; i++) {
@@ -64,6 +66,11 @@ __device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, i
     wp.rank = valid ? rank : -1;
     wp.nv = __popcll(__ballot(valid));
     return wp;
+}
+
+__device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, int n_experts,
+                                                int lane) {
+    return wave_picks_of(lane < top_k ? idx[lane] : -1, top_k, n_experts, lane);
 }
 
 // expert id of the valid pick with rank p (0 if there is none)
@@ -263,10 +270,25 @@ __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, i
     }
 }
 
-template <bool EXACT, bool XF32>
+// Routing computed inside the gate/up kernel (moe_select fused in): every
+// wave runs wave_scores + wave_select on the token's logits, and workgroup
+// (0, 0) publishes the picks for the down kernel and the caller.
+struct RouteArgs {
+    const float *logits, *bias;
+    int score_func;
+    float gate_temp;
+    int norm;
+    float route_scale;
+    int32_t *idx_out;
+    float *w_out;
+};
+
+// CPL > 0: route in the kernel (CPL candidates per lane, E <= 64 CPL);
+// CPL == 0: picks from idx / topk_w.
+template <bool EXACT, bool XF32, int CPL>
 __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const uint8_t *xq, const uint8_t *xs, const float *xf,
-    const int32_t *__restrict__ idx, const float *__restrict__ topk_w,
+    const int32_t *__restrict__ idx, const float *__restrict__ topk_w, RouteArgs ra,
     const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
     uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit,
@@ -278,15 +300,14 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     uint8_t *xs_l = lds + dim;
     __shared__ float gu[kGluKParts][2][32];
     const int slot = blockIdx.y;
-    const int e = idx[slot];
-    if (e < 0 || e >= n_experts) return;  // whole workgroup
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int ksteps = dim / 128;
 
     // waves -> (matrix, 16-row half of a 32-row tile, sub): with tpw == 2
     // the workgroup owns tiles 2x, 2x+1 and `sub` picks the tile (a wave
     // streams the whole K); with tpw == 1 it owns tile x and `sub` picks the
-    // K half. Every wave also converts 1/8 of the token into LDS.
+    // K half. Every wave also converts 1/8 of the token into LDS; its token
+    // loads go out first (they do not depend on the routing).
     const int mat = (w >> 1) & 1, half = w & 1, sub = w >> 2;
     const int kparts = tpw == 2 ? 1 : kGluKParts;
     // token share: blocks [tb0, tb1) (f32) or bytes [tc0, tc1) (e4m3)
@@ -297,6 +318,30 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     if (XF32) tok_load_f32(tr, xf, tb0, tb1, lane);
     else share_load_fp8(tr.b, xq, xs, tc0, tc1, lane);
     mem_order();
+
+    // the slot's expert and routing weight, and the picks' ranks
+    int e;
+    float rw;
+    WavePicks wp;
+    if constexpr (CPL > 0) {
+        float sc[CPL];
+        wave_scores<CPL>(ra.logits, n_experts, ra.score_func, ra.gate_temp, lane, sc);
+        int pk;
+        float pw;
+        wave_select<CPL>(sc, ra.bias, n_experts, top_k, ra.norm, ra.route_scale, lane, pk, pw);
+        e = __builtin_amdgcn_readlane(pk, slot);
+        rw = readlane_f(pw, slot);
+        wp = wave_picks_of(pk, top_k, n_experts, lane);
+        if (blockIdx.x == 0 && slot == 0 && w == 0 && lane < top_k) {
+            ra.idx_out[lane] = pk;
+            ra.w_out[lane] = pw;
+        }
+    } else {
+        e = idx[slot];
+        rw = topk_w[slot];
+        wp = wave_picks(idx, top_k, n_experts, lane);
+    }
+    if (e < 0 || e >= n_experts) return;  // whole workgroup (a pick another rank owns)
 
     const int tile = blockIdx.x * tpw + (tpw == 2 ? sub : 0);
     int k0, k1;
@@ -339,11 +384,10 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
         u = rclamp(u, -limit, limit);
         g = fminf(g, limit);
     }
-    const float rw = topk_w[slot];
     float h = ws_silu(g) * u * rw;
     uint32_t sb;
     uint32_t qb = quant_fp8_block32(h, &sb);
-    const int rank = wave_rank_of_slot(wave_picks(idx, top_k, n_experts, lane), slot);
+    const int rank = wave_rank_of_slot(wp, slot);
     if (lane < 32) {
         hq[(size_t)rank * inter + otile * 32 + n] = (uint8_t)qb;
         if (n == 0) hs[(size_t)rank * (inter / 32) + otile] = (uint8_t)sb;
@@ -462,24 +506,38 @@ extern "C" {
 namespace ws {
 
 static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf,
-                      const int32_t *topk_idx, const float *topk_w, const uint8_t *w1,
-                      const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, uint8_t *hq,
-                      uint8_t *hs, int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
-                      float swiglu_limit, hipStream_t stream) {
+                      const int32_t *topk_idx, const float *topk_w, const RouteArgs *ra,
+                      const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
+                      uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter, int64_t n_experts,
+                      int64_t top_k, float swiglu_limit, hipStream_t stream) {
     // two tiles per workgroup when that still gives every CU a workgroup:
-    // one resident round of 9-wave workgroups, each wave streaming whole K rows
+    // one resident round of 8-wave workgroups, each wave streaming whole K rows
     const int tpw = (inter / 32) * top_k >= 512 ? 2 : 1;
     dim3 grid((unsigned)(inter / 32 / tpw), (unsigned)top_k);
     const bool exact = math_mode() == WS_MATH_EXACT;
     size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
-#define WS_GLU(EX, XF)                                                                        \
-    hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF>), grid, dim3(kDecThreads), lds, stream, \
-                       xq, xs, xf, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, (int)dim,         \
-                       (int)inter, (int)n_experts, (int)top_k, swiglu_limit, tpw)
-    if (exact) {
-        if (xf) WS_GLU(true, true); else WS_GLU(true, false);
+    const RouteArgs none{};
+#define WS_GLU(EX, XF, CPL, RA)                                                                  \
+    hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF, CPL>), grid, dim3(kDecThreads), lds,      \
+                       stream, xq, xs, xf, topk_idx, topk_w, RA, w1, s1, w3, s3, hq, hs,          \
+                       (int)dim, (int)inter, (int)n_experts, (int)top_k, swiglu_limit, tpw)
+    if (ra) {  // routed in the kernel (f32 token)
+        const int cpl = n_experts <= 128 ? 2 : n_experts <= 256 ? 4 : n_experts <= 384 ? 6
+                      : n_experts <= 512 ? 8 : 16;
+#define WS_GLU_R(EX)                                                  \
+        switch (cpl) {                                                \
+            case 2: WS_GLU(EX, true, 2, *ra); break;                  \
+            case 4: WS_GLU(EX, true, 4, *ra); break;                  \
+            case 6: WS_GLU(EX, true, 6, *ra); break;                  \
+            case 8: WS_GLU(EX, true, 8, *ra); break;                  \
+            default: WS_GLU(EX, true, 16, *ra); break;                \
+        }
+        if (exact) { WS_GLU_R(true) } else { WS_GLU_R(false) }
+#undef WS_GLU_R
+    } else if (exact) {
+        if (xf) WS_GLU(true, true, 0, none); else WS_GLU(true, false, 0, none);
     } else {
-        if (xf) WS_GLU(false, true); else WS_GLU(false, false);
+        if (xf) WS_GLU(false, true, 0, none); else WS_GLU(false, false, 0, none);
     }
 #undef WS_GLU
     return launch_status();
@@ -519,8 +577,8 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
     if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
         ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
-    return glu_launch(xq, xs, nullptr, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                      n_experts, top_k, swiglu_limit, stream);
+    return glu_launch(xq, xs, nullptr, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
+                      inter, n_experts, top_k, swiglu_limit, stream);
 }
 
 int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *topk_w,
@@ -536,8 +594,8 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
     if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
         ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
-    return glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                      n_experts, top_k, swiglu_limit, stream);
+    return glu_launch(nullptr, nullptr, x, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
+                      inter, n_experts, top_k, swiglu_limit, stream);
 }
 
 int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
@@ -578,16 +636,54 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, 
     uint8_t *hs = hq + align256(top_k * inter);
     if (dim <= kMaxDimF32) {
         // the gate/up kernel quantises x itself (the act_quant_fp8_emit rule)
-        rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                        n_experts, top_k, swiglu_limit, stream);
+        rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs,
+                        dim, inter, n_experts, top_k, swiglu_limit, stream);
     } else {
         uint8_t *xq = hs + align256(top_k * (inter / 32));
         uint8_t *xs = xq + align256(dim);
         rc = ws_emit8(x, xq, xs, dim, stream);
         if (rc) return rc;
-        rc = glu_launch(xq, xs, nullptr, topk_idx, topk_w, w1, s1, w3, s3, hq, hs, dim, inter,
-                        n_experts, top_k, swiglu_limit, stream);
+        rc = glu_launch(xq, xs, nullptr, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
+                        inter, n_experts, top_k, swiglu_limit, stream);
     }
+    if (rc) return rc;
+    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+}
+
+int ws_moe_decode_route(const float *logits, const float *bias, int score_func, float gate_temp,
+                        int norm_topk_prob, float route_scale, const float *x, const uint8_t *w1,
+                        const uint8_t *s1, const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                        const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                        int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                        float swiglu_limit, void *workspace, size_t workspace_bytes,
+                        ws_stream_t stream) {
+    if (!logits || !bias || !topk_idx || !topk_w) return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExperts || top_k > kMaxTopk || top_k > n_experts) return WS_ERR_SHAPE;
+    if (score_func < WS_SCORE_SOFTMAX || score_func > WS_SCORE_SQRTSOFTPLUS) return WS_ERR_INVALID_ARG;
+    if (score_func == WS_SCORE_SOFTMAX || dim > kMaxDimF32) {
+        // the sequential softmax sum, or a token too wide for the fused
+        // quantisation: route first, then the two expert kernels
+        int rc = ws_moe_topk(logits, bias, nullptr, topk_idx, topk_w, 1, n_experts, top_k,
+                             score_func, gate_temp, norm_topk_prob, route_scale, stream);
+        if (rc) return rc;
+        return ws_moe_decode(x, topk_idx, topk_w, w1, s1, w3, s3, w2, s2, y, dim, inter, n_experts,
+                             top_k, swiglu_limit, workspace, workspace_bytes, stream);
+    }
+    if (!x || !workspace) return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (workspace_bytes < ws_moe_decode_workspace_size(dim, inter, top_k) || !aligned16(workspace))
+        return WS_ERR_INVALID_ARG;
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || !aligned16(w2) ||
+        ((uintptr_t)s1 & 7) || ((uintptr_t)s3 & 7) || ((uintptr_t)s2 & 7) || !w1 || !s1 || !w3 ||
+        !s3 || !w2 || !s2 || !y)
+        return WS_ERR_INVALID_ARG;
+    uint8_t *hq = (uint8_t *)workspace;
+    uint8_t *hs = hq + align256(top_k * inter);
+    const RouteArgs ra{logits, bias, score_func, gate_temp, norm_topk_prob, route_scale,
+                       topk_idx, topk_w};
+    rc = glu_launch(nullptr, nullptr, x, nullptr, nullptr, &ra, w1, s1, w3, s3, hq, hs, dim, inter,
+                    n_experts, top_k, swiglu_limit, stream);
     if (rc) return rc;
     return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
 }

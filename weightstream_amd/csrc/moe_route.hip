@@ -17,6 +17,7 @@
 // sqrtsoftplus uses the device logf and sqrtf; sqrtf is correctly rounded,
 // logf is within 1 ulp of glibc's (not bit-exact).
 #include "ws_internal.hpp"
+#include "ws_route.hpp"
 
 namespace ws {
 
@@ -71,66 +72,8 @@ __global__ __launch_bounds__(64) void gate_logits_kernel(const float *__restrict
     if (e < n_experts) logits[(size_t)m * n_experts + e] = s;
 }
 
-__device__ __forceinline__ float score_fn(float v, int score_func, float gate_temp) {
-    if (gate_temp != 1.0f) v = v / gate_temp;
-    if (score_func == WS_SCORE_SIGMOID) return ws_sigmoid(v);
-    if (score_func == WS_SCORE_SQRTSOFTPLUS) {
-        float sp = v > 20.0f ? v : logf(1.0f + ws_expf(v));
-        return sqrtf(sp);
-    }
-    return v;  // softmax handled by the caller, identity for given scores
-}
-
-// f32 total order (Rust f32::total_cmp) as an unsigned key: larger = greater.
-__device__ __forceinline__ uint32_t total_key_u(float v) {
-    int32_t b = (int32_t)__float_as_uint(v);
-    int32_t k = b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
-    return (uint32_t)k ^ 0x80000000u;
-}
-
-constexpr int kTopkThreads = 256;
-constexpr int kMaxExperts = 1024;
-constexpr int kMaxTopk = 16;
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        uint64_t o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
-// Wave max with DPP lane moves (no LDS permutes): quad swaps, half-row and
-// row mirrors, then row broadcasts 15 and 31 carry the maximum to lane 63.
-#define WS_DPP_MAX(v, ctrl, rmask)                                                           \
-    do {                                                                                    \
-        uint32_t o_ = (uint32_t)__builtin_amdgcn_update_dpp((int)(v), (int)(v), ctrl, rmask, \
-                                                            0xf, false);                    \
-        v = o_ > v ? o_ : v;                                                                \
-    } while (0)
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    WS_DPP_MAX(v, 0xB1, 0xf);   // quad_perm [1,0,3,2]
-    WS_DPP_MAX(v, 0x4E, 0xf);   // quad_perm [2,3,0,1]
-    WS_DPP_MAX(v, 0x141, 0xf);  // row_half_mirror
-    WS_DPP_MAX(v, 0x140, 0xf);  // row_mirror
-    WS_DPP_MAX(v, 0x142, 0xa);  // row_bcast:15 -> rows 1, 3
-    WS_DPP_MAX(v, 0x143, 0xc);  // row_bcast:31 -> rows 2, 3
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-#undef WS_DPP_MAX
-
-__device__ __forceinline__ float readlane_f(float v, int l) {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-// One wave per token row: scores, top-k selection, weights, all in registers.
-// Each lane keeps CPL candidates (expert e = lane + 64 c) as 64-bit keys
-// (total-order key of score+bias, then the complemented index so that ties
-// pick the lower index). A round takes each lane's best key, a 32-bit wave
-// max of the score halves and a ballot; only an exact score tie across lanes
-// needs the 64-bit wave max. Lane k keeps pick k and its score.
+// One wave per token row (wave_scores + wave_select of ws_route.hpp); the
+// softmax path keeps the reference's sequential sum (one lane, LDS).
 template <int CPL>
 __global__ __launch_bounds__(64) void topk_kernel(
     const float *__restrict__ logits, const float *__restrict__ bias, float *__restrict__ scores_out,
@@ -166,86 +109,21 @@ __global__ __launch_bounds__(64) void topk_kernel(
             sc[c] = e < n_experts ? sm[e] / s : 0.0f;
         }
     } else {
-        // logits, biases and the exp table all load at once
-        float v[CPL];
+        wave_scores<CPL>(lg, n_experts, score_func, gate_temp, lane, sc);
+    }
+    if (scores_out) {
 #pragma unroll
-        for (int c = 0; c < CPL; c++) v[c] = lg[min(lane + 64 * c, n_experts - 1)];
-        const uint64_t tab = ws_lane_exp2f_tab(lane);
-        if (gate_temp != 1.0f) {
-#pragma unroll
-            for (int c = 0; c < CPL; c++) v[c] = v[c] / gate_temp;
-        }
-        // score_fn on the lane-table exp (no table loads per value)
-        if (score_func == WS_SCORE_SIGMOID) {
-#pragma unroll
-            for (int c = 0; c < CPL; c++) sc[c] = ws_sigmoid_lanes(v[c], tab);
-        } else if (score_func == WS_SCORE_SQRTSOFTPLUS) {
-#pragma unroll
-            for (int c = 0; c < CPL; c++) {
-                const float ex = ws_expf_lanes(v[c], tab);
-                sc[c] = sqrtf(v[c] > 20.0f ? v[c] : logf(1.0f + ex));
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < CPL; c++) sc[c] = v[c];
+        for (int c = 0; c < CPL; c++) {
+            const int e = lane + 64 * c;
+            if (e < n_experts) scores_out[(size_t)m * n_experts + e] = sc[c];
         }
     }
-    float bv[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; c++) bv[c] = bias[min(lane + 64 * c, n_experts - 1)];
-    uint64_t cand[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const int e = lane + 64 * c;
-        if (scores_out && e < n_experts) scores_out[(size_t)m * n_experts + e] = sc[c];
-        cand[c] = e < n_experts
-                      ? ((uint64_t)total_key_u(sc[c] + bv[c]) << 32) | (uint32_t)(~(uint32_t)e)
-                      : 0ull;
-    }
-    int my_pick = 0;
-    float my_w = 0.0f;
-    for (int k = 0; k < top_k; k++) {
-        uint64_t best = cand[0];
-        int bc = 0;
-#pragma unroll
-        for (int c = 1; c < CPL; c++)
-            if (cand[c] > best) {
-                best = cand[c];
-                bc = c;
-            }
-        const uint32_t hk = (uint32_t)(best >> 32);
-        const uint32_t wk = wave_max_u32(hk);
-        uint64_t bal = __ballot(hk == wk);
-        if (__popcll(bal) > 1) {
-            // equal scores on several lanes: the larger full key (lower index)
-            const uint64_t full = wave_max_u64(hk == wk ? best : 0ull);
-            bal = __ballot(hk == wk && best == full);
-        }
-        const int win = __ffsll((long long)bal) - 1;
-        float sb = sc[0];
-#pragma unroll
-        for (int c = 1; c < CPL; c++) sb = c == bc ? sc[c] : sb;
-        const int e = __builtin_amdgcn_readlane(lane + 64 * bc, win);
-        const float w = readlane_f(sb, win);
-        if (lane == k) {
-            my_pick = e;
-            my_w = w;
-        }
-#pragma unroll
-        for (int c = 0; c < CPL; c++)
-            if (lane == win && c == bc) cand[c] = 0ull;
-    }
-    // norm 1: moe.rs:61 (only when top_k > 1); norm 2: moe_select's
-    // unconditional normalisation (moe.cu:84-88). The sum runs in top-k order.
-    float wout = my_w;
-    if ((norm == 1 && top_k > 1) || norm == 2) {
-        float s = -0.0f;
-        for (int k = 0; k < top_k; k++) s = s + readlane_f(my_w, k);
-        wout = my_w / (s + 1e-20f);
-    }
+    int my_pick;
+    float my_w;
+    wave_select<CPL>(sc, bias, n_experts, top_k, norm, route_scale, lane, my_pick, my_w);
     if (lane < top_k) {
         out_idx[(size_t)m * top_k + lane] = my_pick;
-        out_w[(size_t)m * top_k + lane] = wout * route_scale;
+        out_w[(size_t)m * top_k + lane] = my_w;
     }
 }
 
