@@ -17,8 +17,9 @@ block GEMM TFLOP/s at M=128"):
 Timing: the steps are captured once into a HIP graph (one node per kernel,
 no allocation, no memset) holding exactly `--steps` steps and replayed once;
 wall time between two device synchronisations brackets it. Per-kernel
-durations for the roofline come from HIP events recorded on the launch stream
-around batches of back-to-back launches of that kernel alone.
+durations (the roofline, the GEMMs, the prefill) come from HIP events around
+replays of a graph holding back-to-back calls of that kernel alone, so no host
+launch cost enters them.
 
     python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
 """
@@ -135,32 +136,16 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
         L.emit8(x[t], xq[t], xs[t], DIM, stream=s)
     torch.cuda.synchronize()
 
-    def timed(fn, reps_k, batches=5):
-        """Average kernel duration: `batches` batches of reps_k back-to-back
-        launches, each bracketed by two events on the launch stream (the
-        queue stays ahead of the GPU, so a batch measures kernel time, not
-        launch latency). Returns (average, median of the batch averages)."""
-        per = []
-        for _ in range(batches):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(s)
-            for i in range(reps_k):
-                fn(i % n_tokens)
-            b.record(s)
-            torch.cuda.synchronize()
-            per.append(a.elapsed_time(b) / reps_k)
-        per_sorted = sorted(per)
-        return sum(per) / len(per), per_sorted[len(per) // 2]
-
-    glu = lambda t: L.expert_glu_quant_x(x[t], idx[t], wts[t], w1, s1, w3, s3, hq[t], hs[t],
-                                         INTER, DIM, E, TOPK, stream=s)
-    red = lambda t: L.expert_reduce(hq[t], hs[t], w2, s2, idx[t], y[t], DIM, INTER, E, TOPK,
-                                    stream=s)
+    glu = lambda t, st: L.expert_glu_quant_x(x[t % n_tokens], idx[t % n_tokens], wts[t % n_tokens],
+                                             w1, s1, w3, s3, hq[t % n_tokens], hs[t % n_tokens],
+                                             INTER, DIM, E, TOPK, stream=st)
+    red = lambda t, st: L.expert_reduce(hq[t % n_tokens], hs[t % n_tokens], w2, s2, idx[t % n_tokens],
+                                        y[t % n_tokens], DIM, INTER, E, TOPK, stream=st)
     for t in range(n_tokens):
-        glu(t)
+        glu(t, s)
     reps_k = max(100, n_tokens)
-    glu_avg, glu_med = timed(glu, reps_k)
-    red_avg, red_med = timed(red, reps_k)
+    glu_avg, glu_med = graph_time(torch, glu, reps_k)
+    red_avg, red_med = graph_time(torch, red, reps_k)
     glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + 4 * DIM + TOPK * (INTER + INTER // 32)
     red_bytes = TOPK * (FP4_MAT + FP4_SC) + TOPK * (INTER + INTER // 32) + DIM * 4
     kern = {
@@ -175,6 +160,35 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
     return dict(ms_per_step=ms_per_step, gbs=gbs, step_bytes=step_bytes, kernels=kern,
                 slabs=slabs, logits=logits, bias=bias, x=x, idx=idx, wts=wts, y=y_eager,
                 steps=done)
+
+
+def graph_time(torch, fn, reps, replays=3):
+    """Per-call GPU time of fn(i, stream) for i in range(reps): the reps calls
+    are captured into one HIP graph, so the timed region holds no host launch
+    cost, and the graph is replayed `replays` times between two events on the
+    replay stream. Returns (average, median) in ms per call."""
+    cs = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        fn(0, cs)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cs):
+            for i in range(reps):
+                fn(i, cs)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    per = []
+    s = torch.cuda.current_stream()
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        g.replay()
+        b.record(s)
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b) / reps)
+    per_sorted = sorted(per)
+    return sum(per) / len(per), per_sorted[len(per) // 2]
 
 
 def cpu_baseline_moe(res, seconds):
@@ -250,26 +264,18 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
             if fmt.startswith("f32_128"):
                 # f32 block scales for the same codes (timing only)
                 wsf.fill_(0.02 / 448)
-            def run(c):
+            def run(c, st):
+                c = c % copies
                 if fmt.startswith("ue8m0_32"):
-                    L.fp8_gemm_bf16(aq8, as8, wq[c], ws8[c], y, M, N, K, stream=s)
+                    L.fp8_gemm_bf16(aq8, as8, wq[c], ws8[c], y, M, N, K, stream=st)
                 else:
-                    L.fp8_gemm_f32s(aqf, asf, wq[c], wsf[c], y, M, N, K, out_bf16=True, stream=s)
+                    L.fp8_gemm_f32s(aqf, asf, wq[c], wsf[c], y, M, N, K, out_bf16=True, stream=st)
             for c in range(copies):
-                run(c)
-            per = []
-            for _ in range(5):
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record(s)
-                for i in range(reps):
-                    run(i % copies)
-                b.record(s)
-                torch.cuda.synchronize()
-                per.append(a.elapsed_time(b) / reps)
-            ms = sorted(per)
-            avg = sum(per) / len(per)
+                run(c, s)
+            avg_ms, med_ms = graph_time(torch, run, reps)
+            avg = avg_ms
             bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 2
-            res[fmt] = {"avg_us": avg * 1e3, "median_us": ms[len(ms) // 2] * 1e3,
+            res[fmt] = {"avg_us": avg * 1e3, "median_us": med_ms * 1e3,
                         "TFLOP/s": flops / (avg * 1e-3) / 1e12,
                         "frac_fp8_peak": flops / (avg * 1e-3) / 1e12 / PEAK_FP8_TFLOPS,
                         "GB/s": bytes_ / (avg * 1e-3) / 1e9,
@@ -303,25 +309,17 @@ def bench_prefill(L, torch, dev, packed, reps, m=132):
                      device=dev)
     s = torch.cuda.current_stream()
 
-    def step(b):
+    def step(b, st):
+        b = b % batches
         L.moe_topk(logits[b], bias, None, idx[b], wts[b], m, E, TOPK, L.SCORE_SIGMOID, 1.0, True,
-                   1.0, stream=s)
-        L.moe_prefill(x[b], idx[b], wts[b], *packed, y[b], m, DIM, INTER, E, TOPK, ws, stream=s)
+                   1.0, stream=st)
+        L.moe_prefill(x[b], idx[b], wts[b], *packed, y[b], m, DIM, INTER, E, TOPK, ws, stream=st)
 
     for b in range(batches):
-        step(b)
+        step(b, s)
     torch.cuda.synchronize()
     touched = [len(np.unique(idx[b].cpu().numpy())) for b in range(batches)]
-    per = []
-    for _ in range(3):
-        a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(s)
-        for i in range(reps):
-            step(i % batches)
-        e.record(s)
-        torch.cuda.synchronize()
-        per.append(a.elapsed_time(e) / reps)
-    ms = sum(per) / len(per)
+    ms, _ = graph_time(torch, step, reps)
     avg_bytes = sum(touched) / batches * EXPERT_BYTES
     flops = 2.0 * m * TOPK * 3 * DIM * INTER
     counts = np.bincount(idx[0].cpu().numpy().ravel(), minlength=E)

@@ -121,7 +121,8 @@ def _quantised_case(rng, m, n, k, fp4):
 
 
 GEMM_SHAPES = [(1, 4096, 4096), (1, 1024, 2048), (4, 256, 512), (16, 512, 1024),
-               (17, 96, 384), (64, 256, 1024), (128, 512, 4096), (130, 48, 256)]
+               (17, 96, 384), (64, 256, 1024), (128, 512, 4096), (130, 48, 256),
+               (300, 160, 640), (65, 1024, 4096)]
 
 
 @pytest.mark.parametrize("m,n,k", GEMM_SHAPES)
@@ -147,7 +148,7 @@ def test_fp8_gemm_matches_oracle(m, n, k, gemm_path):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (8, 512, 1024), (128, 256, 2048),
-                                   (33, 80, 512)])
+                                   (33, 80, 512), (200, 192, 1024), (130, 8192, 256)])
 def test_fp4_gemm_matches_oracle(m, n, k, gemm_path):
     rng = np.random.default_rng(2000 + m + n + k)
     aq, as_, wq, ws = _quantised_case(rng, m, n, k, True)
@@ -159,7 +160,7 @@ def test_fp4_gemm_matches_oracle(m, n, k, gemm_path):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (128, 384, 4096), (20, 256, 512),
-                                   (5, 64, 1152)])  # K/128 = 9: the general kernel
+                                   (5, 64, 1152), (257, 320, 1280), (128, 8192, 512)])  # K/128 = 9: the general kernel
 def test_fp8_gemm_f32s_matches_oracle(m, n, k, gemm_path):
     rng = np.random.default_rng(3000 + m + n + k)
     x = activations(rng, m, k)

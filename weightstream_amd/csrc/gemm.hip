@@ -468,248 +468,352 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     return launch_status();
 }
 
-// ---- split-K GEMM with the A block in LDS ---------------------------------
-// For M-batch shapes every CU would otherwise pull all of A through L2 (the
-// L2->CU rate, ~14 TB/s for the whole chip, bounds a 16-column strip kernel at
-// M=128, K=4096 near 9 us). Here a workgroup owns a 128 x 64 output tile and a
-// K range of at most 8 steps (1024 K): its A block (128 x <=1024 e4m3 + scales)
-// is copied into LDS once by direct global->LDS loads, and its 64 columns of W
-// stream from HBM in two register stages of four 128-K steps. The 8 waves own
-// 32 x 32 sub-tiles (2 x 2 MFMA fragments), so every A and W fragment feeds two
-// MFMA tiles. With S > 1 K ranges the splits write f32 partials to the
-// workspace and sk_reduce_kernel adds them in split order (deterministic).
-// Workgroups are numbered so that the S splits of a tile share an XCD
-// (dispatch goes round-robin over the 8 XCDs).
-constexpr int kSkBM = 128, kSkBN = 64, kSkU = 4, kSkMaxSteps = 2 * kSkU;
-constexpr int kSkThreads = 512;
+// ---- pipelined split-K GEMM (A and W streamed through an LDS ring) -------
+// A workgroup (4 waves, 2 x 2 over the tile) owns a 128 x BN output tile and
+// a range of at most kPMaxSteps 128-K steps. Every step's A block (128 x 128
+// e4m3) and weight block (BN x 128 e4m3, or BN x 64 packed e2m1) are copied
+// into one of NS LDS stages by direct global->LDS loads, NS-1 steps ahead of
+// the math, so the weight stream does not wait for the multiply. The scales of
+// the whole K range are copied once, before the first stage. Each wave
+// converts its 64 x BN/2 share of a step to bf16 and runs bf16 MFMAs (exact
+// mode) or feeds the bytes to the scaled MFMA (native mode).
+// LDS rows are 128 B (64 B for e2m1) with their 16-B chunks permuted by the
+// row index, so the 16 rows read by one instruction hit distinct banks.
+constexpr int kPM = 128, kPMaxSteps = 16;
 
-template <bool BFP4>
-struct SkStage {
-    uint4 b[kSkU][2][BFP4 ? 1 : 2];  // W: 2 column fragments
-    uint32_t sb[kSkU][2];            // UE8M0 weight scale of the lane's K block
-    float sbf[kSkU];                 // f32 weight scale (128-block; uniform)
+// BN = 64 or 128: 4 waves (2 x 2, wave tile 64 x BN/2); BN = 256: 8 waves
+// (2 x 4, wave tile 64 x 64), two per SIMD, so one wave's conversions overlap
+// another's MFMAs.
+template <int BN, bool BFP4, int SMODE>
+struct PipeGeom {
+    static constexpr int kWaves = BN == 256 ? 8 : 4;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int kWN = kWaves / 2;                 // waves along N
+    static constexpr int kA = kPM * 128;               // A bytes per step
+    static constexpr int kW = BN * (BFP4 ? 64 : 128);  // weight bytes per step
+    static constexpr int kStage = kA + kW;
+    static constexpr int kAL = kA / 1024 / kWaves;     // 16-B direct loads per wave and step
+    static constexpr int kWL = kW / 1024 / kWaves;
+    static constexpr int kLoads = kAL + kWL;
+    static constexpr int kNJ = BN / kWN / 16;          // 16-column fragments per wave
+    // scale words per step: one per A row, then one per weight scale row
+    static constexpr int kSW = SMODE == kF32s ? (BN + 127) / 128 : (BFP4 ? BN : BN / 32);
+    static constexpr int kScaleBytes = ((kPM + kSW) * kPMaxSteps + 63) / 64 * 256;
+    static constexpr int kNSFit = (160 * 1024 - kScaleBytes) / kStage;
+    static constexpr int NS = kNSFit > 6 ? 6 : kNSFit;  // LDS stages
+    static constexpr int kLds = NS * kStage + kScaleBytes;
 };
 
-// Copy rows of `row_bytes` (row i at src(i)) into an LDS image with a row
-// pitch of `pitch` bytes (>= row_bytes; the padding spreads rows over the LDS
-// banks), `total` = rows * pitch, with direct loads of PIECE bytes per lane
-// (16 or 4). Padding bytes get a copy of the row's last piece.
-template <int PIECE, class Src>
-__device__ __forceinline__ void sk_dma(Src src, int row_bytes, int pitch, int total, uint8_t *lds,
-                                       int w, int lane) {
-    const int per = 64 * PIECE;
-    const int n = (total + per - 1) / per;
-    for (int c = w; c < n; c += kSkThreads / 64) {
-        const int o = min(c * per + lane * PIECE, total - PIECE);
-        const int row = o / pitch, col = min(o - row * pitch, row_bytes - PIECE);
-        const void *gp = (const void *)(src(row) + col);
-        auto *lp = (__attribute__((address_space(3))) void *)(lds + c * per);
-        if constexpr (PIECE == 16) __builtin_amdgcn_global_load_lds(gp, lp, 16, 0, 0);
-        else __builtin_amdgcn_global_load_lds(gp, lp, 4, 0, 0);
+// chunk permutation: 128-B rows (8 chunks) and 64-B rows (4 chunks)
+__device__ __forceinline__ int sw8(int row, int c) { return c ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int sw4(int row, int c) { return c ^ ((row >> 2) & 3); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most `newer` steps' loads (L per step) of this wave are in
+// flight; newer <= KMAX.
+template <int L, int KMAX>
+__device__ __forceinline__ void wait_newer(int newer) {
+    if constexpr (KMAX > 0) {
+        if (newer >= KMAX) wait_vm<KMAX * L>();
+        else wait_newer<L, KMAX - 1>(newer);
+    } else {
+        wait_vm<0>();
     }
 }
 
-template <bool BFP4, int SMODE, int OMODE, bool EXACT>
-__global__ __launch_bounds__(kSkThreads) void gemm_sk_kernel(
-    const uint8_t *A, const void *SA, const uint8_t *B, const void *SB,
-    void *__restrict__ C, int M, int N, int K, int S, int ntn, int tiles,
-    float *__restrict__ part) {
-    extern __shared__ __align__(16) uint8_t sk_lds[];
+template <int BN, bool BFP4, int SMODE, int OMODE, bool EXACT>
+__global__ __launch_bounds__(BN == 256 ? 512 : 256) void gemm_pipe_kernel(
+    const uint8_t *A, const void *SA, const uint8_t *B, const void *SB, void *__restrict__ C,
+    int M, int N, int K, int S, int ntn, float *__restrict__ part) {
+    using G = PipeGeom<BN, BFP4, SMODE>;
+    constexpr int NS = G::NS;
+    extern __shared__ __align__(16) uint8_t p_lds[];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int r = lane & 15, g = lane >> 4;
-    // XCD-aware numbering: ids x, x+8, x+16, ... hold the tiles t = x (mod 8)
-    const int id = blockIdx.x, xcd = id & 7, q = id >> 3;
-    const int tile = xcd + 8 * (q / S), s = q % S;
-    if (tile >= tiles) return;  // whole workgroup
+    const int tile = blockIdx.x / S, s = blockIdx.x % S;
     const int mb = tile / ntn, nt = tile % ntn;
-    const int m0 = mb * kSkBM, n0 = nt * kSkBN;
+    const int m0 = mb * kPM, n0 = nt * BN;
     const int ksteps = K / 128, kbn = K / 32, kb128 = K / 128;
-    const int ka = s * ksteps / S, kz = (s + 1) * ksteps / S, nks = kz - ka;  // nks <= 8
-    const int kr = nks * 128;                           // A bytes per row
-    const int kp = kr + 16;                             // LDS row pitch (bank spread)
-    uint8_t *a_l = sk_lds;                              // [128][kp] e4m3
-    uint8_t *as_l = sk_lds + (size_t)kSkBM * kp;        // UE8M0 [128][nks*4] or f32 [128][nks]
-    const int wm = w & 3, wn = w >> 2;
+    const int ka = s * ksteps / S, kz = (s + 1) * ksteps / S, n = kz - ka;  // n <= kPMaxSteps
+    const int wm = w & 1, wn = w >> 1;
+    uint8_t *const sc_lds = p_lds + NS * G::kStage;
 
-    // W columns n0 + 32 wn + 16 j + r, steps [ka, kz)
-    const uint8_t *brow[2];
-    const uint8_t *sbrow[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int col = min(n0 + 32 * wn + 16 * j + r, N - 1);
-        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + g * 16
-                       : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
-        sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
-    }
-    const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
-    auto load = [&](SkStage<BFP4> &st, int ks0) {
-#pragma unroll
-        for (int u = 0; u < kSkU; u++) {
-            const int ks = max(min(ks0 + u, kz - 1), 0);
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                if (BFP4) {
-                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
-                } else {
-                    const uint8_t *p = brow[j] + (size_t)ks * 128;
-                    st.b[u][j][0] = ldg16_stream(p);
-                    st.b[u][j][BFP4 ? 0 : 1] = ldg16_stream(p + (EXACT ? 16 : 64));
-                }
-                if (SMODE == kUe8m0) st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
-            }
-            if (SMODE == kF32s) st.sbf[u] = sbf_row[ks];
-        }
-    };
-    // 1. the A block and its scales into LDS (rows past M repeat row M-1), issued
-    //    first so that a wait for W stage 0 also covers them
-    sk_dma<16>([&](int i) { return A + (size_t)min(m0 + i, M - 1) * K + (size_t)ka * 128; }, kr,
-               kp, kSkBM * kp, a_l, w, lane);
-    if (SMODE == kUe8m0)
-        sk_dma<4>([&](int i) {
-            return (const uint8_t *)SA + (size_t)min(m0 + i, M - 1) * kbn + ka * 4; },
-                  nks * 4, nks * 4, kSkBM * nks * 4, as_l, w, lane);
-    else
-        sk_dma<4>([&](int i) {
-            return (const uint8_t *)((const float *)SA + (size_t)min(m0 + i, M - 1) * kb128 + ka); },
-                  nks * 4, nks * 4, kSkBM * nks * 4, as_l, w, lane);
-    mem_order();
-    // 2. the two W stages
-    SkStage<BFP4> s0, s1;
-    load(s0, ka);
-    mem_order();
-    load(s1, ka + kSkU);
-    mem_order();
-    // wait until at most stage 1's weight loads are outstanding (a lower bound
-    // on the loads stage 1 issues: its scale loads only make the wait
-    // stricter): this wave's LDS copies and stage 0 have landed
-    constexpr int kStage1Loads = kSkU * 2 * (BFP4 ? 1 : 2);
-    __builtin_amdgcn_s_waitcnt((kStage1Loads & 15) | ((kStage1Loads >> 4) << 14) | (7 << 4) |
-                               (15 << 8));
-    raw_barrier();
-
-    // 3. multiply
-    v4f acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](const SkStage<BFP4> &st, int ks0) {
-#pragma unroll
-        for (int u = 0; u < kSkU; u++) {
-            const int ks = ks0 + u;
-            if (ks >= kz) continue;  // uniform
-            const int kl = ks - ka;
-            if (EXACT) {
-                v8bf bq[2][4];
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const float sbv = SMODE == kUe8m0 ? e8m0_to_f32(st.sb[u][j] & 0xFF) : 1.0f;
-                    if (BFP4) cvt_fp4x32(st.b[u][j][0], sbv, bq[j]);
-                    else cvt_fp8x32(st.b[u][j][0], st.b[u][j][BFP4 ? 0 : 1], sbv, bq[j]);
-                }
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int ml = 32 * wm + 16 * i + r;
-                    const uint8_t *ap = a_l + ml * kp + kl * 128 + g * 32;
-                    const float sav = SMODE == kUe8m0 ? e8m0_to_f32(as_l[ml * nks * 4 + kl * 4 + g])
-                                                      : 1.0f;
-                    v8bf aq[4];
-                    cvt_fp8x32(*(const uint4 *)ap, *(const uint4 *)(ap + 16), sav, aq);
-#pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        if (SMODE == kUe8m0) {
-                            acc[i][j] = mfma_bf16_k128(aq, bq[j], acc[i][j]);
-                        } else {
-                            const v4f pr = mfma_bf16_k128(aq, bq[j], v4f{0.f, 0.f, 0.f, 0.f});
-                            const float *sar = (const float *)as_l + (32 * wm + 16 * i + 4 * g) * nks + kl;
-#pragma unroll
-                            for (int v = 0; v < 4; v++)
-                                acc[i][j][v] = acc[i][j][v] + pr[v] * (sar[v * nks] * st.sbf[u]);
-                        }
-                    }
-                }
+    // ---- 1. scales of steps [ka, kz): word (row * n + j) for A row `row`,
+    // word ((kPM + q) * n + j) for weight scale row q (a 32-column block of
+    // FP8 weights, one FP4 weight row, or a 128-column f32 block). A lane
+    // copies one word; consecutive lanes walk a row's steps, so an
+    // instruction touches few cache lines.
+    {
+        const int words = (kPM + G::kSW) * n;
+        const int ninstr = (words + 63) / 64;
+        for (int c = w; c < ninstr; c += G::kWaves) {
+            const int o = min(c * 64 + lane, words - 1);
+            const int q = o / n, j = o - q * n;
+            const uint8_t *src;
+            if (q < kPM) {
+                const int row = min(m0 + q, M - 1);
+                src = SMODE == kF32s ? (const uint8_t *)((const float *)SA + (size_t)row * kb128 + ka + j)
+                                     : (const uint8_t *)SA + (size_t)row * kbn + (ka + j) * 4;
+            } else if (SMODE == kF32s) {
+                const int wrow = min(n0 / 128 + q - kPM, (N + 127) / 128 - 1);
+                src = (const uint8_t *)((const float *)SB + (size_t)wrow * kb128 + ka + j);
             } else {
-                v8i bf[2];
+                const int wq = q - kPM;
+                const int wrow = BFP4 ? min(n0 + wq, N - 1) : min(n0 / 32 + wq, (N + 31) / 32 - 1);
+                src = (const uint8_t *)SB + (size_t)wrow * kbn + (ka + j) * 4;
+            }
+            __builtin_amdgcn_global_load_lds((const void *)src,
+                                             (__attribute__((address_space(3))) void *)(sc_lds + c * 256),
+                                             4, 0, 0);
+        }
+    }
+
+    // ---- 2. direct loads of one step into stage buffer `buf`; a lane's
+    // source rows are fixed, only the K offset moves
+    const uint8_t *asrc[G::kAL];
 #pragma unroll
-                for (int j = 0; j < 2; j++)
-                    bf[j] = BFP4 ? frag_from4(st.b[u][j][0])
-                                 : frag_from(st.b[u][j][0], st.b[u][j][BFP4 ? 0 : 1]);
+    for (int j = 0; j < G::kAL; j++) {
+        const int o = (w * G::kAL + j) * 1024 + lane * 16;
+        const int row = o >> 7, c = (o >> 4) & 7;
+        asrc[j] = A + (size_t)min(m0 + row, M - 1) * K + sw8(row, c) * 16;
+    }
+    const uint8_t *wsrc[G::kWL];
 #pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const int ml = 32 * wm + 16 * i + r;
-                    const uint8_t *ap = a_l + ml * kp + kl * 128 + g * 16;
-                    const v8i af = frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64));
+    for (int j = 0; j < G::kWL; j++) {
+        const int o = (w * G::kWL + j) * 1024 + lane * 16;
+        if (BFP4) {
+            const int row = o >> 6, c = (o >> 4) & 3;
+            wsrc[j] = B + (size_t)min(n0 + row, N - 1) * (K / 2) + sw4(row, c) * 16;
+        } else {
+            const int row = o >> 7, c = (o >> 4) & 7;
+            wsrc[j] = B + (size_t)min(n0 + row, N - 1) * K + sw8(row, c) * 16;
+        }
+    }
+    auto issue = [&](int buf, int ks) {
+        uint8_t *base = p_lds + buf * G::kStage;
 #pragma unroll
-                    for (int j = 0; j < 2; j++) {
-                        if (SMODE == kUe8m0) {
-                            const int sa = as_l[ml * nks * 4 + kl * 4 + g];
-                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(af, bf[j], acc[i][j], sa,
-                                                                             (int)st.sb[u][j])
-                                             : mfma_scaled<kFmtFp8, kFmtFp8>(af, bf[j], acc[i][j], sa,
-                                                                             (int)st.sb[u][j]);
-                        } else {
-                            const v4f pr = mfma_scaled<kFmtFp8, kFmtFp8>(
-                                af, bf[j], v4f{0.f, 0.f, 0.f, 0.f}, kScaleOne, kScaleOne);
-                            const float *sar = (const float *)as_l + (32 * wm + 16 * i + 4 * g) * nks + kl;
+        for (int j = 0; j < G::kAL; j++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(asrc[j] + (size_t)ks * 128),
+                (__attribute__((address_space(3))) void *)(base + (w * G::kAL + j) * 1024), 16, 0, 0);
 #pragma unroll
-                            for (int v = 0; v < 4; v++)
-                                acc[i][j][v] = acc[i][j][v] + pr[v] * (sar[v * nks] * st.sbf[u]);
-                        }
+        for (int j = 0; j < G::kWL; j++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(wsrc[j] + (size_t)ks * (BFP4 ? 64 : 128)),
+                (__attribute__((address_space(3))) void *)(base + G::kA + (w * G::kWL + j) * 1024),
+                16, 0, 0);
+    };
+
+    // ---- 3. registers of one step (LDS reads as asm: see lds_read_b128)
+    struct Raw {
+        u32x4v a[4][2];
+        u32x4v b[G::kNJ][BFP4 ? 1 : 2];
+        uint32_t sa[4][SMODE == kF32s ? 4 : 1], sb[G::kNJ];
+    };
+    auto fetch = [&](int buf, int i, Raw &x) {
+        const uint32_t base = lds_addr(p_lds) + buf * G::kStage;
+        const uint32_t wl = base + G::kA;
+        const uint32_t sl = lds_addr(sc_lds);
+        const int c0 = EXACT ? 2 * g : g, c1 = EXACT ? 2 * g + 1 : 4 + g;
+#pragma unroll
+        for (int f = 0; f < 4; f++) {
+            const int row = 64 * wm + 16 * f + r;
+            x.a[f][0] = lds_read_b128(base + row * 128 + sw8(row, c0) * 16);
+            x.a[f][1] = lds_read_b128(base + row * 128 + sw8(row, c1) * 16);
+            if (SMODE == kUe8m0) {
+                x.sa[f][0] = lds_read_b32(sl + (row * n + i) * 4);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    x.sa[f][v] = lds_read_b32(sl + ((64 * wm + 16 * f + 4 * g + v) * n + i) * 4);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < G::kNJ; j++) {
+            const int col = (BN / G::kWN) * wn + 16 * j + r;
+            if (BFP4) {
+                x.b[j][0] = lds_read_b128(wl + col * 64 + sw4(col, g) * 16);
+            } else {
+                x.b[j][0] = lds_read_b128(wl + col * 128 + sw8(col, c0) * 16);
+                x.b[j][BFP4 ? 0 : 1] = lds_read_b128(wl + col * 128 + sw8(col, c1) * 16);
+            }
+            const int q = SMODE == kF32s ? col / 128 : (BFP4 ? col : col / 32);
+            x.sb[j] = lds_read_b32(sl + ((kPM + q) * n + i) * 4);
+        }
+    };
+    auto settle = [&](Raw &x) {
+        lds_wait_all();
+#pragma unroll
+        for (int f = 0; f < 4; f++) {
+            lds_ready(x.a[f][0]);
+            lds_ready(x.a[f][1]);
+#pragma unroll
+            for (int v = 0; v < (SMODE == kF32s ? 4 : 1); v++) lds_ready(x.sa[f][v]);
+        }
+#pragma unroll
+        for (int j = 0; j < G::kNJ; j++) {
+            lds_ready(x.b[j][0]);
+            if (!BFP4) lds_ready(x.b[j][BFP4 ? 0 : 1]);
+            lds_ready(x.sb[j]);
+        }
+    };
+    auto u4 = [](const u32x4v &v) { return uint4{v[0], v[1], v[2], v[3]}; };
+
+    v4f acc[4][G::kNJ];
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int j = 0; j < G::kNJ; j++) acc[f][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    // f32 scales: acc += P * (sa[row] * sb) once per step
+    auto scale_add = [&](v4f &a, const v4f &p, const Raw &x, int f, int j) {
+        const float sbf = __uint_as_float(x.sb[j]);
+#pragma unroll
+        for (int v = 0; v < 4; v++) a[v] = a[v] + p[v] * (__uint_as_float(x.sa[f][v]) * sbf);
+    };
+    auto math = [&](const Raw &x) {
+        if (EXACT) {
+            v8bf aq[4][4];
+#pragma unroll
+            for (int f = 0; f < 4; f++)
+                cvt_fp8x32(u4(x.a[f][0]), u4(x.a[f][1]),
+                           SMODE == kUe8m0 ? e8m0_to_f32((x.sa[f][0] >> (8 * g)) & 0xFF) : 1.0f, aq[f]);
+#pragma unroll
+            for (int j = 0; j < G::kNJ; j++) {
+                v8bf bq[4];
+                const float sb = SMODE == kUe8m0 ? e8m0_to_f32((x.sb[j] >> (8 * g)) & 0xFF) : 1.0f;
+                if (BFP4) cvt_fp4x32(u4(x.b[j][0]), sb, bq);
+                else cvt_fp8x32(u4(x.b[j][0]), u4(x.b[j][BFP4 ? 0 : 1]), sb, bq);
+#pragma unroll
+                for (int f = 0; f < 4; f++) {
+                    if (SMODE == kUe8m0) acc[f][j] = mfma_bf16_k128(aq[f], bq, acc[f][j]);
+                    else scale_add(acc[f][j], mfma_bf16_k128(aq[f], bq, v4f{0.f, 0.f, 0.f, 0.f}), x, f, j);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < G::kNJ; j++) {
+                const v8i bf = BFP4 ? frag_from4(u4(x.b[j][0]))
+                                    : frag_from(u4(x.b[j][0]), u4(x.b[j][BFP4 ? 0 : 1]));
+#pragma unroll
+                for (int f = 0; f < 4; f++) {
+                    const v8i af = frag_from(u4(x.a[f][0]), u4(x.a[f][1]));
+                    if (SMODE == kUe8m0) {
+                        const int sa = (x.sa[f][0] >> (8 * g)) & 0xFF, sb = (x.sb[j] >> (8 * g)) & 0xFF;
+                        acc[f][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(af, bf, acc[f][j], sa, sb)
+                                         : mfma_scaled<kFmtFp8, kFmtFp8>(af, bf, acc[f][j], sa, sb);
+                    } else {
+                        scale_add(acc[f][j],
+                                  mfma_scaled<kFmtFp8, kFmtFp8>(af, bf, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                kScaleOne, kScaleOne),
+                                  x, f, j);
                     }
                 }
             }
         }
     };
-    compute(s0, ka);
-    compute(s1, ka + kSkU);
 
-    // 4. store: C directly (one split) or the split's partial
-    auto store_c = [&](int row, int col, float v) {
-        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + col] = v;
-        else ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(v);
-    };
-    const size_t mpad = (size_t)((M + kSkBM - 1) / kSkBM) * kSkBM;
+    // ---- 4. pipeline: NS-1 steps ahead, one refill per step
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int p = 0; p < NS - 1; p++)
+        if (p < n) issue(p, ka + p);
+    for (int i = 0; i < n; i++) {
+        // this wave's copies of step i (and the older scale copies) have
+        // landed once at most min(n-1-i, NS-2) newer steps are in flight
+        mem_order();
+        wait_newer<G::kLoads, NS - 2>(min(n - 1 - i, NS - 2));
+        raw_barrier();  // every wave's copies of step i are in LDS; step i-1's buffer is free
+        Raw x;
+        fetch(i % NS, i, x);
+        if (i + NS - 1 < n) issue((i + NS - 1) % NS, ka + i + NS - 1);
+        settle(x);
+        math(x);
+    }
+
+    // ---- 5. store: C directly (one split), or the split's partial in
+    // fragment order (one 1-KB float4 row per fragment: coalesced)
+    if (S > 1) {
+        float4 *pp = (float4 *)part + (((size_t)s * gridDim.x / S + tile) * G::kWaves + w) * (4 * G::kNJ * 64);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int col = n0 + 32 * wn + 16 * j + r;
+        for (int f = 0; f < 4; f++)
+#pragma unroll
+            for (int j = 0; j < G::kNJ; j++)
+                pp[(f * G::kNJ + j) * 64 + lane] = float4{acc[f][j][0], acc[f][j][1], acc[f][j][2], acc[f][j][3]};
+        return;
+    }
+#pragma unroll
+    for (int f = 0; f < 4; f++)
+#pragma unroll
+        for (int j = 0; j < G::kNJ; j++) {
+            const int col = n0 + (BN / G::kWN) * wn + 16 * j + r;
+            if (col >= N) continue;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int row = m0 + 32 * wm + 16 * i + 4 * g + v;
-                if (S == 1) {
-                    if (row < M && col < N) store_c(row, col, acc[i][j][v]);
-                } else if (col < N) {
-                    part[((size_t)s * mpad + row) * N + col] = acc[i][j][v];
+                const int row = m0 + 64 * wm + 16 * f + 4 * g + v;
+                if (row < M) {
+                    if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + col] = acc[f][j][v];
+                    else ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(acc[f][j][v]);
                 }
             }
         }
 }
 
 // Sum of the S partials of every output in split order (deterministic);
-// the kernel boundary after gemm_sk_kernel makes them visible.
-template <int OMODE>
-__global__ __launch_bounds__(256) void sk_reduce_kernel(const float *__restrict__ part,
-                                                        void *__restrict__ C, int M, int N, int S,
-                                                        size_t mpad) {
-    const size_t o = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    const size_t total = (size_t)M * N;
-    if (o >= total) return;
-    const size_t plane = mpad * N;
-    float4 acc = *(const float4 *)(part + o);
-    for (int q = 1; q < S; q++) {
-        const float4 v = *(const float4 *)(part + (size_t)q * plane + o);
-        acc.x = acc.x + v.x;
-        acc.y = acc.y + v.y;
-        acc.z = acc.z + v.z;
-        acc.w = acc.w + v.w;
+// the kernel boundary after gemm_pipe_kernel makes them visible. Partials are
+// in the GEMM's fragment order: [split][tile][wave][f][j][lane] float4, the
+// float4 holding rows 4g..4g+3 (g = lane / 16) of column lane % 16.
+template <int BN, int OMODE>
+__global__ __launch_bounds__(256) void pipe_reduce_kernel(const float4 *__restrict__ part,
+                                                          void *__restrict__ C, int M, int N, int S,
+                                                          int tiles, int ntn) {
+    constexpr int NW = BN == 256 ? 8 : 4, WN = NW / 2, NJ = BN / WN / 16;
+    const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;  // float4 index within a split
+    const size_t plane = (size_t)tiles * NW * 4 * NJ * 64;
+    if (q >= plane) return;
+    // loads in groups of four, all issued before the adds (planes past S-1
+    // repeat the last one and are not added); the sum runs in split order
+    float4 acc = float4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = part[(size_t)min(s0 + u, S - 1) * plane + q];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (s0 + u >= S) break;
+            if (s0 + u == 0) {
+                acc = v[u];
+            } else {
+                acc.x = acc.x + v[u].x;
+                acc.y = acc.y + v[u].y;
+                acc.z = acc.z + v[u].z;
+                acc.w = acc.w + v[u].w;
+            }
+        }
     }
-    if (OMODE == kOutF32) {
-        *(float4 *)((float *)C + o) = acc;
-    } else {
-        uint16_t *c = (uint16_t *)C + o;
-        *(uint2 *)c = uint2{(uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16),
-                            (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16)};
+    const int lane = (int)(q & 63);
+    size_t rest = q >> 6;
+    const int j = (int)(rest % NJ);
+    rest /= NJ;
+    const int f = (int)(rest & 3);
+    rest >>= 2;
+    const int w = (int)(rest % NW);
+    const int tile = (int)(rest / NW);
+    const int mb = tile / ntn, nt = tile % ntn;
+    const int col = nt * BN + (BN / WN) * (w >> 1) + 16 * j + (lane & 15);
+    if (col >= N) return;
+    const int row0 = mb * 128 + 64 * (w & 1) + 16 * f + 4 * (lane >> 4);
+    const float v[4] = {acc.x, acc.y, acc.z, acc.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const int row = row0 + e;
+        if (row >= M) break;
+        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + col] = v[e];
+        else ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(v[e]);
     }
 }
 
@@ -726,48 +830,60 @@ static SkWorkspace &sk_ws() {
     return g_sk_ws[dev];
 }
 
-// Splits for (M, N, K): every split at most 8 steps, enough workgroups to
-// cover the CUs; 0 when the split-K kernel does not apply.
-static int sk_splits(int M, int N, int K, size_t ws_bytes) {
+// Splits for the pipelined kernel: K ranges of at most kPMaxSteps steps, and
+// as many as keep every CU busy with one workgroup; 0 when the workspace is
+// too small.
+static int pipe_splits(int M, int N, int K, int BN, size_t ws_bytes) {
     const int ksteps = K / 128;
-    const int tiles = ((M + kSkBM - 1) / kSkBM) * ((N + kSkBN - 1) / kSkBN);
-    int S = (ksteps + kSkMaxSteps - 1) / kSkMaxSteps;
-    const int want = (cu_count() + tiles - 1) / tiles;
-    if (want > S) S = want;
+    const int tiles = ((M + kPM - 1) / kPM) * ((N + BN - 1) / BN);
+    static const int forced = [] {
+        const char *e = getenv("WS_PIPE_S");
+        return e ? atoi(e) : 0;
+    }();
+    int S = forced > 0 ? forced : cu_count() / tiles;
+    const int smin = (ksteps + kPMaxSteps - 1) / kPMaxSteps;
+    if (S < smin) S = smin;
     if (S > ksteps) S = ksteps;
-    const size_t mpad = (size_t)((M + kSkBM - 1) / kSkBM) * kSkBM;
-    if (S > 1 && (size_t)S * mpad * N * 4 > ws_bytes) return 0;
+    // partials: S planes of tiles x (128 x BN) floats
+    if (S > 1 && (size_t)S * tiles * kPM * BN * 4 > ws_bytes) return 0;
     return S;
 }
 
-template <bool BFP4, int SMODE, int OMODE>
-static int launch_sk(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
-                     int m, int n, int k, hipStream_t stream) {
+// Tile width of the pipelined kernel for (M, N): 256 columns when that still
+// gives every eighth CU a tile, else 64; WS_PIPE_BN forces 64, 128 or 256.
+static int pipe_bn(int M, int N) {
+    static const int forced = [] {
+        const char *e = getenv("WS_PIPE_BN");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced == 64 || forced == 128 || forced == 256) return forced;
+    const int mt = (M + kPM - 1) / kPM;
+    // measured at M=128, K=4096: 256 wins at N=12288, 64 at N=4096 and 2048
+    // (fewer partial bytes per split than 128)
+    return mt * ((N + 255) / 256) * 8 >= cu_count() ? 256 : 64;
+}
+
+template <int BN, bool BFP4, int SMODE, int OMODE>
+static int launch_pipe(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
+                       int m, int n, int k, hipStream_t stream) {
+    using G = PipeGeom<BN, BFP4, SMODE>;
     SkWorkspace &wsp = sk_ws();
-    if (!wsp.ptr) return -1;
-    const int S = sk_splits(m, n, k, wsp.bytes);
+    const int S = pipe_splits(m, n, k, BN, wsp.ptr ? wsp.bytes : 0);
     if (S <= 0) return -1;
-    const int ksteps = k / 128;
-    const int nks_max = (ksteps + S - 1) / S;
-    const int ntn = (n + kSkBN - 1) / kSkBN;
-    const int tiles = ((m + kSkBM - 1) / kSkBM) * ntn;
-    const size_t lds = (size_t)kSkBM * (nks_max * 128 + 16) + (size_t)kSkBM * nks_max * 4;
-    const unsigned grid = (unsigned)(8 * ((tiles + 7) / 8) * S);
+    const int ntn = (n + BN - 1) / BN;
+    const int tiles = ((m + kPM - 1) / kPM) * ntn;
     float *part = (float *)wsp.ptr;
     if (math_mode() == WS_MATH_NATIVE)
-        hipLaunchKernelGGL((gemm_sk_kernel<BFP4, SMODE, OMODE, false>), dim3(grid),
-                           dim3(kSkThreads), lds, stream, a, sa, b, sb, out, m, n, k, S, ntn,
-                           tiles, part);
+        hipLaunchKernelGGL((gemm_pipe_kernel<BN, BFP4, SMODE, OMODE, false>), dim3(tiles * S),
+                           dim3(G::kThreads), G::kLds, stream, a, sa, b, sb, out, m, n, k, S, ntn, part);
     else
-        hipLaunchKernelGGL((gemm_sk_kernel<BFP4, SMODE, OMODE, true>), dim3(grid),
-                           dim3(kSkThreads), lds, stream, a, sa, b, sb, out, m, n, k, S, ntn,
-                           tiles, part);
+        hipLaunchKernelGGL((gemm_pipe_kernel<BN, BFP4, SMODE, OMODE, true>), dim3(tiles * S),
+                           dim3(G::kThreads), G::kLds, stream, a, sa, b, sb, out, m, n, k, S, ntn, part);
     int rc = launch_status();
     if (rc || S == 1) return rc;
-    const size_t mpad = (size_t)((m + kSkBM - 1) / kSkBM) * kSkBM;
-    const size_t quads = ((size_t)m * n + 3) / 4;
-    hipLaunchKernelGGL((sk_reduce_kernel<OMODE>), dim3((unsigned)((quads + 255) / 256)), dim3(256),
-                       0, stream, part, out, m, n, S, mpad);
+    const size_t quads = (size_t)tiles * G::kWaves * 4 * G::kNJ * 64;
+    hipLaunchKernelGGL((pipe_reduce_kernel<BN, OMODE>), dim3((unsigned)((quads + 255) / 256)),
+                       dim3(256), 0, stream, (const float4 *)part, out, m, n, S, tiles, ntn);
     return launch_status();
 }
 
@@ -804,16 +920,15 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
     int M = (int)m, N = (int)n, K = (int)k;
     int cfg = forced_cfg();
     if (cfg < 0) {
-        // K-parallel strips (one workgroup per 16 columns); -1: shape outside
-        // what they stage, use the general kernel
-        // split-K unless the 16-column strips alone fill the chip in one round
-        // (measured at M=128, K=4096: strips win at N=4096, split-K at N=2048
-        // and N=12288)
-        const int strips = N / 16, cus = cu_count();
-        const bool strips_fit = strips >= cus * 3 / 4 && strips <= cus * 3 / 2;
-        int rc = (M > 16 && !strips_fit)
-                     ? launch_sk<BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
-                     : -1;
+        // M > 64: pipelined 128-row tiles (128 columns when that still gives
+        // every eighth CU a tile, else 64); M <= 64: K-parallel 16-column strips
+        int rc = -1;
+        if (M > 64) {
+            const int bn = pipe_bn(M, N);
+            rc = bn == 256   ? launch_pipe<256, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
+                 : bn == 128 ? launch_pipe<128, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
+                             : launch_pipe<64, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
+        }
         if (rc >= 0) return rc;
         if (M <= 16) rc = launch_kp<1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
         else if (M <= 32) rc = launch_kp<2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
@@ -839,15 +954,16 @@ using namespace ws;
 extern "C" {
 
 size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
-    if (m <= 0 || n <= 0 || k <= 0 || k % 128) return 0;
-    const int64_t ksteps = k / 128;
-    int64_t S = (ksteps + kSkMaxSteps - 1) / kSkMaxSteps;
-    const int64_t tiles = ((m + kSkBM - 1) / kSkBM) * ((n + kSkBN - 1) / kSkBN);
-    const int64_t want = (cu_count() + tiles - 1) / tiles;
-    if (want > S) S = want;
-    if (S > ksteps) S = ksteps;
-    const int64_t mpad = (m + kSkBM - 1) / kSkBM * kSkBM;
-    return (size_t)(S > 1 ? S : 1) * mpad * n * 4;
+    if (m <= 0 || n <= 0 || k <= 0 || k % 128 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24))
+        return 0;
+    size_t best = 0;
+    for (int bn : {64, 128, 256}) {
+        const int S = pipe_splits((int)m, (int)n, (int)k, bn, (size_t)-1);
+        const size_t tiles = (size_t)((m + kPM - 1) / kPM) * ((n + bn - 1) / bn);
+        const size_t need = S > 1 ? (size_t)S * tiles * kPM * bn * 4 : 0;
+        if (need > best) best = need;
+    }
+    return best;
 }
 
 int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream) {

@@ -98,6 +98,28 @@ __device__ __forceinline__ void raw_barrier() {
     mem_order();
 }
 
+// LDS reads the compiler does not see as memory accesses. After direct
+// global->LDS loads into other buffers are issued, the compiler would make an
+// ordinary LDS read wait for all of them (it cannot tell the buffers apart);
+// these reads are ordered by the caller instead: issue them, then
+// lds_wait_all() and lds_ready() on every result before use.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+__device__ __forceinline__ u32x4v lds_read_b128(uint32_t a) {
+    u32x4v v;
+    __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
+    uint32_t v;
+    __asm__ volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+__device__ __forceinline__ void lds_wait_all() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+template <class T>
+__device__ __forceinline__ void lds_ready(T &v) { __asm__ volatile("" : "+v"(v)); }
+
 // Barrier that orders LDS only: global loads issued before it stay in flight.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
