@@ -333,6 +333,96 @@ def bench_prefill(L, torch, dev, packed, reps, m=132):
                                   ">20": int((counts > 20).sum())}}
 
 
+def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
+    """Config 5: the full synthetic MoE block, `layers` layers stacked, each
+    with its own weights: FP8 attention output projection (K=8192 -> 4096)
+    added to the residual, f32 gate GEMV (384 x 4096), top-8 sigmoid routing,
+    the 384 routed FP4 experts (M=1: ws_moe_decode_route; M>1: ws_moe_topk +
+    the grouped ws_moe_prefill), the shared FP8 expert (inter 2048) and the
+    two acc_f32 adds. Routed layers 2..4 are device copies of layer 1's packed
+    experts (distinct memory, so no layer reads another's weights from
+    cache). Reported per layer; bytes = weights touched once."""
+    import numpy as np
+    OD, SI = 8192, 2048   # out-projection K, shared expert intermediate
+
+    def fp8(rows, cols):
+        w = torch.empty((rows, cols), dtype=torch.float32, device=dev).normal_(0.0, 0.02,
+                                                                              generator=gen)
+        q = torch.empty((rows, cols), dtype=torch.uint8, device=dev)
+        sc = torch.empty((rows // 32, cols // 32), dtype=torch.uint8, device=dev)
+        L.weight_quant_fp8(w, q, sc, rows, cols)
+        return q, sc
+
+    lay = []
+    for li in range(layers):
+        routed = packed if li == 0 else tuple(t.clone() for t in packed)
+        lay.append({"routed": routed, "wo": fp8(DIM, OD),
+                    "shared": fp8(SI, DIM) + fp8(SI, DIM) + fp8(DIM, SI),
+                    "gate": torch.empty((E, DIM), dtype=torch.float32, device=dev).normal_(
+                        0.0, 0.02, generator=gen),
+                    "bias": torch.randn((E,), device=dev, generator=gen) * 0.1})
+    torch.cuda.synchronize()
+    out = {}
+    for M in Ms:
+        attn = torch.randn((layers, M, OD), device=dev, generator=gen)
+        h0 = torch.randn((M, DIM), device=dev, generator=gen)
+        h = torch.empty_like(h0)
+        aq = torch.empty((M, OD), dtype=torch.uint8, device=dev)
+        asc = torch.empty((M, OD // 32), dtype=torch.uint8, device=dev)
+        o = torch.empty((M, DIM), dtype=torch.float32, device=dev)
+        logits = torch.empty((M, E), dtype=torch.float32, device=dev)
+        idx = torch.empty((layers, M, TOPK), dtype=torch.int32, device=dev)
+        wts = torch.empty((layers, M, TOPK), dtype=torch.float32, device=dev)
+        yr = torch.empty((M, DIM), dtype=torch.float32, device=dev)
+        ys = torch.empty((M, DIM), dtype=torch.float32, device=dev)
+        sws = torch.empty(L.shared_expert_workspace_size(M, DIM, SI), dtype=torch.uint8,
+                          device=dev)
+        dws = torch.empty(L.moe_decode_workspace_size(DIM, INTER, TOPK), dtype=torch.uint8,
+                          device=dev)
+        pws = torch.empty(L.moe_prefill_workspace_size(M, DIM, INTER, TOPK, E),
+                          dtype=torch.uint8, device=dev)
+
+        def step(i, st):
+            h.copy_(h0)
+            for li, w in enumerate(lay):
+                L.emit8(attn[li], aq, asc, M * OD, stream=st)
+                L.fp8_gemm(aq, asc, *w["wo"], o, M, DIM, OD, stream=st)
+                L.acc_f32(o, h, M * DIM, stream=st)
+                L.moe_gate_logits(h, w["gate"], logits, M, DIM, E, stream=st)
+                if M == 1:
+                    L.moe_decode_route(logits, w["bias"], L.SCORE_SIGMOID, 1.0, 1, 1.0, h,
+                                       *w["routed"], yr, idx[li], wts[li], DIM, INTER, E, TOPK,
+                                       dws, stream=st)
+                else:
+                    L.moe_topk(logits, w["bias"], None, idx[li], wts[li], M, E, TOPK,
+                               L.SCORE_SIGMOID, 1.0, True, 1.0, stream=st)
+                    L.moe_prefill(h, idx[li], wts[li], *w["routed"], yr, M, DIM, INTER, E, TOPK,
+                                  pws, stream=st)
+                L.shared_expert_fp8(h, *w["shared"], ys, M, DIM, SI, sws, stream=st)
+                L.acc_f32(ys, yr, M * DIM, stream=st)
+                L.acc_f32(yr, h, M * DIM, stream=st)
+
+        step(0, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        if not torch.isfinite(h).all():
+            raise RuntimeError("MoE block output is not finite")
+        ms, med = graph_time(torch, step, reps)
+        touched = [len(np.unique(idx[li].cpu().numpy())) for li in range(layers)]
+        layer_bytes = (np.mean(touched) * EXPERT_BYTES + 3 * SI * DIM + 3 * (SI // 32) * (DIM // 32)
+                       + DIM * OD + (DIM // 32) * (OD // 32) + E * DIM * 4)
+        per_layer = ms / layers
+        out[str(M)] = {"us_per_layer": per_layer * 1e3, "layers": layers,
+                       "experts_touched_per_layer": touched,
+                       "bytes_per_layer": int(layer_bytes),
+                       "GB/s": layer_bytes / (per_layer * 1e-3) / 1e9,
+                       "frac_hbm_peak": layer_bytes / (per_layer * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                       "tokens_per_s": M / (ms * 1e-3)}
+        log("block M=%d: %.1f us/layer, %.0f GB/s" % (M, per_layer * 1e3, out[str(M)]["GB/s"]))
+    del lay
+    torch.cuda.synchronize()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,6 +432,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--no-block", action="store_true", help="skip config 5 (full MoE block)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device-to-device 5 times (calibrates the HBM "
                          "traffic counters against a known byte count) and exit")
@@ -404,6 +495,7 @@ def main():
                               if k in ("avg_us", "GB/s", "TFLOP/s")}
     L.set_math_mode(L.MATH_EXACT)
     log("prefill: %s" % prefill)
+    block = bench_block(L, torch, dev, packed, gen) if not args.no_block else None
     gemm = gemv = None
     if not args.no_gemm:
         gemv = bench_gemm(L, torch, dev, 100, M=1, Ns=(4096,))
@@ -437,6 +529,7 @@ def main():
         "fp8_gemv_m1": gemv,
         "fp8_gemm_m128": gemm,
         "moe_prefill_m132": prefill,
+        "moe_block_4_layers": block,
     }
     print(json.dumps(line), flush=True)
 

@@ -178,6 +178,25 @@ int ws_moe_route(const float *x, const uint16_t *gate_w, const float *bias, floa
  * out = silu(min(g,10)) * clamp(u,-10,10) * rw, in moe.rs:187-201's order. */
 int ws_swiglu(const float *gate, const float *up, float *out, int64_t n, float rw,
               ws_stream_t stream);
+/* launch.rs:1175-1179 acc_f32 (gemv.cu:63): y[i] += x[i] for i < n (both
+ * 16-byte aligned). */
+int ws_acc_f32(const float *x, float *y, int64_t n, ws_stream_t stream);
+/* The shared FP8 expert of the MoE block: weightstream-ref moe.rs:210-250
+ * (shared_expert_hidden), run on the device as the engine's moe_shared_step
+ * (engine.rs:4063) does with emit8 + fp8_gemm + swiglu launches.
+ * x [m, dim] f32; w1, w3 e4m3 [inter, dim] with UE8M0 [inter/32, dim/32];
+ * w2 e4m3 [dim, inter] with UE8M0 [dim/32, inter/32]; y [m, dim] f32 (written,
+ * not accumulated). h = silu(min(g, L)) * clamp(u, -L, L) with L =
+ * swiglu_limit (<= 0: no clamps), quantised per 1x32 before the down GEMM.
+ * dim and inter multiples of 128. The workspace (256-byte aligned, at least
+ * ws_shared_expert_workspace_size bytes) holds the quantised token, g, u and
+ * the quantised hidden state; the GEMMs use the registered split-K workspace
+ * (ws_set_gemm_workspace) when there is one. */
+size_t ws_shared_expert_workspace_size(int64_t m, int64_t dim, int64_t inter);
+int ws_shared_expert_fp8(const float *x, const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
+                         const uint8_t *s3, const uint8_t *w2, const uint8_t *s2, float *y,
+                         int64_t m, int64_t dim, int64_t inter, float swiglu_limit,
+                         void *workspace, size_t workspace_bytes, ws_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Packed FP4 expert weights. The routed-expert entry points below read FP4

@@ -71,6 +71,10 @@ SIGNATURES = {
     "ws_moe_select": (_i, [_p, _p, _p, _p, _i64, _i64, _f, _p]),
     "ws_moe_route": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p]),
     "ws_swiglu": (_i, [_p, _p, _p, _i64, _f, _p]),
+    "ws_acc_f32": (_i, [_p, _p, _i64, _p]),
+    "ws_shared_expert_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
+    "ws_shared_expert_fp8": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p,
+                                  C.c_size_t, _p]),
     "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_x": (_i, [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_reduce": (_i, [_p] * 6 + [_i64, _i64, _i64, _i64, _p]),

@@ -17,7 +17,8 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libweightstream_hip.so")
 
-SOURCES = ["common.hip", "pack.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip"]
+SOURCES = ["common.hip", "pack.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip",
+           "moe_shared.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

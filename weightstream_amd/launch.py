@@ -228,6 +228,24 @@ def swiglu(gate, up, out, n, rw, stream=None):
     _call("ws_swiglu", _ptr(gate), _ptr(up), _ptr(out), n, rw, _s(stream))
 
 
+def acc_f32(x, y, n, stream=None):
+    """launch.rs:1175 acc_f32: y += x."""
+    _call("ws_acc_f32", _ptr(x), _ptr(y), n, _s(stream))
+
+
+def shared_expert_workspace_size(m, dim, inter):
+    return int(_lib.load().ws_shared_expert_workspace_size(m, dim, inter))
+
+
+def shared_expert_fp8(x, w1, s1, w3, s3, w2, s2, y, m, dim, inter, workspace,
+                      swiglu_limit=10.0, stream=None):
+    """moe.rs:210-250 shared_expert_hidden for m tokens (engine.rs:4063
+    moe_shared_step): FP8 gate/up, SwiGLU, FP8 down; y written."""
+    _call("ws_shared_expert_fp8", _ptr(x), _ptr(w1), _ptr(s1), _ptr(w3), _ptr(s3), _ptr(w2),
+          _ptr(s2), _ptr(y), m, dim, inter, swiglu_limit, _ptr(workspace),
+          workspace.numel() * workspace.element_size(), _s(stream))
+
+
 # ---- routed experts, decode (launch.rs:89-206) ---------------------------------
 def expert_glu_quant(act_x, act_x_s, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slots, s_slots,
                      n, k, n_experts, top_k, swiglu_limit=10.0, stream=None):
