@@ -56,18 +56,23 @@ def test_device_expf_equals_glibc_on_every_input():
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-def test_gate_logits_bit_exact(bf16):
-    rng = np.random.default_rng(200 + bf16)
-    m, dim, E = 3, 4096, 384
+@pytest.mark.parametrize("m,dim,E", [(3, 4096, 384), (40, 1024, 100), (1, 1000, 64),
+                                     (17, 256, 33)])
+def test_gate_logits_bit_exact(bf16, m, dim, E):
+    """dim % 128 == 0: the pipelined kernel (16 x 16 blocks, partial ones at
+    the edges); otherwise the per-lane kernel."""
+    rng = np.random.default_rng(200 + bf16 + m + dim)
     x = rng.standard_normal((m, dim)).astype(np.float32)
     w = (rng.standard_normal((E, dim)) * 0.02).astype(np.float32)
     if bf16:
-        wb = np.array([O.f32_to_bf16(float(v)) for v in w.ravel()], np.uint16).reshape(E, dim)
+        bits = w.view(np.uint32)  # finite values: RNE to bf16 (quant.rs:95-101)
+        wb = ((bits + (((bits >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint16)
+        assert wb[0, 0] == O.f32_to_bf16(float(w[0, 0]))
         w = (wb.astype(np.uint32) << 16).view(np.float32)
         dw = dev(wb.view(np.int16))
     else:
         dw = dev(w)
-    announce("gate_logits bf16=%d" % bf16)
+    announce("gate_logits bf16=%d m=%d dim=%d E=%d" % (bf16, m, dim, E))
     logits = torch.empty((m, E), dtype=torch.float32, device=DEV)
     L.moe_gate_logits(dev(x), dw, logits, m, dim, E)
     got = host(logits)

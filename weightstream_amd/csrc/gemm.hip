@@ -508,24 +508,6 @@ struct PipeGeom {
 __device__ __forceinline__ int sw8(int row, int c) { return c ^ ((row >> 1) & 7); }
 __device__ __forceinline__ int sw4(int row, int c) { return c ^ ((row >> 2) & 3); }
 
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Wait until at most `newer` steps' loads (L per step) of this wave are in
-// flight; newer <= KMAX.
-template <int L, int KMAX>
-__device__ __forceinline__ void wait_newer(int newer) {
-    if constexpr (KMAX > 0) {
-        if (newer >= KMAX) wait_vm<KMAX * L>();
-        else wait_newer<L, KMAX - 1>(newer);
-    } else {
-        wait_vm<0>();
-    }
-}
-
 template <int BN, bool BFP4, int SMODE, int OMODE, bool EXACT>
 __global__ __launch_bounds__(BN == 256 ? 512 : 256) void gemm_pipe_kernel(
     const uint8_t *A, const void *SA, const uint8_t *B, const void *SB, void *__restrict__ C,

@@ -72,6 +72,111 @@ __global__ __launch_bounds__(64) void gate_logits_kernel(const float *__restrict
     if (e < n_experts) logits[(size_t)m * n_experts + e] = s;
 }
 
+// ---- gate logits, pipelined (dim % 128 == 0) --------------------------------
+// A workgroup (4 waves) computes a block of kGM tokens x kGE experts, one lane
+// per (token, expert) chain; every chain is the sequential dot of num::gemv
+// above (multiply then add, d = 0..dim-1), so the logits are the same bits.
+// The block's token rows and weight rows are streamed through a kGS-stage LDS
+// ring of kGC-element chunks by direct global->LDS loads, kGS-1 chunks ahead
+// of the chains, which read them back from LDS: the sequential adds never
+// wait on global memory. Rows keep their 16-byte pieces permuted by the row
+// index so that the 16 rows read at one position fall on distinct banks.
+constexpr int kGE = 16, kGM = 16, kGC = 128, kGS = 4;
+
+template <bool BF16>
+struct GateGeom {
+    static constexpr int kXRow = kGC * 4;                // bytes of a token row chunk
+    static constexpr int kWRow = kGC * (BF16 ? 2 : 4);   // bytes of a weight row chunk
+    static constexpr int kX = kGM * kXRow;
+    static constexpr int kW = kGE * kWRow;
+    static constexpr int kStage = kX + kW;
+    static constexpr int kLoads = kStage / 1024 / 4;     // 16-B direct loads per wave and chunk
+};
+
+template <bool BF16>
+__global__ __launch_bounds__(256) void gate_logits_pipe_kernel(const float *x, const void *gw,
+                                                               float *__restrict__ logits, int m_rows,
+                                                               int dim, int n_experts) {
+    using G = GateGeom<BF16>;
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int e0 = blockIdx.x * kGE, m0 = blockIdx.y * kGM;
+    const int nc = dim / kGC;
+    constexpr int kEB = BF16 ? 2 : 4;
+
+    // a lane's direct-load sources: fixed rows, the chunk offset moves
+    const uint8_t *src[G::kLoads];
+#pragma unroll
+    for (int j = 0; j < G::kLoads; j++) {
+        const int o = (w * G::kLoads + j) * 1024 + lane * 16;
+        if (o < G::kX) {
+            const int row = o / G::kXRow, c = (o % G::kXRow) / 16;
+            src[j] = (const uint8_t *)(x + (size_t)min(m0 + row, m_rows - 1) * dim) +
+                     (c ^ (row & 15)) * 16;
+        } else {
+            const int oo = o - G::kX;
+            const int row = oo / G::kWRow, c = (oo % G::kWRow) / 16;
+            src[j] = (const uint8_t *)gw + (size_t)min(e0 + row, n_experts - 1) * dim * kEB +
+                     (c ^ (row & 15)) * 16;
+        }
+    }
+    auto issue = [&](int buf, int chunk) {
+        uint8_t *base = g_lds + buf * G::kStage;
+#pragma unroll
+        for (int j = 0; j < G::kLoads; j++) {
+            const int off = (w * G::kLoads + j) * 1024 < G::kX ? chunk * G::kXRow : chunk * G::kWRow;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(src[j] + off),
+                (__attribute__((address_space(3))) void *)(base + (w * G::kLoads + j) * 1024), 16,
+                0, 0);
+        }
+    };
+
+    const int tm = t >> 4, te = t & 15;
+    float s = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kGS - 1; p++)
+        if (p < nc) issue(p, p);
+    for (int i = 0; i < nc; i++) {
+        mem_order();
+        wait_newer<G::kLoads, kGS - 2>(min(nc - 1 - i, kGS - 2));
+        raw_barrier();  // chunk i is in LDS for every wave; chunk i-1's buffer is free
+        if (i + kGS - 1 < nc) issue((i + kGS - 1) % kGS, i + kGS - 1);
+        const uint32_t xb = lds_addr(g_lds) + (i % kGS) * G::kStage + tm * G::kXRow;
+        const uint32_t wb = lds_addr(g_lds) + (i % kGS) * G::kStage + G::kX + te * G::kWRow;
+        // 32 elements at a time: 8 pieces of the token row, 8 (f32) or 4
+        // (bf16) pieces of the weight row
+#pragma unroll
+        for (int sub = 0; sub < kGC / 32; sub++) {
+            u32x4v xv[8], wv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) xv[k] = lds_read_b128(xb + ((sub * 8 + k) ^ (tm & 15)) * 16);
+#pragma unroll
+            for (int k = 0; k < (BF16 ? 4 : 8); k++)
+                wv[k] = lds_read_b128(wb + ((sub * (BF16 ? 4 : 8) + k) ^ (te & 15)) * 16);
+            lds_wait_all();
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                lds_ready(xv[k]);
+                if (!BF16 || k < 4) lds_ready(wv[k]);
+            }
+#pragma unroll
+            for (int j = 0; j < 32; j++) {
+                const float xe = __uint_as_float(xv[j / 4][j % 4]);
+                float we;
+                if (BF16) {
+                    const uint32_t word = wv[j / 8][(j % 8) / 2];
+                    we = __uint_as_float((j & 1) ? (word & 0xFFFF0000u) : (word << 16));
+                } else {
+                    we = __uint_as_float(wv[j / 4][j % 4]);
+                }
+                s = s + xe * we;
+            }
+        }
+    }
+    if (m0 + tm < m_rows && e0 + te < n_experts) logits[(size_t)(m0 + tm) * n_experts + e0 + te] = s;
+}
+
 // One wave per token row (wave_scores + wave_select of ws_route.hpp); the
 // softmax path keeps the reference's sequential sum (one lane, LDS).
 template <int CPL>
@@ -186,6 +291,18 @@ static int gate_logits_launch(const float *x, const void *gw, int bf16, float *l
     if (!x || !gw || !logits) return WS_ERR_INVALID_ARG;
     if (m <= 0 || dim <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 8 || m > 65535 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
+    if (dim % kGC == 0 && m <= (1 << 20)) {
+        dim3 g2((unsigned)((n_experts + kGE - 1) / kGE), (unsigned)((m + kGM - 1) / kGM));
+        if (bf16)
+            hipLaunchKernelGGL(gate_logits_pipe_kernel<true>, g2, dim3(256),
+                               kGS * GateGeom<true>::kStage, stream, x, gw, logits, (int)m,
+                               (int)dim, (int)n_experts);
+        else
+            hipLaunchKernelGGL(gate_logits_pipe_kernel<false>, g2, dim3(256),
+                               kGS * GateGeom<false>::kStage, stream, x, gw, logits, (int)m,
+                               (int)dim, (int)n_experts);
+        return launch_status();
+    }
     dim3 grid((unsigned)((n_experts + 63) / 64), (unsigned)m);
     if (bf16)
         hipLaunchKernelGGL(gate_logits_kernel<true>, grid, dim3(64), 0, stream, x, gw, logits,

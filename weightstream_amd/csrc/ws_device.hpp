@@ -120,6 +120,25 @@ __device__ __forceinline__ void lds_wait_all() { __asm__ volatile("s_waitcnt lgk
 template <class T>
 __device__ __forceinline__ void lds_ready(T &v) { __asm__ volatile("" : "+v"(v)); }
 
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maximum).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wait until at most `newer` steps' loads (L per step) of this wave are in
+// flight; newer <= KMAX.
+template <int L, int KMAX>
+__device__ __forceinline__ void wait_newer(int newer) {
+    if constexpr (KMAX > 0) {
+        if (newer >= KMAX) wait_vm<KMAX * L>();
+        else wait_newer<L, KMAX - 1>(newer);
+    } else {
+        wait_vm<0>();
+    }
+}
+
 // Barrier that orders LDS only: global loads issued before it stay in flight.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
