@@ -56,11 +56,12 @@ def test_device_expf_equals_glibc_on_every_input():
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-@pytest.mark.parametrize("m,dim,E", [(3, 4096, 384), (40, 1024, 100), (1, 1000, 64),
+@pytest.mark.parametrize("m,dim,E", [(3, 4096, 384), (1, 4096, 384), (40, 1024, 100), (1, 1000, 64), (5, 768, 50),
                                      (17, 256, 33)])
 def test_gate_logits_bit_exact(bf16, m, dim, E):
-    """dim % 128 == 0: the pipelined kernel (16 x 16 blocks, partial ones at
-    the edges); otherwise the per-lane kernel."""
+    """dim % 256 == 0: the pipelined kernel (4 x 1, 16 x 4 or 8 x 8 blocks of
+    experts x tokens, partial ones at the edges); otherwise the per-lane
+    kernel."""
     rng = np.random.default_rng(200 + bf16 + m + dim)
     x = rng.standard_normal((m, dim)).astype(np.float32)
     w = (rng.standard_normal((E, dim)) * 0.02).astype(np.float32)

@@ -72,35 +72,37 @@ __global__ __launch_bounds__(64) void gate_logits_kernel(const float *__restrict
     if (e < n_experts) logits[(size_t)m * n_experts + e] = s;
 }
 
-// ---- gate logits, pipelined (dim % 128 == 0) --------------------------------
-// A workgroup (4 waves) computes a block of kGM tokens x kGE experts, one lane
-// per (token, expert) chain; every chain is the sequential dot of num::gemv
-// above (multiply then add, d = 0..dim-1), so the logits are the same bits.
-// The block's token rows and weight rows are streamed through a kGS-stage LDS
-// ring of kGC-element chunks by direct global->LDS loads, kGS-1 chunks ahead
-// of the chains, which read them back from LDS: the sequential adds never
-// wait on global memory. Rows keep their 16-byte pieces permuted by the row
-// index so that the 16 rows read at one position fall on distinct banks.
-constexpr int kGE = 16, kGM = 16, kGC = 128, kGS = 4;
+// ---- gate logits, pipelined (dim % 256 == 0) --------------------------------
+// One wave computes a block of TM tokens x TE experts, one lane per (token,
+// expert) chain; every chain is the sequential dot of num::gemv above
+// (multiply then add, d = 0..dim-1), so the logits are the same bits. The
+// block's token rows and weight rows are streamed through a kGS-stage LDS ring
+// of kGC-element chunks by direct global->LDS loads, kGS-1 chunks ahead of the
+// chains, which read them back from LDS: the sequential adds never wait on
+// global memory. Small blocks (4 experts for one token) spread the weight
+// stream over many CUs. Rows keep their 16-byte pieces permuted by the row
+// index so that rows read at one position fall on distinct banks.
+constexpr int kGC = 256, kGS = 4;
 
-template <bool BF16>
+template <int TE, int TM, bool BF16>
 struct GateGeom {
     static constexpr int kXRow = kGC * 4;                // bytes of a token row chunk
     static constexpr int kWRow = kGC * (BF16 ? 2 : 4);   // bytes of a weight row chunk
-    static constexpr int kX = kGM * kXRow;
-    static constexpr int kW = kGE * kWRow;
+    static constexpr int kX = TM * kXRow;
+    static constexpr int kW = TE * kWRow;
     static constexpr int kStage = kX + kW;
-    static constexpr int kLoads = kStage / 1024 / 4;     // 16-B direct loads per wave and chunk
+    static constexpr int kLoads = kStage / 1024;         // 16-B direct loads per chunk
+    static_assert(kStage % 1024 == 0 && TE * TM <= 64 && (kGS - 2) * kLoads < 64, "gate block");
 };
 
-template <bool BF16>
-__global__ __launch_bounds__(256) void gate_logits_pipe_kernel(const float *x, const void *gw,
-                                                               float *__restrict__ logits, int m_rows,
-                                                               int dim, int n_experts) {
-    using G = GateGeom<BF16>;
+template <int TE, int TM, bool BF16>
+__global__ __launch_bounds__(64) void gate_logits_pipe_kernel(const float *x, const void *gw,
+                                                              float *__restrict__ logits,
+                                                              int m_rows, int dim, int n_experts) {
+    using G = GateGeom<TE, TM, BF16>;
     extern __shared__ __align__(16) uint8_t g_lds[];
-    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-    const int e0 = blockIdx.x * kGE, m0 = blockIdx.y * kGM;
+    const int lane = threadIdx.x;
+    const int e0 = blockIdx.x * TE, m0 = blockIdx.y * TM;
     const int nc = dim / kGC;
     constexpr int kEB = BF16 ? 2 : 4;
 
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256) void gate_logits_pipe_kernel(const float *x, c
     const uint8_t *src[G::kLoads];
 #pragma unroll
     for (int j = 0; j < G::kLoads; j++) {
-        const int o = (w * G::kLoads + j) * 1024 + lane * 16;
+        const int o = j * 1024 + lane * 16;
         if (o < G::kX) {
             const int row = o / G::kXRow, c = (o % G::kXRow) / 16;
             src[j] = (const uint8_t *)(x + (size_t)min(m0 + row, m_rows - 1) * dim) +
@@ -124,15 +126,14 @@ __global__ __launch_bounds__(256) void gate_logits_pipe_kernel(const float *x, c
         uint8_t *base = g_lds + buf * G::kStage;
 #pragma unroll
         for (int j = 0; j < G::kLoads; j++) {
-            const int off = (w * G::kLoads + j) * 1024 < G::kX ? chunk * G::kXRow : chunk * G::kWRow;
+            const int off = j * 1024 < G::kX ? chunk * G::kXRow : chunk * G::kWRow;
             __builtin_amdgcn_global_load_lds(
                 (const void *)(src[j] + off),
-                (__attribute__((address_space(3))) void *)(base + (w * G::kLoads + j) * 1024), 16,
-                0, 0);
+                (__attribute__((address_space(3))) void *)(base + j * 1024), 16, 0, 0);
         }
     };
 
-    const int tm = t >> 4, te = t & 15;
+    const int tm = min(lane / TE, TM - 1), te = lane % TE;
     float s = 0.0f;
 #pragma unroll
     for (int p = 0; p < kGS - 1; p++)
@@ -140,41 +141,70 @@ __global__ __launch_bounds__(256) void gate_logits_pipe_kernel(const float *x, c
     for (int i = 0; i < nc; i++) {
         mem_order();
         wait_newer<G::kLoads, kGS - 2>(min(nc - 1 - i, kGS - 2));
-        raw_barrier();  // chunk i is in LDS for every wave; chunk i-1's buffer is free
+        raw_barrier();  // chunk i is in LDS; chunk i-1's buffer is free
         if (i + kGS - 1 < nc) issue((i + kGS - 1) % kGS, i + kGS - 1);
         const uint32_t xb = lds_addr(g_lds) + (i % kGS) * G::kStage + tm * G::kXRow;
         const uint32_t wb = lds_addr(g_lds) + (i % kGS) * G::kStage + G::kX + te * G::kWRow;
-        // 32 elements at a time: 8 pieces of the token row, 8 (f32) or 4
-        // (bf16) pieces of the weight row
+        // 16 elements at a time: 4 pieces of the token row and 4 (f32) or 2
+        // (bf16) of the weight row; the next group's reads are issued before
+        // this group's adds, so LDS latency overlaps the chain
+        constexpr int kWP = BF16 ? 2 : 4;        // weight pieces per group
+        constexpr int kRd = 4 + kWP;             // LDS reads per group
+        u32x4v xv[2][4], wv[2][4];
+        auto reads = [&](int grp, u32x4v *xr, u32x4v *wr) {
 #pragma unroll
-        for (int sub = 0; sub < kGC / 32; sub++) {
-            u32x4v xv[8], wv[8];
+            for (int k = 0; k < 4; k++) xr[k] = lds_read_b128(xb + ((grp * 4 + k) ^ (tm & 15)) * 16);
 #pragma unroll
-            for (int k = 0; k < 8; k++) xv[k] = lds_read_b128(xb + ((sub * 8 + k) ^ (tm & 15)) * 16);
+            for (int k = 0; k < kWP; k++) wr[k] = lds_read_b128(wb + ((grp * kWP + k) ^ (te & 15)) * 16);
+        };
+        reads(0, xv[0], wv[0]);
 #pragma unroll
-            for (int k = 0; k < (BF16 ? 4 : 8); k++)
-                wv[k] = lds_read_b128(wb + ((sub * (BF16 ? 4 : 8) + k) ^ (te & 15)) * 16);
-            lds_wait_all();
-#pragma unroll
-            for (int k = 0; k < 8; k++) {
-                lds_ready(xv[k]);
-                if (!BF16 || k < 4) lds_ready(wv[k]);
+        for (int grp = 0; grp < kGC / 16; grp++) {
+            const int cur = grp & 1;
+            if (grp + 1 < kGC / 16) {
+                reads(grp + 1, xv[cur ^ 1], wv[cur ^ 1]);
+                lds_wait<kRd>();
+            } else {
+                lds_wait<0>();
             }
 #pragma unroll
-            for (int j = 0; j < 32; j++) {
-                const float xe = __uint_as_float(xv[j / 4][j % 4]);
+            for (int k = 0; k < 4; k++) lds_ready(xv[cur][k]);
+#pragma unroll
+            for (int k = 0; k < kWP; k++) lds_ready(wv[cur][k]);
+            // the 16 products first (independent), then the 16 dependent adds
+            float pr[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const float xe = __uint_as_float(xv[cur][j / 4][j % 4]);
                 float we;
                 if (BF16) {
-                    const uint32_t word = wv[j / 8][(j % 8) / 2];
+                    const uint32_t word = wv[cur][j / 8][(j % 8) / 2];
                     we = __uint_as_float((j & 1) ? (word & 0xFFFF0000u) : (word << 16));
                 } else {
-                    we = __uint_as_float(wv[j / 4][j % 4]);
+                    we = __uint_as_float(wv[cur][j / 4][j % 4]);
                 }
-                s = s + xe * we;
+                pr[j] = xe * we;
             }
+#pragma unroll
+            for (int j = 0; j < 16; j++) s = s + pr[j];
         }
     }
-    if (m0 + tm < m_rows && e0 + te < n_experts) logits[(size_t)(m0 + tm) * n_experts + e0 + te] = s;
+    if (lane < TE * TM && m0 + tm < m_rows && e0 + te < n_experts)
+        logits[(size_t)(m0 + tm) * n_experts + e0 + te] = s;
+}
+
+template <int TE, int TM>
+static void gate_pipe_launch(const float *x, const void *gw, int bf16, float *logits, int64_t m,
+                             int64_t dim, int64_t n_experts, hipStream_t stream) {
+    dim3 g((unsigned)((n_experts + TE - 1) / TE), (unsigned)((m + TM - 1) / TM));
+    if (bf16)
+        hipLaunchKernelGGL((gate_logits_pipe_kernel<TE, TM, true>), g, dim3(64),
+                           (kGS * GateGeom<TE, TM, true>::kStage), stream, x, gw, logits, (int)m,
+                           (int)dim, (int)n_experts);
+    else
+        hipLaunchKernelGGL((gate_logits_pipe_kernel<TE, TM, false>), g, dim3(64),
+                           (kGS * GateGeom<TE, TM, false>::kStage), stream, x, gw, logits, (int)m,
+                           (int)dim, (int)n_experts);
 }
 
 // One wave per token row (wave_scores + wave_select of ws_route.hpp); the
@@ -292,15 +322,11 @@ static int gate_logits_launch(const float *x, const void *gw, int bf16, float *l
     if (m <= 0 || dim <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 8 || m > 65535 || n_experts > (1 << 20)) return WS_ERR_SHAPE;
     if (dim % kGC == 0 && m <= (1 << 20)) {
-        dim3 g2((unsigned)((n_experts + kGE - 1) / kGE), (unsigned)((m + kGM - 1) / kGM));
-        if (bf16)
-            hipLaunchKernelGGL(gate_logits_pipe_kernel<true>, g2, dim3(256),
-                               kGS * GateGeom<true>::kStage, stream, x, gw, logits, (int)m,
-                               (int)dim, (int)n_experts);
-        else
-            hipLaunchKernelGGL(gate_logits_pipe_kernel<false>, g2, dim3(256),
-                               kGS * GateGeom<false>::kStage, stream, x, gw, logits, (int)m,
-                               (int)dim, (int)n_experts);
+        // one token: 4 experts per wave (the weight stream spread over many
+        // CUs); a few tokens: 16 x 4 blocks; more: 8 x 8
+        if (m == 1) gate_pipe_launch<4, 1>(x, gw, bf16, logits, m, dim, n_experts, stream);
+        else if (m <= 4) gate_pipe_launch<16, 4>(x, gw, bf16, logits, m, dim, n_experts, stream);
+        else gate_pipe_launch<8, 8>(x, gw, bf16, logits, m, dim, n_experts, stream);
         return launch_status();
     }
     dim3 grid((unsigned)((n_experts + 63) / 64), (unsigned)m);

@@ -117,6 +117,13 @@ __device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
     return v;
 }
 __device__ __forceinline__ void lds_wait_all() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Wait until at most N of this wave's LDS reads (lds_read_*) are in flight;
+// LDS reads complete in issue order.
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N) : "memory");
+}
 template <class T>
 __device__ __forceinline__ void lds_ready(T &v) { __asm__ volatile("" : "+v"(v)); }
 
