@@ -41,9 +41,9 @@ FP4_SC = INTER * DIM // 32          # UE8M0 bytes of one matrix
 EXPERT_BYTES = 3 * (FP4_MAT + FP4_SC)
 # HBM bytes per launch of the exact-math gate/up kernel at config 3, from
 # rocprofv3 FETCH_SIZE + WRITE_SIZE counter runs calibrated against a plain
-# 256 MiB copy (profiles/traffic_expert_kernels_moe_decode.md holds the runs and
+# 256 MiB copy (profiles/traffic_hot_kernels.md holds the runs and
 # commands; counters cannot be read from inside this process).
-GLU_TRAFFIC_BYTES = 71805786
+GLU_TRAFFIC_BYTES = 71806821
 
 
 def log(*a):
@@ -476,7 +476,7 @@ def main():
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["GB/s"] / PEAK_HBM_GBS,
             "traffic": GLU_TRAFFIC_BYTES,
             "algorithmic_bytes": k["bytes"], "avg_us": k["avg_us"],
-            "traffic_source": "profiles/traffic_expert_kernels_moe_decode.md"}
+            "traffic_source": "profiles/traffic_hot_kernels.md"}
     cpu = None
     if not args.no_cpu:
         import multiprocessing
