@@ -67,8 +67,10 @@ def _run_decode(x, idx, w, packed, dim, inter, E, k, limit=10.0):
 
 @pytest.mark.parametrize("E,dim,inter,k", [(16, 1024, 512, 4), (64, 2048, 768, 6),
                                            (384, 4096, 2048, 8), (8, 128, 128, 3),
-                                           (8, 10240, 256, 2)])
+                                           (8, 10240, 256, 2), (24, 5120, 2304, 6)])
 def test_moe_decode_matches_oracle(E, dim, inter, k):
+    """(24, 5120, 2304, 6): the DS4.1F expert shape (dim 5120, moe_inter_dim
+    2304, top-6; weightstream-ref testdata/config-1017.json)."""
     rng = np.random.default_rng(700 + E)
     gen = torch.Generator(device=DEV)
     gen.manual_seed(E)
@@ -201,7 +203,8 @@ def test_prepack_fp4_layout():
 
 
 @pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (64, 2048, 768, 6, 2),
-                                                 (100, 1024, 512, 4, 1), (32, 1024, 256, 4, 0)])
+                                                 (100, 1024, 512, 4, 1), (32, 1024, 256, 4, 0),
+                                                 (384, 5120, 2304, 6, 2)])
 def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
     """The routing computed inside the gate/up kernel gives the same picks and
     weights as ws_moe_topk (bit for bit) and the same y as ws_moe_decode on
