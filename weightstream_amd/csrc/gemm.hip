@@ -259,6 +259,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 template <int MF, int NF, int U>
 struct KpStage {
     uint4 a[U][MF][2];
+    uint32_t sa[U][MF];
     uint4 b[U][NF][2];
     uint32_t sb[U][NF];
     float sbf[U];
@@ -274,6 +275,9 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                                                                 int N, int K) {
     constexpr int kRows = 16 * MF * GMH;
     constexpr int kCols = 16 * NF;
+    // UE8M0 activation scales: staged in LDS for blocks of rows; a single
+    // 16-row fragment (GEMV) loads its word per step instead (no prologue)
+    constexpr bool kStageSa = SMODE == kF32s || kRows > 16;
     constexpr int kThreads = 64 * GMH * GK;
     extern __shared__ __align__(16) float kp_lds[];
     float *part = kp_lds;                         // [GK][kRows][kCols]
@@ -293,7 +297,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     // four steps at a time, and staged in LDS as [step][row].
     uint4 sav[kKpMaxSaPerThread];
     const int nsa = kRows * ksteps;  // <= kThreads * 4 * kKpMaxSaPerThread (checked on the host)
-    {
+    if (kStageSa) {
 #pragma unroll
         for (int j = 0; j < kKpMaxSaPerThread; j++) {
             // element e = row_local * ksteps + ks, four at a time (ksteps % 4 == 0)
@@ -308,10 +312,12 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     }
 
     const uint8_t *arow[MF];
+    const uint8_t *sarow[MF];
 #pragma unroll
     for (int i = 0; i < MF; i++) {
         const int row = min(mb + ml + 16 * i + r, M - 1);
         arow[i] = A + (size_t)row * K + (EXACT ? g * 32 : g * 16);
+        sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
     }
     const uint8_t *brow[NF];
     const uint8_t *sbrow[NF];
@@ -333,6 +339,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                 const uint8_t *p = arow[i] + (size_t)ks * 128;
                 st.a[u][i][0] = ldg16(p);
                 st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
+                if (!kStageSa) st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * g);
             }
 #pragma unroll
             for (int j = 0; j < NF; j++) {
@@ -371,10 +378,9 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
 #pragma unroll
                 for (int i = 0; i < MF; i++) {
                     v8bf aq[4];
-                    const float sav_f =
-                        SMODE == kUe8m0
-                            ? e8m0_to_f32((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF)
-                            : 1.0f;
+                    const uint32_t saw = !kStageSa ? st.sa[u][i]
+                                         : ((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g);
+                    const float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(saw & 0xFF) : 1.0f;
                     cvt_fp8x32(st.a[u][i][0], st.a[u][i][1], sav_f, aq);
 #pragma unroll
                     for (int j = 0; j < NF; j++) {
@@ -398,9 +404,10 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
 #pragma unroll
                 for (int i = 0; i < MF; i++) {
                     const v8i a = frag_from(st.a[u][i][0], st.a[u][i][1]);
-                    const int sai = SMODE == kUe8m0
-                                        ? (int)((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF)
-                                        : 0;
+                    const int sai =
+                        SMODE != kUe8m0 ? 0
+                        : !kStageSa     ? (int)(st.sa[u][i] & 0xFF)
+                                        : (int)((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF);
 #pragma unroll
                     for (int j = 0; j < NF; j++) {
                         if (SMODE == kUe8m0) {
@@ -428,7 +435,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     mem_order();
     load(s1, k0 + U);
     mem_order();
-    {
+    if (kStageSa) {
         uint32_t *sa_w = (uint32_t *)sa_l;
 #pragma unroll
         for (int j = 0; j < kKpMaxSaPerThread; j++) {
@@ -489,7 +496,8 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     constexpr int rows = 16 * MF * GMH, threads = 64 * GMH * GK;
     if (n % (16 * NF)) return -1;
     const int ksteps = k / 128;
-    if (rows * ksteps > threads * 4 * kKpMaxSaPerThread || ksteps % 4 || ((uintptr_t)sa & 15))
+    constexpr bool stage = SMODE == kF32s || rows > 16;
+    if (stage && (rows * ksteps > threads * 4 * kKpMaxSaPerThread || ksteps % 4 || ((uintptr_t)sa & 15)))
         return -1;  // caller falls back to the general kernel
     size_t lds = (size_t)GK * rows * 16 * NF * 4 + (size_t)ksteps * rows * 4;
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows));
