@@ -206,6 +206,39 @@ def test_fp8_gemm_full_size_vs_fp64_dequant(n, gemm_path):
     assert_close(host(out), want, GEMM_TOL, "fp8_gemm full %dx%dx%d" % (m, n, k))
 
 
+# The engine's FP8 projection shapes (N, K) (weightstream-gpu engine.rs:3388-3398:
+# q_a, q_b, wkv, wo_b, shared w1/w3, fused w13, shared w2, engram wkv, drafter).
+MODEL_SHAPES = [(1280, 5120), (8192, 1280), (512, 5120), (5120, 2048), (2304, 5120),
+                (4608, 5120), (5120, 2304), (25600, 5120), (1280, 15360)]
+
+
+@pytest.mark.parametrize("n,k", MODEL_SHAPES)
+@pytest.mark.parametrize("m", [1, 6, 128])
+def test_fp8_gemm_model_shapes_vs_fp64_dequant(m, n, k, gemm_path):
+    """The real projection shapes through the dispatch (every kernel family
+    and the fallbacks for K/128 not a multiple of 4), against an f64 matmul of
+    the dequantised operands on the device."""
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(m * 7 + n + k)
+    announce("fp8_gemm model shape %s m=%d n=%d k=%d" % (gemm_path, m, n, k))
+    x = torch.randn((m, k), device=DEV, generator=gen)
+    w = torch.randn((n, k), device=DEV, generator=gen) * 0.02
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    as_ = torch.empty((m, k // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, aq, as_, m * k)
+    wq = torch.empty((n, k), dtype=torch.uint8, device=DEV)
+    ws = torch.empty(((n + 31) // 32, k // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(w, wq, ws, n, k)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm(aq, as_, wq, ws, out, m, n, k)
+    table = torch.from_numpy(O.e4m3_decode_table().astype(np.float64)).to(DEV)
+    pw = lambda s: torch.pow(2.0, s.to(torch.float64) - 127)
+    da = table[aq.long()] * pw(as_).repeat_interleave(32, 1)
+    dw = table[wq.long()] * pw(ws).repeat_interleave(32, 0)[:n].repeat_interleave(32, 1)
+    want = (da @ dw.T).cpu().numpy()
+    assert_close(host(out), want, GEMM_TOL, "fp8_gemm %dx%dx%d" % (m, n, k))
+
+
 def test_gemm_rejects_bad_shapes():
     a = torch.zeros(256, dtype=torch.uint8, device=DEV)
     out = torch.zeros(256, dtype=torch.float32, device=DEV)

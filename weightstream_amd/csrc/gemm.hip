@@ -265,7 +265,7 @@ struct KpStage {
     float sbf[U];
 };
 
-constexpr int kKpMaxSaPerThread = 4;  // f32 A scales staged per thread (float4 each)
+constexpr int kKpMaxSaWords = 16;  // activation scale words staged per thread
 
 template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT>
 __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A, const void *SA,
@@ -293,20 +293,37 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     const int kbn = K / 32, kb128 = K / 128;
 
     // activation scales of the workgroup's rows, one 32-bit word per (row,
-    // step): the f32 scale, or the step's four UE8M0 bytes. Loaded first,
-    // four steps at a time, and staged in LDS as [step][row].
-    uint4 sav[kKpMaxSaPerThread];
-    const int nsa = kRows * ksteps;  // <= kThreads * 4 * kKpMaxSaPerThread (checked on the host)
+    // step): the f32 scale, or the step's four UE8M0 bytes. Loaded first
+    // and staged in LDS as [step][row].
+    // four steps per 16-byte load when the rows allow it, else word by word
+    uint32_t sav[kKpMaxSaWords];
+    const int nsa = kRows * ksteps;  // <= kThreads * kKpMaxSaWords (checked on the host)
+    const bool quad = (ksteps % 4) == 0 && (((uintptr_t)SA & 15) == 0);
     if (kStageSa) {
+        if (quad) {
 #pragma unroll
-        for (int j = 0; j < kKpMaxSaPerThread; j++) {
-            // element e = row_local * ksteps + ks, four at a time (ksteps % 4 == 0)
-            const int e = min((j * kThreads + t) * 4, nsa - 4);
-            const int rl = e / ksteps, ks = e % ksteps;
-            const int row = min(mb + rl, M - 1);
-            sav[j] = SMODE == kF32s
-                         ? *(const uint4 *)((const float *)SA + (size_t)row * kb128 + ks)
-                         : *(const uint4 *)((const uint8_t *)SA + (size_t)row * kbn + ks * 4);
+            for (int j = 0; j < kKpMaxSaWords / 4; j++) {
+                // words e..e+3 = row_local * ksteps + ks .. +3
+                const int e = min((j * kThreads + t) * 4, nsa - 4);
+                const int rl = e / ksteps, ks = e % ksteps;
+                const int row = min(mb + rl, M - 1);
+                const uint4 v = SMODE == kF32s
+                                    ? *(const uint4 *)((const uint32_t *)SA + (size_t)row * kb128 + ks)
+                                    : *(const uint4 *)((const uint8_t *)SA + (size_t)row * kbn + ks * 4);
+                sav[4 * j] = v.x;
+                sav[4 * j + 1] = v.y;
+                sav[4 * j + 2] = v.z;
+                sav[4 * j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kKpMaxSaWords; j++) {
+                const int e = min(j * kThreads + t, nsa - 1);
+                const int rl = e / ksteps, ks = e % ksteps;
+                const int row = min(mb + rl, M - 1);
+                sav[j] = SMODE == kF32s ? *((const uint32_t *)SA + (size_t)row * kb128 + ks)
+                                        : *(const uint32_t *)((const uint8_t *)SA + (size_t)row * kbn + ks * 4);
+            }
         }
         mem_order();
     }
@@ -438,13 +455,11 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     if (kStageSa) {
         uint32_t *sa_w = (uint32_t *)sa_l;
 #pragma unroll
-        for (int j = 0; j < kKpMaxSaPerThread; j++) {
-            const int e = (j * kThreads + t) * 4;
+        for (int j = 0; j < kKpMaxSaWords; j++) {
+            const int e = quad ? ((j / 4) * kThreads + t) * 4 + j % 4 : j * kThreads + t;
             if (e >= nsa) continue;
             const int rl = e / ksteps, ks = e % ksteps;
-            const uint32_t v[4] = {sav[j].x, sav[j].y, sav[j].z, sav[j].w};
-#pragma unroll
-            for (int c = 0; c < 4; c++) sa_w[(ks + c) * kRows + rl] = v[c];
+            sa_w[ks * kRows + rl] = sav[j];
         }
         lds_barrier();
     }
@@ -497,7 +512,7 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     if (n % (16 * NF)) return -1;
     const int ksteps = k / 128;
     constexpr bool stage = SMODE == kF32s || rows > 16;
-    if (stage && (rows * ksteps > threads * 4 * kKpMaxSaPerThread || ksteps % 4 || ((uintptr_t)sa & 15)))
+    if (stage && rows * ksteps > threads * kKpMaxSaWords)
         return -1;  // caller falls back to the general kernel
     size_t lds = (size_t)GK * rows * 16 * NF * 4 + (size_t)ksteps * rows * 4;
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows));
