@@ -288,6 +288,47 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
     return out
 
 
+def bench_model_shapes(L, torch, dev, reps=40, Ms=(1, 128)):
+    """the engine's other FP8 projections at their real (N, K)
+    (weightstream-gpu engine.rs:3388-3398), UE8M0 scales, exact math, bf16
+    out, weights rotated over > 400 MB of copies (cold)."""
+    shapes = {"q_a": (1280, 5120), "q_b": (8192, 1280), "wkv": (512, 5120),
+              "wo_b": (5120, 2048), "shared_w13": (2304, 5120), "shared_w13_fused": (4608, 5120),
+              "shared_w2": (5120, 2304), "engram_wkv": (25600, 5120),
+              "drafter_main_proj": (1280, 15360)}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    ws = torch.empty(max(L.gemm_workspace_size(128, n, k) for n, k in shapes.values()) + 256,
+                     dtype=torch.uint8, device=dev)
+    L.set_gemm_workspace(ws)
+    out = {}
+    for name, (N, K) in shapes.items():
+        copies = max(2, math.ceil(400e6 / (N * K)))
+        w = torch.randn((N, K), device=dev, generator=gen) * 0.02
+        wq = torch.empty((copies, N, K), dtype=torch.uint8, device=dev)
+        ws8 = torch.empty((copies, (N + 31) // 32, K // 32), dtype=torch.uint8, device=dev)
+        for c in range(copies):
+            L.weight_quant_fp8(w, wq[c], ws8[c], N, K)
+        res = {}
+        for M in Ms:
+            x = torch.randn((M, K), device=dev, generator=gen)
+            aq = torch.empty((M, K), dtype=torch.uint8, device=dev)
+            asc = torch.empty((M, K // 32), dtype=torch.uint8, device=dev)
+            L.emit8(x, aq, asc, M * K)
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            run = lambda i, st: L.fp8_gemm_bf16(aq, asc, wq[i % copies], ws8[i % copies], y, M, N,
+                                                K, stream=st)
+            avg, _ = graph_time(torch, run, reps)
+            byts = N * K + (N // 32) * (K // 32) + M * K + M * N * 2
+            res["m%d" % M] = {"avg_us": avg * 1e3, "GB/s": byts / (avg * 1e-3) / 1e9,
+                              "TFLOP/s": 2.0 * M * N * K / (avg * 1e-3) / 1e12}
+        out["%s_%dx%d" % (name, N, K)] = res
+        del wq, ws8
+    torch.cuda.synchronize()
+    L.set_gemm_workspace(None)
+    return out
+
+
 def bench_prefill(L, torch, dev, packed, reps, m=132):
     """Config 4: grouped prefill of m tokens through the same 384-expert layer,
     router logits skewed by Zipf(1.1) popularity (log p_e added to N(0,1)
@@ -496,10 +537,11 @@ def main():
     L.set_math_mode(L.MATH_EXACT)
     log("prefill: %s" % prefill)
     block = bench_block(L, torch, dev, packed, gen) if not args.no_block else None
-    gemm = gemv = None
+    gemm = gemv = shapes = None
     if not args.no_gemm:
         gemv = bench_gemm(L, torch, dev, 100, M=1, Ns=(4096,))
         gemm = bench_gemm(L, torch, dev, 40)
+        shapes = bench_model_shapes(L, torch, dev)
 
     line = {
         "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
@@ -528,6 +570,7 @@ def main():
                         "note": "FP4xFP8 scaled MFMA; ~13-bit internal accumulation"},
         "fp8_gemv_m1": gemv,
         "fp8_gemm_m128": gemm,
+        "fp8_gemm_model_shapes": shapes,
         "moe_prefill_m132": prefill,
         "moe_block_4_layers": block,
     }
