@@ -278,8 +278,8 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
  * moe_grouped_tl(_cached)(_on) :478-580, moe_swiglu_route :673,
  * moe_combine_f32 :689). Routes r = token * top_k + j. Expert slabs are
  * packed (ws_prepack_fp4). Shapes: dim and inter multiples of 128, dim <=
- * 4096 (a 32-slot tile of x is staged in LDS), inter <= 2048; WS_ERR_SHAPE
- * otherwise.
+ * 8192 (a 32-slot tile of x, or above 4096 a 16-slot half of it, is staged
+ * in LDS), inter <= 4096; WS_ERR_SHAPE otherwise.
  * ------------------------------------------------------------------- */
 /* launch.rs:430-468 moe_dispatch_tl (moe_dispatch.cu:17): per-expert counts,
  * 32-padded offsets in ascending expert id (exclusive scan), psum = offset +

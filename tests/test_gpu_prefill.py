@@ -2,13 +2,24 @@
 work and bit-exact with the oracle's restatement of moe_dispatch_kernel's
 contract; the grouped MoE output matches the per-token CPU MoE
 (weightstream-ref moe.rs:75-84,162-208) within max relative error 1e-3
-(floor at 1% of the output scale), the tolerance of the decode path."""
+(floor at 1% of the output scale), the tolerance of the decode path.
+
+The hidden state h is re-quantised to FP8 between the two GEMMs. An element
+of h whose exact value sits within f32 reassociation distance of an e4m3
+rounding midpoint can land one step apart in the oracle (sequential f32 dot)
+and on the GPU (MFMA accumulation); that step, times one column of w2, can
+exceed the end-to-end tolerance. A row that misses the tolerance is therefore
+re-checked stage by stage: every element where the GPU's h differs from the
+oracle's must be such a midpoint case (adjacent e4m3 values, the oracle's f32 h within
+1e-4 of the block's scale from the midpoint), and the output must then match
+the oracle's down projection and expert-ordered sum of the GPU's h within the
+same tolerance."""
 import numpy as np
 import pytest
 import torch
 
 import oracle_lib as O
-from gpu_util import DEV, announce, assert_close, dev, host, rand_fp4_weights
+from gpu_util import DEV, announce, assert_close, dev, host, rand_fp4_weights, rel_err_stats
 from weightstream_amd import launch as L
 
 pytestmark = pytest.mark.gpu
@@ -98,7 +109,9 @@ def _host_experts(slabs, experts, E, dim, inter):
 
 @pytest.mark.parametrize("m,E,dim,inter,k,check", [(40, 64, 1024, 512, 6, 40),
                                                     (132, 384, 4096, 2048, 8, 6),
-                                                    (5, 16, 512, 256, 4, 5)])
+                                                    (5, 16, 512, 256, 4, 5),
+                                                    (96, 64, 5120, 2304, 6, 6),
+                                                    (33, 8, 8192, 4096, 2, 4)])
 def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
     rng = np.random.default_rng(900 + m + E)
     gen = torch.Generator(device=DEV)
@@ -117,9 +130,63 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
     gi, gw, gy = host(idx), host(w), host(y)
     rows = np.linspace(0, m - 1, check).astype(int)
     H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
+    staged = None
     for r in rows:
         want = O.moe_routed(*H, dim, inter, x[r], gi[r], gw[r])
-        assert_close(gy[r], want, MOE_TOL, "moe_prefill row %d" % r)
+        if rel_err_stats(gy[r], want)[0] <= MOE_TOL:
+            assert_close(gy[r], want, MOE_TOL, "moe_prefill row %d" % r)
+            continue
+        if staged is None:
+            staged = _staged_hidden(x, idx, w, _packed(slabs, E, dim, inter), m, E, dim, inter, k)
+        _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
+
+
+def _staged_hidden(x, idx, w, P, m, E, dim, inter, k):
+    """The GPU's re-quantised h per slot (emit8 + dispatch + grouped gate/up),
+    decoded to f32, and route -> slot."""
+    routes = m * k
+    tiles = L.moe_tiles(routes, E)
+    xq = torch.empty((m, dim), dtype=torch.uint8, device=DEV)
+    xs = torch.empty((m, dim // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(dev(x), xq, xs, m * dim)
+    i32 = lambda n: torch.empty(n, dtype=torch.int32, device=DEV)
+    order, rp, te, nt = i32(tiles * 32), i32(routes), i32(tiles), i32(1)
+    lw = torch.empty(tiles * 32, dtype=torch.float32, device=DEV)
+    L.moe_dispatch_tl(idx, w, order, lw, rp, te, i32(E), i32(E), i32(E), nt, m, k, tiles, E)
+    hq = torch.zeros((tiles * 32, inter), dtype=torch.uint8, device=DEV)
+    hs = torch.zeros((tiles * 32, inter // 32), dtype=torch.uint8, device=DEV)
+    L.moe_grouped_glu_quant(xq, xs, order, lw, te, nt, P[0], P[1], P[2], P[3], hq, hs, dim,
+                            inter, E, k, tiles, 10.0)
+    torch.cuda.synchronize()
+    tab = O.e4m3_decode_table().astype(np.float64)
+    h = tab[host(hq)] * np.repeat(2.0 ** (host(hs).astype(np.float64) - 127), 32, axis=1)
+    return h, host(rp)
+
+
+def _check_by_stages(got_row, x_row, gi, gw, H, staged, r, k, dim, inter, limit=10.0):
+    h_gpu, route_pos = staged
+    y = np.zeros(dim, np.float32)
+    flips = 0
+    for j in np.argsort(gi, kind="stable"):  # expert order, as moe.rs:75-84 sums
+        e, rw = int(gi[j]), float(gw[j])
+        g = O.fp4_gemv(H[0][e], H[1][e], inter, dim, x_row).astype(np.float64)
+        u = O.fp4_gemv(H[2][e], H[3][e], inter, dim, x_row).astype(np.float64)
+        g, u = np.minimum(g, limit), np.clip(u, -limit, limit)
+        h_pre = g / (1.0 + np.exp(-g)) * u * rw
+        h_or = O.fp8_snap(h_pre.astype(np.float32)).astype(np.float64)
+        hg = h_gpu[route_pos[r * k + j]]
+        for i in np.nonzero(hg != h_or)[0]:
+            blk = np.abs(h_or[i // 32 * 32:(i // 32 + 1) * 32]).max()
+            mid = 0.5 * (hg[i] + h_or[i])
+            assert abs(hg[i] - h_or[i]) <= blk / 8, "row %d h[%d]: not adjacent" % (r, i)
+            assert abs(h_pre[i] - mid) <= 1e-4 * blk, \
+                "row %d h[%d]: %r vs %r, not a rounding midpoint" % (r, i, hg[i], h_or[i])
+            flips += 1
+        y += O.fp4_gemv(H[4][e], H[5][e], dim, inter, hg.astype(np.float32))
+    print("[moe_prefill row %d] %d h element(s) on an e4m3 rounding midpoint" % (r, flips),
+          flush=True)
+    assert flips > 0, "row %d misses the tolerance with h identical to the oracle's" % r
+    assert_close(got_row, y, MOE_TOL, "moe_prefill row %d (staged)" % r)
 
 
 def test_prefill_of_one_token_matches_decode():
@@ -140,3 +207,17 @@ def test_prefill_of_one_token_matches_decode():
     y2 = torch.empty(dim, dtype=torch.float32, device=DEV)
     L.moe_decode(x[0], idx[0], w[0], *slabs, y2, dim, inter, E, k, wsd)
     assert_close(host(y1)[0], host(y2), MOE_TOL, "prefill(1) vs decode")
+
+
+def test_moe_prefill_rejects_oversized_shapes():
+    """dim above 8192 or inter above 4096 do not fit the LDS-staged A tile."""
+    k, E = 2, 4
+    for dim, inter in [(8320, 256), (256, 4224)]:
+        ws = torch.empty(L.moe_prefill_workspace_size(4, dim, inter, k, E), dtype=torch.uint8,
+                         device=DEV)
+        b = torch.zeros(1 << 12, dtype=torch.uint8, device=DEV)
+        f = torch.zeros(4 * dim, dtype=torch.float32, device=DEV)
+        idx = torch.zeros((4, k), dtype=torch.int32, device=DEV)
+        w = torch.zeros((4, k), dtype=torch.float32, device=DEV)
+        with pytest.raises(RuntimeError, match="unsupported shape"):
+            L.moe_prefill(f, idx, w, b, b, b, b, b, b, f, 4, dim, inter, E, k, ws)

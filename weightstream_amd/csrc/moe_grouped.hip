@@ -131,31 +131,35 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
 }
 
 // ---- grouped expert GEMM streaming ----------------------------------------
-// Work unit = (32-slot tile, block of output columns). The grid has one
-// workgroup per CU; workgroup i takes the contiguous units
-// [i*U/G, (i+1)*U/G) of the U = used_tiles x column_blocks units (the used
-// tile count is read on the device, so every workgroup gets an equal share).
-// Within a unit each wave streams one packed 16-row FP4 band of the tile's
-// expert over its K range in two register stages (steps [k0, k0+8) and
-// [k0+8, k1)); the stages of the next unit are loaded while the current unit
-// is multiplied, so the weight stream never drains between units. The tile's
-// A rows (32 token rows of x for gate/up, 32 slot rows of hq for down; FP8 +
-// UE8M0) sit in LDS, copied with direct global->LDS loads whenever the
-// workgroup moves to a new tile.
+// Work unit = (ROWS-slot A block of a 32-slot tile, block of output columns).
+// The grid has one workgroup per CU; workgroup i takes the contiguous units
+// [i*U/G, (i+1)*U/G) of the U = used_tiles x (32/ROWS) x column_blocks units
+// (the used tile count is read on the device, so every workgroup gets an
+// equal share). Within a unit each wave streams one packed 16-row FP4 band of
+// the tile's expert over its K range as a sequence of 8-step chunks held in
+// two register stages: chunk q of the workgroup's run (unit q / nch, chunk
+// q % nch) sits in stage q & 1, and chunk q + 2 is loaded as soon as chunk q
+// is multiplied, so the weight stream runs on across chunks and units. The
+// A block (ROWS token rows of x for gate/up, 32 slot rows of hq for down;
+// FP8 + UE8M0) sits in LDS, copied with direct global->LDS loads whenever
+// the workgroup moves to a new block. ROWS is 32, or 16 when a 32-row block
+// of the K bytes would not fit in LDS (gate/up at dim > 4096; the 16-row
+// halves of a tile then stream the weights once each).
 constexpr int kGThreads = 512;  // 8 waves
+constexpr int kGCols = 32;      // gate/up columns (intermediate rows) per unit
 
-// The tile's 32 A rows into LDS, a_l[32][K + 16] (the 16-byte pad spreads the
-// rows of an MFMA fragment over the LDS banks) and their UE8M0 bytes
-// as_l[32][K/32], with direct global->LDS loads (global_load_lds_dwordx4 /
-// _dword: no VGPR staging). One instruction fills a contiguous 1 KB (256 B)
-// of the LDS image; lane l moves the 16 (4) bytes at image offset o, which
-// belong to row o / pitch (pad bytes repeat the row's last piece). Row i of A
-// starts at arow(i), its scales at srow(i). Completion is awaited by the
-// caller (vmcnt) before the barrier.
+// A block of `rows` A rows into LDS, a_l[rows][K + 16] (the 16-byte pad
+// spreads the rows of an MFMA fragment over the LDS banks) and their UE8M0
+// bytes as_l[rows][K/32], with direct global->LDS loads
+// (global_load_lds_dwordx4 / _dword: no VGPR staging). One instruction fills a
+// contiguous 1 KB (256 B) of the LDS image; lane l moves the 16 (4) bytes at
+// image offset o, which belong to row o / pitch (pad bytes repeat the row's
+// last piece). Row i of A starts at arow(i), its scales at srow(i). Completion
+// is awaited by the caller (vmcnt) before the barrier.
 template <class ARow, class SRow>
-__device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, int lane,
+__device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int rows, int K, int w, int lane,
                                            uint8_t *a_l, uint8_t *as_l) {
-    const int pitch = K + 16, total = kTile * pitch;
+    const int pitch = K + 16, total = rows * pitch;
     const int nq = (total + 1023) / 1024;  // the last piece overhangs into the image's slack
     for (int c = w; c < nq; c += kGThreads / 64) {
         const int o = min(c * 1024 + lane * 16, total - 16);
@@ -164,9 +168,9 @@ __device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, i
                                          (__attribute__((address_space(3))) void *)(a_l + c * 1024),
                                          16, 0, 0);
     }
-    const int ks = K / 32, nsq = (kTile * ks + 255) / 256;
+    const int ks = K / 32, nsq = (rows * ks + 255) / 256;
     for (int c = w; c < nsq; c += kGThreads / 64) {
-        const int o = min(c * 256 + lane * 4, kTile * ks - 4);
+        const int o = min(c * 256 + lane * 4, rows * ks - 4);
         const int row = o / ks, col = o - row * ks;
         __builtin_amdgcn_global_load_lds((const void *)(srow(row) + col),
                                          (__attribute__((address_space(3))) void *)(as_l + c * 256),
@@ -175,19 +179,20 @@ __device__ __forceinline__ void g_dma_tile(ARow arow, SRow srow, int K, int w, i
 }
 
 // Bytes of the A image (rounded up to whole 1 KB pieces) and of the whole
-// LDS tile (scales padded to whole 256-byte pieces)
-__host__ __device__ constexpr size_t g_a_lds(int K) {
-    return ((size_t)kTile * (K + 16) + 1023) / 1024 * 1024;
+// LDS block (scales padded to whole 256-byte pieces)
+__host__ __device__ constexpr size_t g_a_lds(int rows, int K) {
+    return ((size_t)rows * (K + 16) + 1023) / 1024 * 1024;
 }
-__host__ __device__ constexpr size_t g_tile_lds(int K) {
-    return g_a_lds(K) + ((size_t)kTile * (K / 32) + 255) / 256 * 256;
+__host__ __device__ constexpr size_t g_tile_lds(int rows, int K) {
+    return g_a_lds(rows, K) + ((size_t)rows * (K / 32) + 255) / 256 * 256;
 }
 
-// One stage (steps [ks0, kend), at most kU) of a band times the two 16-slot A
-// fragments in LDS (row stride K bytes, scales as_l[slot][K/32]).
-// D[m][n]: slot 4*(lane/16)+v of fragment i, band row lane%16.
-template <bool EXACT>
-__device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const uint8_t *a_l,
+// Steps [ks0, kend) (at most kU) of a band, held in one stage, times the NF
+// 16-slot A fragments in LDS (row stride K + 16 bytes, scales
+// as_l[slot][K/32]). D[m][n]: slot 4*(lane/16)+v of fragment i, band row
+// lane%16.
+template <bool EXACT, int NF>
+__device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[NF], const uint8_t *a_l,
                                           const uint8_t *as_l, int K, int ks0, int kend,
                                           int lane) {
     const int r = lane & 15, g = lane >> 4;
@@ -200,7 +205,7 @@ __device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const 
             v8bf bq[4];
             cvt_fp4x32(st.w[u], e8m0_to_f32(sbyte), bq);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < NF; i++) {
                 const int slot = i * 16 + r;
                 const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 32;
                 v8bf aq[4];
@@ -211,7 +216,7 @@ __device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[2], const 
         } else {
             const v8i b = frag_from4(st.w[u]);
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
+            for (int i = 0; i < NF; i++) {
                 const int slot = i * 16 + r;
                 const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 16;
                 acc[i] = mfma_scaled<kFmtFp8, kFmtFp4>(
@@ -227,13 +232,25 @@ __device__ __forceinline__ int g_expert(const int32_t *tile_expert, int tile, in
     return e < 0 ? 0 : (e >= n_experts ? n_experts - 1 : e);
 }
 
+// The chunk stream of one wave over the units [u0, u1): chunk q is unit
+// u0 + q / nch, chunk q % nch, i.e. steps [k0 + 8c, min(k0 + 8c + 8, k1))
+// of the wave's K range [k0, k1) (empty past k1; nch is the same for every
+// wave of the workgroup, so all of them pass unit boundaries, and the
+// barriers there, together). Loads past the last chunk repeat it.
+struct ChunkStream {
+    int u0, total, nch, k0, k1;
+    __device__ __forceinline__ int unit(int q) const { return u0 + min(q, total - 1) / nch; }
+    __device__ __forceinline__ int cb(int q) const { return k0 + (min(q, total - 1) % nch) * kU; }
+    __device__ __forceinline__ int ce(int q) const { return min(cb(q) + kU, k1); }
+};
+
 // ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
-// Unit = (tile, 32 intermediate columns nt). Wave w: matrix (w>>1)&1 (w1|w3),
-// 16-row half w&1, K half w>>2 (each 8-step aligned, at most 16 steps: dim
-// <= 4096). The epilogue adds the K halves, applies SwiGLU x routing weight to
-// the 32 x 32 tile and quantises each slot's 32 values (one FP8 1x32 block) to
-// hq/hs.
-template <bool EXACT>
+// Unit = (A block, 32 intermediate columns nt). Wave w: matrix (w>>1)&1
+// (w1|w3), 16-row half w&1 of the 32 columns, K part w>>2 (k_part8 halves
+// rounded to 8-step stages). The K parts meet in LDS (gu), added in part
+// order; then a half-wave per slot row applies SwiGLU, the routing weight and
+// the FP8 1x32 quantisation (one block = the 32 columns of the unit).
+template <bool EXACT, int ROWS>
 __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     const uint8_t *xq, const uint8_t *xs, const int32_t *__restrict__ order,
     const float *__restrict__ layout_w, const int32_t *__restrict__ tile_expert,
@@ -241,117 +258,131 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     const uint8_t *__restrict__ s1, const uint8_t *__restrict__ w3,
     const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq, uint8_t *__restrict__ hs, int dim,
     int inter, int n_experts, int top_k, float limit) {
+    constexpr int NF = ROWS / 16, H = kTile / ROWS;
     extern __shared__ __align__(16) uint8_t g_lds[];
-    uint8_t *a_l = g_lds;                           // [32][dim + 16]
-    uint8_t *as_l = g_lds + g_a_lds(dim);            // [32][dim/32] (+ padding)
-    __shared__ float gu[2][2][kTile][kTile + 1];
-    __shared__ float rw_l[kTile];  // routing weight of each slot of the tile (0: padding)
-    __shared__ int pad_l[kTile];
+    uint8_t *a_l = g_lds;                              // [ROWS][dim + 16]
+    uint8_t *as_l = g_lds + g_a_lds(ROWS, dim);        // [ROWS][dim/32] (+ padding)
+    __shared__ float gu[2][2][ROWS][kGCols + 1];
+    __shared__ float rw_l[ROWS];  // routing weight of each slot of the block (0: padding)
+    __shared__ int pad_l[ROWS];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const uint64_t tab = ws_lane_exp2f_tab(lane);
     const int r = lane & 15, g = lane >> 4;
     const int mat = (w >> 1) & 1, half = w & 1, kpart = w >> 2;
-    int k0, k1;
-    k_part8(dim / 128, kpart, 2, k0, k1);
-    const int km = min(k0 + kU, k1);  // stage 0: [k0, km), stage 1: [km, k1)
-    const int NT = inter / 32;
-    const int units = *num_tiles * NT;
-    const int u0 = (int)((long)blockIdx.x * units / gridDim.x);
+    ChunkStream cs;
+    k_part8(dim / 128, kpart, 2, cs.k0, cs.k1);
+    cs.nch = ((dim / 128 + kU - 1) / kU + 1) / 2;  // chunks of the longer K part
+    const int NT = inter / kGCols;
+    const int units = *num_tiles * H * NT;
+    cs.u0 = (int)((long)blockIdx.x * units / gridDim.x);
     const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
-    if (u0 >= u1) return;  // whole workgroup
+    if (cs.u0 >= u1) return;  // whole workgroup
+    cs.total = (u1 - cs.u0) * cs.nch;
     const size_t wmat = (size_t)inter * (dim / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
     const uint8_t *wm = mat ? w3 : w1;
     const uint8_t *sm = mat ? s3 : s1;
     auto band_of = [&](int u) {
-        const int e = g_expert(tile_expert, u / NT, n_experts);
+        const int e = g_expert(tile_expert, u / (H * NT), n_experts);
         return fp4_band(wm + (size_t)e * wmat, sm + (size_t)e * smat, (u % NT) * 2 + half, dim,
                         lane);
     };
+    auto load_q = [&](Fp4Stage &st, int q) { fp4_load(st, band_of(cs.unit(q)), cs.cb(q), cs.ce(q)); };
     Fp4Stage st0, st1;
-    {
-        const Fp4Band b = band_of(u0);
-        fp4_load(st0, b, k0, km);
-        mem_order();
-        fp4_load(st1, b, km, k1);
-        mem_order();
-    }
-    int cur_tile = -1;
-    for (int u = u0; u < u1; u++) {
-        const int tile = u / NT, nt = u % NT;
-        const int slot0 = tile * kTile;
-        if (tile != cur_tile) {  // uniform: stage the tile's token rows in LDS
-            int my_tok = 0;
-            if (lane < kTile) {
-                const int route = order[slot0 + lane];
-                my_tok = route >= 0 ? route / top_k : 0;
-                if (w == 0) {
-                    pad_l[lane] = route < 0;
-                    rw_l[lane] = layout_w[slot0 + lane];
+    load_q(st0, 0);
+    mem_order();
+    load_q(st1, 1);
+    mem_order();
+    int cur_blk = -1;
+    v4f acc[NF];
+    auto step = [&](Fp4Stage &st, int q) {
+        const int u = cs.unit(q), c = q % cs.nch;
+        const int blk = u / NT, nt = u % NT;
+        const int slot0 = (blk / H) * kTile + (blk % H) * ROWS;
+        if (c == 0) {
+            if (blk != cur_blk) {  // uniform: stage the block's token rows in LDS
+                int my_tok = 0;
+                if (lane < ROWS) {
+                    const int route = order[slot0 + lane];
+                    my_tok = route >= 0 ? route / top_k : 0;
+                    if (w == 0) {
+                        pad_l[lane] = route < 0;
+                        rw_l[lane] = layout_w[slot0 + lane];
+                    }
                 }
+                g_dma_tile([&](int i) { return xq + (size_t)__shfl(my_tok, i, 64) * dim; },
+                           [&](int i) { return xs + (size_t)__shfl(my_tok, i, 64) * (dim / 32); },
+                           ROWS, dim, w, lane, a_l, as_l);
+                __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+                lds_barrier();
+                cur_blk = blk;
             }
-            g_dma_tile([&](int i) { return xq + (size_t)__shfl(my_tok, i, 64) * dim; },
-                       [&](int i) { return xs + (size_t)__shfl(my_tok, i, 64) * (dim / 32); },
-                       dim, w, lane, a_l, as_l);
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+#pragma unroll
+            for (int i = 0; i < NF; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        g_compute<EXACT, NF>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        load_q(st, q + 2);
+        if (c == cs.nch - 1) {  // the unit's K parts are complete: epilogue
+#pragma unroll
+            for (int i = 0; i < NF; i++)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    gu[kpart][mat][i * 16 + 4 * g + v][half * 16 + r] = acc[i][v];
             lds_barrier();
-            cur_tile = tile;
-        }
-        const Fp4Band bn = band_of(min(u + 1, u1 - 1));
-        v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        g_compute<EXACT>(st0, acc, a_l, as_l, dim, k0, km, lane);
-        fp4_load(st0, bn, k0, km);
-        g_compute<EXACT>(st1, acc, a_l, as_l, dim, km, k1, lane);
-        fp4_load(st1, bn, km, k1);
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-            for (int v = 0; v < 4; v++) gu[kpart][mat][i * 16 + 4 * g + v][half * 16 + r] = acc[i][v];
-        lds_barrier();
-        // a half-wave per slot row (32 values = one FP8 block)
-        const int col = t & 31;
-        for (int srow = t >> 5; srow < kTile; srow += kGThreads / 32) {
-            const int slot = slot0 + srow;
-            const bool pad = pad_l[srow] != 0;
-            float gv = gu[0][0][srow][col] + gu[1][0][srow][col];
-            float uv = gu[0][1][srow][col] + gu[1][1][srow][col];
-            if (limit > 0.0f) {
-                uv = rclamp(uv, -limit, limit);
-                gv = fminf(gv, limit);
+            // a half-wave per slot row (32 values = one FP8 block)
+            const int col = t & 31;
+            for (int srow = t >> 5; srow < ROWS; srow += kGThreads / 32) {
+                const int slot = slot0 + srow;
+                const bool pad = pad_l[srow] != 0;
+                float gv = gu[0][0][srow][col] + gu[1][0][srow][col];
+                float uv = gu[0][1][srow][col] + gu[1][1][srow][col];
+                if (limit > 0.0f) {
+                    uv = rclamp(uv, -limit, limit);
+                    gv = fminf(gv, limit);
+                }
+                // every lane evaluates silu (the lane-table exp permutes across the wave)
+                const float sg = ws_silu_lanes(gv, tab);
+                const float h = pad ? 0.0f : sg * uv * rw_l[srow];
+                uint32_t sbyte;
+                const uint32_t qb = quant_fp8_block32(h, &sbyte);
+                hq[(size_t)slot * inter + nt * kGCols + col] = (uint8_t)qb;
+                if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
             }
-            // every lane evaluates silu (the lane-table exp permutes across the wave)
-            const float sg = ws_silu_lanes(gv, tab);
-            const float h = pad ? 0.0f : sg * uv * rw_l[srow];
-            uint32_t sbyte;
-            const uint32_t q = quant_fp8_block32(h, &sbyte);
-            hq[(size_t)slot * inter + nt * kTile + col] = (uint8_t)q;
-            if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
+            lds_barrier();
         }
-        lds_barrier();
+    };
+    int q = 0;
+    for (; q + 1 < cs.total; q += 2) {
+        step(st0, q);
+        step(st1, q + 1);
     }
+    if (q < cs.total) step(st0, q);
 }
 
 // ---- grouped down ---------------------------------------------------------
 // Unit = (tile, 128 output columns nt); wave w owns columns nt*128 + 16w ..
-// over the whole K = inter (at most 16 steps: inter <= 2048), so each output
-// is one wave's sum and is written straight from registers. f32 out[slot,
-// dim].
+// over the whole K = inter (chunk stream of 8-step chunks), so each output is
+// one wave's sum and is written straight from registers. f32 out[slot, dim].
 template <bool EXACT>
 __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
     const int32_t *__restrict__ num_tiles, const uint8_t *__restrict__ w2,
     const uint8_t *__restrict__ s2, float *__restrict__ out, int dim, int inter, int n_experts) {
     extern __shared__ __align__(16) uint8_t g_lds[];
-    uint8_t *a_l = g_lds;                             // [32][inter + 16]
-    uint8_t *as_l = g_lds + g_a_lds(inter);          // [32][inter/32] (+ padding)
+    uint8_t *a_l = g_lds;                                // [32][inter + 16]
+    uint8_t *as_l = g_lds + g_a_lds(kTile, inter);      // [32][inter/32] (+ padding)
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int k1 = inter / 128, km = min(kU, k1);
+    ChunkStream cs;
+    cs.k0 = 0;
+    cs.k1 = inter / 128;
+    cs.nch = (cs.k1 + kU - 1) / kU;
     const int NT = dim / 128;
     const int units = *num_tiles * NT;
-    const int u0 = (int)((long)blockIdx.x * units / gridDim.x);
+    cs.u0 = (int)((long)blockIdx.x * units / gridDim.x);
     const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
-    if (u0 >= u1) return;  // whole workgroup
+    if (cs.u0 >= u1) return;  // whole workgroup
+    cs.total = (u1 - cs.u0) * cs.nch;
     const size_t wmat = (size_t)dim * (inter / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
     auto band_of = [&](int u) {
@@ -359,40 +390,47 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
         return fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, (u % NT) * 8 + w, inter,
                         lane);
     };
+    auto load_q = [&](Fp4Stage &st, int q) { fp4_load(st, band_of(cs.unit(q)), cs.cb(q), cs.ce(q)); };
     Fp4Stage s0, s1;
-    {
-        const Fp4Band b = band_of(u0);
-        fp4_load(s0, b, 0, km);
-        mem_order();
-        fp4_load(s1, b, km, k1);
-        mem_order();
-    }
+    load_q(s0, 0);
+    mem_order();
+    load_q(s1, 1);
+    mem_order();
     int cur_tile = -1;
-    for (int u = u0; u < u1; u++) {
+    v4f acc[2];
+    auto step = [&](Fp4Stage &st, int q) {
+        const int u = cs.unit(q), c = q % cs.nch;
         const int tile = u / NT, nt = u % NT;
         const int slot0 = tile * kTile;
-        if (tile != cur_tile) {  // uniform: stage the tile's hq rows in LDS
-            lds_barrier();       // every wave is done with the previous tile
-            g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
-                       [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); }, inter, w,
-                       lane, a_l, as_l);
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
-            lds_barrier();
-            cur_tile = tile;
+        if (c == 0) {
+            if (tile != cur_tile) {  // uniform: stage the tile's hq rows in LDS
+                lds_barrier();       // every wave is done with the previous tile
+                g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
+                           [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); }, kTile,
+                           inter, w, lane, a_l, as_l);
+                __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+                lds_barrier();
+                cur_tile = tile;
+            }
+            acc[0] = acc[1] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        const Fp4Band bn = band_of(min(u + 1, u1 - 1));
-        v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        g_compute<EXACT>(s0, acc, a_l, as_l, inter, 0, km, lane);
-        fp4_load(s0, bn, 0, km);
-        g_compute<EXACT>(s1, acc, a_l, as_l, inter, km, k1, lane);
-        fp4_load(s1, bn, km, k1);
-        const int col = nt * 128 + w * 16 + r;
+        g_compute<EXACT, 2>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        load_q(st, q + 2);
+        if (c == cs.nch - 1) {
+            const int col = nt * 128 + w * 16 + r;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int v = 0; v < 4; v++)
-                out[(size_t)(slot0 + i * 16 + 4 * g + v) * dim + col] = acc[i][v];
+                for (int v = 0; v < 4; v++)
+                    out[(size_t)(slot0 + i * 16 + 4 * g + v) * dim + col] = acc[i][v];
+        }
+    };
+    int q = 0;
+    for (; q + 1 < cs.total; q += 2) {
+        step(s0, q);
+        step(s1, q + 1);
     }
+    if (q < cs.total) step(s0, q);
 }
 
 // ---- combine: y[row] = sum of its routes' outputs in ascending slot order --
@@ -472,17 +510,24 @@ int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t
         return WS_ERR_SHAPE;
     if (!al16(xq) || !al16(w1) || !al16(w3) || !al4(xs) || !al8(s1) || !al8(s3))
         return WS_ERR_INVALID_ARG;
-    if (dim > 4096) return WS_ERR_SHAPE;  // the A tile (32 x dim bytes) lives in LDS
-    const size_t lds = g_tile_lds((int)dim);
+    // the A block (ROWS x dim bytes) lives in LDS: 32 rows up to dim 4096,
+    // 16-row halves of each tile up to 8192
+    if (dim > 8192) return WS_ERR_SHAPE;
     dim3 grid((unsigned)cu_count());
-    if (math_mode() == WS_MATH_EXACT)
-        hipLaunchKernelGGL(grouped_glu_quant_kernel<true>, grid, dim3(kGThreads), lds, stream, xq, xs, order,
-                           layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs, (int)dim,
-                           (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
-    else
-        hipLaunchKernelGGL(grouped_glu_quant_kernel<false>, grid, dim3(kGThreads), lds, stream, xq, xs,
-                           order, layout_w, tile_expert, num_tiles, w1, s1, w3, s3, hq, hs,
-                           (int)dim, (int)inter, (int)n_experts, (int)top_k, swiglu_limit);
+#define WS_GLU(E, R)                                                                          \
+    hipLaunchKernelGGL((grouped_glu_quant_kernel<E, R>), grid, dim3(kGThreads),              \
+                       g_tile_lds(R, (int)dim), stream, xq, xs, order, layout_w, tile_expert,  \
+                       num_tiles, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,              \
+                       (int)n_experts, (int)top_k, swiglu_limit)
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    if (dim <= 4096) {
+        if (exact) WS_GLU(true, 32);
+        else WS_GLU(false, 32);
+    } else {
+        if (exact) WS_GLU(true, 16);
+        else WS_GLU(false, 16);
+    }
+#undef WS_GLU
     return launch_status();
 }
 
@@ -494,8 +539,8 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
     if (dim <= 0 || inter <= 0 || n_experts <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
     if (dim % 128 || inter % 128 || tiles > 65535) return WS_ERR_SHAPE;
     if (!al16(hq) || !al16(w2) || !al4(hs) || !al8(s2)) return WS_ERR_INVALID_ARG;
-    if (inter > 2048) return WS_ERR_SHAPE;  // one wave's K range fits two 8-step stages
-    const size_t lds = g_tile_lds((int)inter);
+    if (inter > 4096) return WS_ERR_SHAPE;  // the 32 x inter hq tile lives in LDS
+    const size_t lds = g_tile_lds(kTile, (int)inter);
     dim3 grid((unsigned)cu_count());
     if (math_mode() == WS_MATH_EXACT)
         hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(kGThreads), lds, stream, hq, hs,
@@ -537,6 +582,8 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
     if (!x || !topk_idx || !topk_w || !y || !workspace) return WS_ERR_INVALID_ARG;
     if (rows <= 0 || dim <= 0 || inter <= 0 || n_experts <= 0 || top_k <= 0)
         return WS_ERR_INVALID_ARG;
+    // every stage's shape limit, checked before the first launch
+    if (dim % 128 || inter % 128 || dim > 8192 || inter > 4096) return WS_ERR_SHAPE;
     if (workspace_bytes < ws_moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts) ||
         !al16(workspace))
         return WS_ERR_INVALID_ARG;
