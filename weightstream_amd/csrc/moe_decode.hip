@@ -314,28 +314,29 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     const int nblk = dim / 32;
     const int tb0 = w * nblk / kGluStreamWaves, tb1 = (w + 1) * nblk / kGluStreamWaves;
     const int tc0 = tb0 * 32, tc1 = tb1 * 32;
+    // the routing inputs first (the weight loads wait for the routing), then
+    // the token share
+    RouteIn<(CPL > 0 ? CPL : 1)> rin;
+    if constexpr (CPL > 0) route_load<CPL>(rin, ra.logits, ra.bias, n_experts, lane);
+    mem_order();
     TokenRegs tr;
     if (XF32) tok_load_f32(tr, xf, tb0, tb1, lane);
     else share_load_fp8(tr.b, xq, xs, tc0, tc1, lane);
     mem_order();
 
-    // the slot's expert and routing weight, and the picks' ranks
+    // the slot's expert: with the routing in the kernel, the top-k rounds
+    // up to this slot's run before the weight loads go out and the rest
+    // while they are in flight (the same rounds in the same order)
     int e;
     float rw;
     WavePicks wp;
+    WaveTopk<(CPL > 0 ? CPL : 1)> tk;
     if constexpr (CPL > 0) {
         float sc[CPL];
-        wave_scores<CPL>(ra.logits, n_experts, ra.score_func, ra.gate_temp, lane, sc);
-        int pk;
-        float pw;
-        wave_select<CPL>(sc, ra.bias, n_experts, top_k, ra.norm, ra.route_scale, lane, pk, pw);
-        e = __builtin_amdgcn_readlane(pk, slot);
-        rw = readlane_f(pw, slot);
-        wp = wave_picks_of(pk, top_k, n_experts, lane);
-        if (blockIdx.x == 0 && slot == 0 && w == 0 && lane < top_k) {
-            ra.idx_out[lane] = pk;
-            ra.w_out[lane] = pw;
-        }
+        wave_scores_of<CPL>(rin.v, ra.score_func, ra.gate_temp, lane, sc);
+        tk.init(sc, rin.b, n_experts, lane);
+        e = 0;
+        for (int k = 0; k <= slot; k++) e = tk.round(k, lane);
     } else {
         e = idx[slot];
         rw = topk_w[slot];
@@ -355,6 +356,19 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     mem_order();
     fp4_load(st1, band, k0 + kU, k1);
     mem_order();
+
+    // the routing weight and the picks' ranks
+    if constexpr (CPL > 0) {
+        for (int k = slot + 1; k < top_k; k++) tk.round(k, lane);
+        const int pk = tk.pick;
+        const float pw = tk.weight(top_k, ra.norm, ra.route_scale);
+        rw = readlane_f(pw, slot);
+        wp = wave_picks_of(pk, top_k, n_experts, lane);
+        if (blockIdx.x == 0 && slot == 0 && w == 0 && lane < top_k) {
+            ra.idx_out[lane] = pk;
+            ra.w_out[lane] = pw;
+        }
+    }
 
     if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
     else share_store_fp8<EXACT>(tr.b, tc0, tc1, lane, x_l, xq_l, xs_l);

@@ -60,15 +60,31 @@ __device__ __forceinline__ float readlane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// Scores of experts lane + 64 c (c < CPL) from logits lg[E]: sigmoid,
+// The routing inputs of experts lane + 64 c (c < CPL): logits and bias,
+// loaded together so that their latencies overlap.
+template <int CPL>
+struct RouteIn {
+    float v[CPL], b[CPL];
+};
+
+template <int CPL>
+__device__ __forceinline__ void route_load(RouteIn<CPL> &in, const float *lg, const float *bias,
+                                           int n_experts, int lane) {
+#pragma unroll
+    for (int c = 0; c < CPL; c++) in.v[c] = lg[min(lane + 64 * c, n_experts - 1)];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) in.b[c] = bias[min(lane + 64 * c, n_experts - 1)];
+}
+
+// Scores of experts lane + 64 c (c < CPL) from their logits: sigmoid,
 // sqrtsoftplus or identity (softmax needs the whole row; not handled here),
 // after dividing by gate_temp. The exp table sits in lane registers.
 template <int CPL>
-__device__ __forceinline__ void wave_scores(const float *lg, int n_experts, int score_func,
-                                            float gate_temp, int lane, float sc[CPL]) {
+__device__ __forceinline__ void wave_scores_of(const float lg[CPL], int score_func,
+                                               float gate_temp, int lane, float sc[CPL]) {
     float v[CPL];
 #pragma unroll
-    for (int c = 0; c < CPL; c++) v[c] = lg[min(lane + 64 * c, n_experts - 1)];
+    for (int c = 0; c < CPL; c++) v[c] = lg[c];
     const uint64_t tab = ws_lane_exp2f_tab(lane);
     if (gate_temp != 1.0f) {
 #pragma unroll
@@ -89,6 +105,16 @@ __device__ __forceinline__ void wave_scores(const float *lg, int n_experts, int 
     }
 }
 
+// ... from logits lg[E]
+template <int CPL>
+__device__ __forceinline__ void wave_scores(const float *lg, int n_experts, int score_func,
+                                            float gate_temp, int lane, float sc[CPL]) {
+    float v[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) v[c] = lg[min(lane + 64 * c, n_experts - 1)];
+    wave_scores_of<CPL>(v, score_func, gate_temp, lane, sc);
+}
+
 // Top-k of score + bias (f32 total order, ties to the lower index) over
 // experts lane + 64 c; lane k < top_k gets pick k and its weight: the score,
 // normalised by the top-k-order sum + 1e-20 (norm 1: moe.rs:61, only when
@@ -97,32 +123,45 @@ __device__ __forceinline__ void wave_scores(const float *lg, int n_experts, int 
 // the complemented index); a round is a lane-local max, a 32-bit DPP wave max
 // of the score halves and a ballot; only an exact score tie across lanes
 // takes the 64-bit wave max.
+// bv[c]: the bias of expert lane + 64 c.
 template <int CPL>
-__device__ __forceinline__ void wave_select(const float sc[CPL], const float *bias, int n_experts,
-                                            int top_k, int norm, float route_scale, int lane,
-                                            int &my_pick, float &my_w) {
-    float bv[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; c++) bv[c] = bias[min(lane + 64 * c, n_experts - 1)];
+struct WaveTopk {
     uint64_t cand[CPL];
+    float sc[CPL];
+    int pick;  // lane k: pick k, once round k has run
+    float ws;  // lane k: its score
+
+    __device__ __forceinline__ void init(const float s[CPL], const float bv[CPL], int n_experts,
+                                         int lane) {
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const int e = lane + 64 * c;
-        cand[c] = e < n_experts
-                      ? ((uint64_t)total_key_u(sc[c] + bv[c]) << 32) | (uint32_t)(~(uint32_t)e)
-                      : 0ull;
+        for (int c = 0; c < CPL; c++) {
+            const int e = lane + 64 * c;
+            cand[c] = e < n_experts
+                          ? ((uint64_t)total_key_u(s[c] + bv[c]) << 32) | (uint32_t)(~(uint32_t)e)
+                          : 0ull;
+            sc[c] = s[c];
+        }
+        pick = 0;
+        ws = 0.0f;
     }
-    my_pick = 0;
-    float ws = 0.0f;
-    for (int k = 0; k < top_k; k++) {
+
+    // round k: the largest remaining key; returns its expert id (uniform)
+    __device__ __forceinline__ int round(int k, int lane) {
+        // the lane's largest key and its score (keys are distinct: the low
+        // half is the complemented expert id), no indexing by position
+        // (the asm keeps each score a register value: a select between
+        // array elements would otherwise become an indexed load of a
+        // private-memory copy of the array)
         uint64_t best = cand[0];
-        int bc = 0;
+        float sb = sc[0];
 #pragma unroll
-        for (int c = 1; c < CPL; c++)
-            if (cand[c] > best) {
-                best = cand[c];
-                bc = c;
-            }
+        for (int c = 1; c < CPL; c++) {
+            float v = sc[c];
+            __asm__("" : "+v"(v));
+            const bool gt = cand[c] > best;
+            best = gt ? cand[c] : best;
+            sb = gt ? v : sb;
+        }
         const uint32_t hk = (uint32_t)(best >> 32);
         const uint32_t wk = wave_max_u32(hk);
         uint64_t bal = __ballot(hk == wk);
@@ -132,26 +171,49 @@ __device__ __forceinline__ void wave_select(const float sc[CPL], const float *bi
             bal = __ballot(hk == wk && best == full);
         }
         const int win = __ffsll((long long)bal) - 1;
-        float sb = sc[0];
-#pragma unroll
-        for (int c = 1; c < CPL; c++) sb = c == bc ? sc[c] : sb;
-        const int e = __builtin_amdgcn_readlane(lane + 64 * bc, win);
+        const int e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)best, win);
         const float w = readlane_f(sb, win);
         if (lane == k) {
-            my_pick = e;
+            pick = e;
             ws = w;
         }
 #pragma unroll
-        for (int c = 0; c < CPL; c++)
-            if (lane == win && c == bc) cand[c] = 0ull;
+        for (int c = 0; c < CPL; c++) cand[c] = (lane == win && cand[c] == best) ? 0ull : cand[c];
+        return e;
     }
-    float wout = ws;
-    if ((norm == 1 && top_k > 1) || norm == 2) {
-        float s = -0.0f;
-        for (int k = 0; k < top_k; k++) s = s + readlane_f(ws, k);
-        wout = ws / (s + 1e-20f);
+
+    // lane k's weight after all top_k rounds
+    __device__ __forceinline__ float weight(int top_k, int norm, float route_scale) const {
+        float wout = ws;
+        if ((norm == 1 && top_k > 1) || norm == 2) {
+            float s = -0.0f;
+            for (int k = 0; k < top_k; k++) s = s + readlane_f(ws, k);
+            wout = ws / (s + 1e-20f);
+        }
+        return wout * route_scale;
     }
-    my_w = wout * route_scale;
+};
+
+template <int CPL>
+__device__ __forceinline__ void wave_select_of(const float sc[CPL], const float bv[CPL],
+                                               int n_experts, int top_k, int norm,
+                                               float route_scale, int lane, int &my_pick,
+                                               float &my_w) {
+    WaveTopk<CPL> tk;
+    tk.init(sc, bv, n_experts, lane);
+    for (int k = 0; k < top_k; k++) tk.round(k, lane);
+    my_pick = tk.pick;
+    my_w = tk.weight(top_k, norm, route_scale);
+}
+
+template <int CPL>
+__device__ __forceinline__ void wave_select(const float sc[CPL], const float *bias, int n_experts,
+                                            int top_k, int norm, float route_scale, int lane,
+                                            int &my_pick, float &my_w) {
+    float bv[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) bv[c] = bias[min(lane + 64 * c, n_experts - 1)];
+    wave_select_of<CPL>(sc, bv, n_experts, top_k, norm, route_scale, lane, my_pick, my_w);
 }
 
 }  // namespace ws
