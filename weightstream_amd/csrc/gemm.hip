@@ -525,6 +525,269 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     return launch_status();
 }
 
+// ---- A-resident GEMM: a 32-row block of A in LDS, K split over 8 waves ----
+// For M of a few hundred with K <= 4096 (M = 128: the projection shapes). A
+// workgroup owns 32 rows x 16*NF columns and the whole K. Its 32 rows of A
+// (one contiguous block of M x K row-major e4m3) and their scales are copied
+// once into LDS by direct global->LDS loads (rows padded to K + 16 bytes, so
+// the 16 rows one read touches fall on distinct banks); the weight rows are
+// streamed into registers in double-buffered stages (each weight byte is read
+// once). Wave w multiplies K part w of the tile; the 8 partial tiles meet in
+// LDS (reusing the A image) and are added in wave order (deterministic).
+// Every A element is converted once per workgroup, and nothing is re-read
+// from HBM: A is 0.5 MB, the weights cross HBM once.
+constexpr int kAlRows = 32, kAlWaves = 8;
+
+__host__ __device__ constexpr size_t al_a_bytes(int K) {
+    return ((size_t)kAlRows * (K + 16) + 1023) / 1024 * 1024;
+}
+// scales of the 32 rows: K / 32 bytes per row in both scale modes (K/32
+// UE8M0 bytes, or K/128 f32), padded to whole 1 KB pieces
+__host__ __device__ constexpr size_t al_s_bytes(int K) {
+    return ((size_t)kAlRows * (K / 32) + 1023) / 1024 * 1024;
+}
+
+template <int NF>
+struct AlStage {
+    uint4 b[NF][2];
+    uint32_t sb[NF];
+    float sbf;
+};
+
+template <int NF, int SMODE, int OMODE, bool EXACT>
+__global__ __launch_bounds__(64 * kAlWaves) void gemm_al_kernel(const uint8_t *A, const void *SA,
+                                                                const uint8_t *B, const void *SB,
+                                                                void *__restrict__ C, int M, int N,
+                                                                int K) {
+    constexpr int kCols = 16 * NF;
+    extern __shared__ __align__(16) uint8_t al_lds[];
+    uint8_t *a_l = al_lds;
+    uint8_t *s_l = al_lds + al_a_bytes(K);
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * kCols, mb = blockIdx.y * kAlRows;
+    const int ksteps = K / 128, kbn = K / 32, kb128 = K / 128;
+    const int k0 = w * ksteps / kAlWaves, k1 = (w + 1) * ksteps / kAlWaves;
+    const int pitch = K + 16;
+
+    // 1. the A block and its scales into LDS (rows past M repeat row M-1;
+    // a piece that would cross the image's end repeats its last 16 bytes).
+    // Every workgroup of a row block copies the same bytes at the same time:
+    // each starts at its own piece, so that they do not all queue on the
+    // same L2 channel.
+    {
+        const int total = kAlRows * pitch, nq = (total + 1023) / 1024;
+        const int rot = (int)((blockIdx.x * 41u) % (unsigned)nq);
+        for (int c0 = w; c0 < nq; c0 += kAlWaves) {
+            const int c = c0 + rot < nq ? c0 + rot : c0 + rot - nq;
+            const int o = min(c * 1024 + lane * 16, total - 16);
+            const int row = o / pitch, col = min(o - row * pitch, K - 16);
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(A + (size_t)min(mb + row, M - 1) * K + col),
+                (__attribute__((address_space(3))) void *)(a_l + c * 1024), 16, 0, 0);
+        }
+        const int stot = kAlRows * kbn, nsq = (stot + 1023) / 1024;
+        const int srot = (int)(blockIdx.x % (unsigned)nsq);
+        for (int c0 = w; c0 < nsq; c0 += kAlWaves) {
+            const int c = c0 + srot < nsq ? c0 + srot : c0 + srot - nsq;
+            const int o = min(c * 1024 + lane * 16, stot - 16);
+            const int row = o / kbn, col = o - row * kbn;
+            __builtin_amdgcn_global_load_lds(
+                (const void *)((const uint8_t *)SA + (size_t)min(mb + row, M - 1) * kbn + col),
+                (__attribute__((address_space(3))) void *)(s_l + c * 1024), 16, 0, 0);
+        }
+    }
+    // the A copies are older than every weight load below: loads complete in
+    // issue order, so waiting for "all but the weight loads" waits for them
+    mem_order();
+
+    // 2. the wave's weight rows: 16 B at K offset 32g (+16) (exact) or 16g
+    // (+64) (native) of each 128-K step
+    const uint8_t *brow[NF];
+    const uint8_t *sbrow[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const int col = n0 + 16 * j + r;
+        brow[j] = B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
+        sbrow[j] = (const uint8_t *)SB + (size_t)(col / 32) * kbn;
+    }
+    const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
+    auto load = [&](AlStage<NF> &st, int ks0) {
+        const int ks = max(min(ks0, k1 - 1), 0);
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            const uint8_t *p = brow[j] + (size_t)ks * 128;
+            st.b[j][0] = ldg16_stream(p);
+            st.b[j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+            if (SMODE == kUe8m0) st.sb[j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
+        }
+        if (SMODE == kF32s) st.sbf = sbf_row[ks];
+    };
+    constexpr int kStageLoads = 2 * NF + (SMODE == kUe8m0 ? NF : 1);
+
+    v4f acc[2][NF];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < NF; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t a_base = lds_addr(a_l), s_base = lds_addr(s_l);
+    auto compute = [&](const AlStage<NF> &st, int ks) {
+        if (ks >= k1) return;  // uniform
+        // the wave's two A fragments of this step, and their scales
+        u32x4v alo[2], ahi[2];
+        uint32_t saw[2];
+        float saf[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int rl = 16 * i + r;
+            const uint32_t ap = a_base + rl * pitch + ks * 128 + (EXACT ? g * 32 : g * 16);
+            alo[i] = lds_read_b128(ap);
+            ahi[i] = lds_read_b128(ap + (EXACT ? 16 : 64));
+            if (SMODE == kUe8m0) {
+                saw[i] = lds_read_b32(s_base + rl * kbn + ks * 4);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    saf[i][v] = __uint_as_float(
+                        lds_read_b32(s_base + ((16 * i + 4 * g + v) * kb128 + ks) * 4));
+            }
+        }
+        lds_wait_all();
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            lds_ready(alo[i]);
+            lds_ready(ahi[i]);
+            if (SMODE == kUe8m0) lds_ready(saw[i]);
+            else {
+#pragma unroll
+                for (int v = 0; v < 4; v++) lds_ready(saf[i][v]);
+            }
+        }
+        if (EXACT) {
+            v8bf bq[NF][4];
+#pragma unroll
+            for (int j = 0; j < NF; j++)
+                cvt_fp8x32(st.b[j][0], st.b[j][1],
+                           SMODE == kUe8m0 ? e8m0_to_f32(st.sb[j] & 0xFF) : 1.0f, bq[j]);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                v8bf aq[4];
+                cvt_fp8x32(uint4{alo[i][0], alo[i][1], alo[i][2], alo[i][3]},
+                           uint4{ahi[i][0], ahi[i][1], ahi[i][2], ahi[i][3]},
+                           SMODE == kUe8m0 ? e8m0_to_f32((saw[i] >> (8 * g)) & 0xFF) : 1.0f, aq);
+#pragma unroll
+                for (int j = 0; j < NF; j++) {
+                    if (SMODE == kUe8m0) {
+                        acc[i][j] = mfma_bf16_k128(aq, bq[j], acc[i][j]);
+                    } else {
+                        const v4f p = mfma_bf16_k128(aq, bq[j], v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            acc[i][j][v] = acc[i][j][v] + p[v] * (saf[i][v] * st.sbf);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const v8i a = frag_from(uint4{alo[i][0], alo[i][1], alo[i][2], alo[i][3]},
+                                        uint4{ahi[i][0], ahi[i][1], ahi[i][2], ahi[i][3]});
+#pragma unroll
+                for (int j = 0; j < NF; j++) {
+                    const v8i b = frag_from(st.b[j][0], st.b[j][1]);
+                    if (SMODE == kUe8m0) {
+                        acc[i][j] = mfma_scaled<kFmtFp8, kFmtFp8>(
+                            a, b, acc[i][j], (int)((saw[i] >> (8 * g)) & 0xFF),
+                            (int)(st.sb[j] & 0xFF));
+                    } else {
+                        const v4f p = mfma_scaled<kFmtFp8, kFmtFp8>(
+                            a, b, v4f{0.f, 0.f, 0.f, 0.f}, kScaleOne, kScaleOne);
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            acc[i][j][v] = acc[i][j][v] + p[v] * (saf[i][v] * st.sbf);
+                    }
+                }
+            }
+        }
+    };
+
+    AlStage<NF> s0, s1;
+    load(s0, k0);
+    mem_order();
+    load(s1, k0 + 1);
+    mem_order();
+    wait_vm<2 * kStageLoads>();  // this wave's A / scale copies have landed
+    raw_barrier();               // ... and every wave's
+
+    const int nst = k1 - k0;
+    int i = 0, ks = k0;
+    for (; i + 3 < nst; i += 2, ks += 2) {
+        compute(s0, ks);
+        load(s0, ks + 2);
+        compute(s1, ks + 1);
+        load(s1, ks + 3);
+    }
+    const int rest = nst - i;
+    if (rest == 3) {
+        compute(s0, ks);
+        load(s0, ks + 2);
+        compute(s1, ks + 1);
+        compute(s0, ks + 2);
+    } else {
+        if (rest >= 1) compute(s0, ks);
+        if (rest == 2) compute(s1, ks + 1);
+    }
+
+    // the K parts meet in LDS (the A image is no longer read), in wave order
+    __syncthreads();
+    float *part = (float *)al_lds;  // [8][32][kCols]
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                part[(w * kAlRows + 16 * f + 4 * g + v) * kCols + 16 * j + r] = acc[f][j][v];
+    __syncthreads();
+    for (int o = t; o < kAlRows * kCols; o += 64 * kAlWaves) {
+        const int rl = o / kCols, c = o % kCols;
+        const int row = mb + rl;
+        if (row >= M) continue;
+        float sum = part[rl * kCols + c];
+#pragma unroll
+        for (int q = 1; q < kAlWaves; q++) sum = sum + part[(q * kAlRows + rl) * kCols + c];
+        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + n0 + c] = sum;
+        else ((uint16_t *)C)[(size_t)row * N + n0 + c] = f32_to_bf16(sum);
+    }
+}
+
+template <int NF, int SMODE, int OMODE>
+static int launch_al(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
+                     int m, int n, int k, hipStream_t stream) {
+    if (n % (16 * NF) || k % 512 || k > 4096) return -1;
+    const size_t lds = al_a_bytes(k) + al_s_bytes(k);
+    if ((size_t)kAlWaves * kAlRows * 16 * NF * 4 > lds) return -1;  // the partials reuse it
+    dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + kAlRows - 1) / kAlRows));
+    const bool exact = math_mode() != WS_MATH_NATIVE;
+    const void *fn = exact ? (const void *)gemm_al_kernel<NF, SMODE, OMODE, true>
+                           : (const void *)gemm_al_kernel<NF, SMODE, OMODE, false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[exact]) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
+            hipSuccess)
+            return -1;
+        attr_set[exact] = true;
+    }
+    if (exact)
+        hipLaunchKernelGGL((gemm_al_kernel<NF, SMODE, OMODE, true>), grid, dim3(64 * kAlWaves), lds,
+                           stream, a, sa, b, sb, out, m, n, k);
+    else
+        hipLaunchKernelGGL((gemm_al_kernel<NF, SMODE, OMODE, false>), grid, dim3(64 * kAlWaves), lds,
+                           stream, a, sa, b, sb, out, m, n, k);
+    return launch_status();
+}
+
 // ---- pipelined split-K GEMM (A and W streamed through an LDS ring) -------
 // A workgroup (4 waves, 2 x 2 over the tile) owns a 128 x BN output tile and
 // a range of at most kPMaxSteps 128-K steps. Every step's A block (128 x 128
@@ -962,15 +1225,19 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         int rc = -1;
         // 1. 32-column strips when they give the chip one round of workgroups:
         // 64-row blocks (M=128, N=4096) or 32-row blocks (M=128, N=2048;
-        // M=64, N=4096). Measured at K=4096: 16.4 and 11.3 us against 19.7
-        // and 15.7 for the split-K kernel.
+        // M=64, N=4096). Measured at K=4096: 16.4 us (kp) and 10.0 us (A in
+        // LDS; kp 11.3) against 19.7 and 15.7 for the split-K kernel.
         if (M > 16 && N % 32 == 0) {
             const long cus = cu_count();
             const long wg64 = (long)(N / 32) * ((M + 63) / 64), wg32 = (long)(N / 32) * ((M + 31) / 32);
-            if (wg64 * 4 >= cus * 3 && wg64 * 2 <= cus * 3)
+            if (wg64 * 4 >= cus * 3 && wg64 * 2 <= cus * 3) {
                 rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-            else if (wg32 * 4 >= cus * 3 && wg32 * 2 <= cus * 3)
-                rc = launch_kp<2, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+            } else if (wg32 * 4 >= cus * 3 && wg32 * 2 <= cus * 3) {
+                // 32-row blocks: the A-resident kernel (K <= 4096), else kp
+                if (!BFP4) rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
+                if (rc < 0)
+                    rc = launch_kp<2, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+            }
         }
         if (rc >= 0) return rc;
         // 2. M > 64: the pipelined split-K kernel (128-row tiles)
