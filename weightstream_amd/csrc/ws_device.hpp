@@ -116,6 +116,11 @@ __device__ __forceinline__ uint32_t lds_read_b32(uint32_t a) {
     __asm__ volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(a));
     return v;
 }
+// LDS store the compiler does not see (so it adds no wait for outstanding
+// direct global->LDS loads); ordered by the caller with lds_wait_all().
+__device__ __forceinline__ void lds_write_b32(uint32_t a, uint32_t v) {
+    __asm__ volatile("ds_write_b32 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
 __device__ __forceinline__ void lds_wait_all() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Wait until at most N of this wave's LDS reads (lds_read_*) are in flight;
 // LDS reads complete in issue order.
