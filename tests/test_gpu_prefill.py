@@ -221,3 +221,42 @@ def test_moe_prefill_rejects_oversized_shapes():
         w = torch.zeros((4, k), dtype=torch.float32, device=DEV)
         with pytest.raises(RuntimeError, match="unsupported shape"):
             L.moe_prefill(f, idx, w, b, b, b, b, b, b, f, 4, dim, inter, E, k, ws)
+
+
+@pytest.mark.parametrize("m,E,dim,inter,k", [(40, 64, 1024, 512, 6), (9, 16, 512, 256, 4)])
+def test_prefill_stages_compose_to_moe_prefill(m, E, dim, inter, k):
+    """emit8 -> dispatch -> grouped gate/up -> grouped down (every slot) ->
+    combine through the public entry points gives the bits of ws_moe_prefill
+    (which multiplies and writes only the slots that hold routes)."""
+    rng = np.random.default_rng(990 + m)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(990 + m)
+    P = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
+    logits, bias = zipf_routing(rng, m, E, k)
+    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), None, idx, w, m, E, k, O.SCORE_SIGMOID, 1.0, True, 1.0)
+    x = dev(rng.standard_normal((m, dim)).astype(np.float32))
+    announce("prefill stages m=%d E=%d dim=%d inter=%d k=%d" % (m, E, dim, inter, k))
+    ws = torch.empty(L.moe_prefill_workspace_size(m, dim, inter, k, E), dtype=torch.uint8,
+                     device=DEV)
+    y1 = torch.empty((m, dim), dtype=torch.float32, device=DEV)
+    L.moe_prefill(x, idx, w, *P, y1, m, dim, inter, E, k, ws)
+
+    routes, tiles = m * k, L.moe_tiles(m * k, E)
+    xq = torch.empty((m, dim), dtype=torch.uint8, device=DEV)
+    xs = torch.empty((m, dim // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, xq, xs, m * dim)
+    i32 = lambda n: torch.empty(n, dtype=torch.int32, device=DEV)
+    order, rp, te, nt = i32(tiles * 32), i32(routes), i32(tiles), i32(1)
+    lw = torch.empty(tiles * 32, dtype=torch.float32, device=DEV)
+    L.moe_dispatch_tl(idx, w, order, lw, rp, te, i32(E), i32(E), i32(E), nt, m, k, tiles, E)
+    hq = torch.empty((tiles * 32, inter), dtype=torch.uint8, device=DEV)
+    hs = torch.empty((tiles * 32, inter // 32), dtype=torch.uint8, device=DEV)
+    L.moe_grouped_glu_quant(xq, xs, order, lw, te, nt, P[0], P[1], P[2], P[3], hq, hs, dim,
+                            inter, E, k, tiles, 10.0)
+    down = torch.empty((tiles * 32, dim), dtype=torch.float32, device=DEV)
+    L.moe_grouped_down(hq, hs, te, nt, P[4], P[5], down, dim, inter, E, tiles)
+    y2 = torch.empty((m, dim), dtype=torch.float32, device=DEV)
+    L.moe_combine_f32(down, rp, y2, dim, k, m, tiles)
+    assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))

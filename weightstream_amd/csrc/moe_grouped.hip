@@ -294,6 +294,7 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     load_q(st1, 1);
     mem_order();
     int cur_blk = -1;
+    bool low_only = false;  // the block's slots 16.. are all padding (a 32-row block)
     v4f acc[NF];
     auto step = [&](Fp4Stage &st, int q) {
         const int u = cs.unit(q), c = q % cs.nch;
@@ -302,17 +303,21 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
         if (c == 0) {
             if (blk != cur_blk) {  // uniform: stage the block's token rows in LDS
                 int my_tok = 0;
+                bool padded = true;
                 if (lane < ROWS) {
                     const int route = order[slot0 + lane];
                     my_tok = route >= 0 ? route / top_k : 0;
+                    padded = route < 0;
                     if (w == 0) {
                         pad_l[lane] = route < 0;
                         rw_l[lane] = layout_w[slot0 + lane];
                     }
                 }
+                // only the rows that hold routes are copied and multiplied
+                low_only = NF == 2 && (__ballot(!padded) >> 16) == 0;
                 g_dma_tile([&](int i) { return xq + (size_t)__shfl(my_tok, i, 64) * dim; },
                            [&](int i) { return xs + (size_t)__shfl(my_tok, i, 64) * (dim / 32); },
-                           ROWS, dim, w, lane, a_l, as_l);
+                           low_only ? 16 : ROWS, dim, w, lane, a_l, as_l);
                 __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
                 lds_barrier();
                 cur_blk = blk;
@@ -320,7 +325,10 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 #pragma unroll
             for (int i = 0; i < NF; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        g_compute<EXACT, NF>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        if (low_only)  // uniform; the upper fragment's sums stay 0 (padding slots)
+            g_compute<EXACT, 1>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        else
+            g_compute<EXACT, NF>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
         load_q(st, q + 2);
         if (c == cs.nch - 1) {  // the unit's K parts are complete: epilogue
 #pragma unroll
@@ -366,8 +374,9 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 template <bool EXACT>
 __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
-    const int32_t *__restrict__ num_tiles, const uint8_t *__restrict__ w2,
-    const uint8_t *__restrict__ s2, float *__restrict__ out, int dim, int inter, int n_experts) {
+    const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ order,
+    const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
+    int dim, int inter, int n_experts) {
     extern __shared__ __align__(16) uint8_t g_lds[];
     uint8_t *a_l = g_lds;                                // [32][inter + 16]
     uint8_t *as_l = g_lds + g_a_lds(kTile, inter);      // [32][inter/32] (+ padding)
@@ -397,6 +406,10 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     load_q(s1, 1);
     mem_order();
     int cur_tile = -1;
+    // with `order`: the tile's slots that hold routes (bit i: slot i); only
+    // those rows are written, and a tile whose slots 16.. are all padding
+    // copies and multiplies 16 rows. Without it every slot counts.
+    uint32_t real = 0xFFFFFFFFu;
     v4f acc[2];
     auto step = [&](Fp4Stage &st, int q) {
         const int u = cs.unit(q), c = q % cs.nch;
@@ -404,25 +417,34 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
         const int slot0 = tile * kTile;
         if (c == 0) {
             if (tile != cur_tile) {  // uniform: stage the tile's hq rows in LDS
+                if (order) {
+                    const bool has = lane < kTile && order[slot0 + min(lane, kTile - 1)] >= 0;
+                    real = (uint32_t)__ballot(has);
+                }
                 lds_barrier();       // every wave is done with the previous tile
                 g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
-                           [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); }, kTile,
-                           inter, w, lane, a_l, as_l);
+                           [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); },
+                           (real >> 16) == 0 ? 16 : kTile, inter, w, lane, a_l, as_l);
                 __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
                 lds_barrier();
                 cur_tile = tile;
             }
             acc[0] = acc[1] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        g_compute<EXACT, 2>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        if ((real >> 16) == 0)  // uniform
+            g_compute<EXACT, 1>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        else
+            g_compute<EXACT, 2>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
         load_q(st, q + 2);
         if (c == cs.nch - 1) {
             const int col = nt * 128 + w * 16 + r;
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    out[(size_t)(slot0 + i * 16 + 4 * g + v) * dim + col] = acc[i][v];
+                for (int v = 0; v < 4; v++) {
+                    const int row = i * 16 + 4 * g + v;
+                    if ((real >> row) & 1) out[(size_t)(slot0 + row) * dim + col] = acc[i][v];
+                }
         }
     };
     int q = 0;
@@ -531,6 +553,11 @@ int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t
     return launch_status();
 }
 
+static int grouped_down_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+                               const int32_t *num_tiles, const int32_t *order, const uint8_t *w2,
+                               const uint8_t *s2, float *out, int64_t dim, int64_t inter,
+                               int64_t n_experts, int64_t tiles, ws_stream_t stream);
+
 int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
                         const int32_t *num_tiles, const uint8_t *w2, const uint8_t *s2,
                         float *out, int64_t dim, int64_t inter, int64_t n_experts, int64_t tiles,
@@ -540,15 +567,25 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
     if (dim % 128 || inter % 128 || tiles > 65535) return WS_ERR_SHAPE;
     if (!al16(hq) || !al16(w2) || !al4(hs) || !al8(s2)) return WS_ERR_INVALID_ARG;
     if (inter > 4096) return WS_ERR_SHAPE;  // the 32 x inter hq tile lives in LDS
+    return grouped_down_launch(hq, hs, tile_expert, num_tiles, nullptr, w2, s2, out, dim, inter,
+                               n_experts, tiles, stream);
+}
+
+// order == nullptr: every slot of a used tile is computed and written
+static int grouped_down_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+                               const int32_t *num_tiles, const int32_t *order, const uint8_t *w2,
+                               const uint8_t *s2, float *out, int64_t dim, int64_t inter,
+                               int64_t n_experts, int64_t tiles, ws_stream_t stream) {
+    (void)tiles;
     const size_t lds = g_tile_lds(kTile, (int)inter);
     dim3 grid((unsigned)cu_count());
     if (math_mode() == WS_MATH_EXACT)
         hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(kGThreads), lds, stream, hq, hs,
-                           tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
+                           tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,
                            (int)n_experts);
     else
         hipLaunchKernelGGL(grouped_down_kernel<false>, grid, dim3(kGThreads), lds, stream, hq, hs,
-                           tile_expert, num_tiles, w2, s2, out, (int)dim, (int)inter,
+                           tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,
                            (int)n_experts);
     return launch_status();
 }
@@ -584,6 +621,7 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
         return WS_ERR_INVALID_ARG;
     // every stage's shape limit, checked before the first launch
     if (dim % 128 || inter % 128 || dim > 8192 || inter > 4096) return WS_ERR_SHAPE;
+    if (!w2 || !s2 || !al16(w2) || !al8(s2)) return WS_ERR_INVALID_ARG;
     if (workspace_bytes < ws_moe_prefill_workspace_size(rows, dim, inter, top_k, n_experts) ||
         !al16(workspace))
         return WS_ERR_INVALID_ARG;
@@ -616,8 +654,10 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
     rc = ws_moe_grouped_glu_quant(xq, xs, order, layout_w, tile_expert, ntiles, w1, s1, w3, s3, hq,
                                   hs, dim, inter, n_experts, top_k, tiles, swiglu_limit, stream);
     if (rc) return rc;
-    rc = ws_moe_grouped_down(hq, hs, tile_expert, ntiles, w2, s2, down, dim, inter, n_experts,
-                             tiles, stream);
+    // only the slots that hold routes are multiplied and written (the
+    // combine reads those)
+    rc = grouped_down_launch(hq, hs, tile_expert, ntiles, order, w2, s2, down, dim, inter,
+                             n_experts, tiles, stream);
     if (rc) return rc;
     return ws_moe_combine(down, route_pos, y, rows, dim, top_k, tiles, stream);
 }
