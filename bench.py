@@ -43,7 +43,9 @@ EXPERT_BYTES = 3 * (FP4_MAT + FP4_SC)
 # rocprofv3 FETCH_SIZE + WRITE_SIZE counter runs calibrated against a plain
 # 256 MiB copy (profiles/traffic_hot_kernels.md holds the runs and
 # commands; counters cannot be read from inside this process).
-GLU_TRAFFIC_BYTES = 71806821
+# The gate/up kernel as the decode step runs it (routing fused in:
+# expert_glu_quant_kernel<true, true, 6>).
+GLU_TRAFFIC_BYTES = 71934874
 
 
 def log(*a):
@@ -136,22 +138,36 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
         L.emit8(x[t], xq[t], xs[t], DIM, stream=s)
     torch.cuda.synchronize()
 
-    glu = lambda t, st: L.expert_glu_quant_x(x[t % n_tokens], idx[t % n_tokens], wts[t % n_tokens],
-                                             w1, s1, w3, s3, hq[t % n_tokens], hs[t % n_tokens],
-                                             INTER, DIM, E, TOPK, stream=st)
+    # the gate/up kernel as the step runs it: routing from the logits fused in
+    ridx = torch.empty_like(idx)
+    rwts = torch.empty_like(wts)
+    glu = lambda t, st: L.expert_glu_quant_route(
+        logits[t % n_tokens], bias, L.SCORE_SIGMOID, 1.0, 1, 1.0, x[t % n_tokens], w1, s1, w3,
+        s3, hq[t % n_tokens], hs[t % n_tokens], ridx[t % n_tokens], rwts[t % n_tokens], DIM,
+        INTER, E, TOPK, stream=st)
+    # the same kernel with the picks given (no routing)
+    glu_given = lambda t, st: L.expert_glu_quant_x(x[t % n_tokens], idx[t % n_tokens],
+                                                   wts[t % n_tokens], w1, s1, w3, s3,
+                                                   hq[t % n_tokens], hs[t % n_tokens], INTER,
+                                                   DIM, E, TOPK, stream=st)
     red = lambda t, st: L.expert_reduce(hq[t % n_tokens], hs[t % n_tokens], w2, s2, idx[t % n_tokens],
                                         y[t % n_tokens], DIM, INTER, E, TOPK, stream=st)
     for t in range(n_tokens):
         glu(t, s)
     reps_k = max(100, n_tokens)
     glu_avg, glu_med = graph_time(torch, glu, reps_k)
+    given_avg, given_med = graph_time(torch, glu_given, reps_k)
     red_avg, red_med = graph_time(torch, red, reps_k)
     glu_bytes = TOPK * 2 * (FP4_MAT + FP4_SC) + 4 * DIM + TOPK * (INTER + INTER // 32)
     red_bytes = TOPK * (FP4_MAT + FP4_SC) + TOPK * (INTER + INTER // 32) + DIM * 4
     kern = {
+        # + the logits and bias the fused routing reads
         "expert_glu_quant_kernel": {"avg_us": glu_avg * 1e3, "median_us": glu_med * 1e3,
-                                    "bytes": glu_bytes,
-                                    "GB/s": glu_bytes / (glu_avg * 1e-3) / 1e9},
+                                    "bytes": glu_bytes + 2 * E * 4,
+                                    "GB/s": (glu_bytes + 2 * E * 4) / (glu_avg * 1e-3) / 1e9},
+        "expert_glu_quant_kernel (picks given, no routing)": {
+            "avg_us": given_avg * 1e3, "median_us": given_med * 1e3, "bytes": glu_bytes,
+            "GB/s": glu_bytes / (given_avg * 1e-3) / 1e9},
         "expert_reduce_kernel": {"avg_us": red_avg * 1e3, "median_us": red_med * 1e3,
                                  "bytes": red_bytes,
                                  "GB/s": red_bytes / (red_avg * 1e-3) / 1e9},
@@ -515,7 +531,8 @@ def main():
     gen.set_state(gen_state)
     res = bench_moe(L, torch, dev, args.steps, args.warmup, args.tokens, slabs, gen, packed)
     k = res["kernels"]["expert_glu_quant_kernel"]
-    roof = {"kernel": "expert_glu_quant_kernel", "bound": "hbm", "achieved": k["GB/s"],
+    roof = {"kernel": "expert_glu_quant_kernel<exact, f32 token, routing fused>", "bound": "hbm",
+            "achieved": k["GB/s"],
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["GB/s"] / PEAK_HBM_GBS,
             "traffic": GLU_TRAFFIC_BYTES,
             "algorithmic_bytes": k["bytes"], "avg_us": k["avg_us"],

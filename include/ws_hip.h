@@ -240,6 +240,20 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
                           const uint8_t *s3, uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter,
                           int64_t n_experts, int64_t top_k, float swiglu_limit,
                           ws_stream_t stream);
+/* moe_select (launch.rs:1043, moe.cu:48) fused into ws_expert_glu_quant_x:
+ * the gate/up kernel of ws_moe_decode_route on its own. Every workgroup
+ * routes the token from logits[E] (+ bias, score_func sigmoid or
+ * sqrtsoftplus, gate_temp, norm_topk_prob, route_scale as ws_moe_topk) and
+ * writes hq/hs [top_k, inter] (+ [top_k, inter/32]) by pick rank; the picks
+ * land in topk_idx / topk_w [top_k]. dim <= 8192, E <= 1024; softmax scores
+ * are rejected (WS_ERR_INVALID_ARG: they need the sequential sum). */
+int ws_expert_glu_quant_route(const float *logits, const float *bias, int score_func,
+                              float gate_temp, int norm_topk_prob, float route_scale,
+                              const float *x, const uint8_t *w1, const uint8_t *s1,
+                              const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                              int32_t *topk_idx, float *topk_w, int64_t dim, int64_t inter,
+                              int64_t n_experts, int64_t top_k, float swiglu_limit,
+                              ws_stream_t stream);
 /* expert_reduce (moe_grouped.cu:165, launch.rs:178-206): y[dim] = sum over
  * picks in ascending expert id of w2_e . h_e, one f32 add per expert. */
 int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,

@@ -231,3 +231,32 @@ def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
     assert torch.equal(idx1, idx2)
     assert np.array_equal(host(w1_).view(np.uint32), host(w2_).view(np.uint32))
     assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
+
+
+@pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (384, 5120, 2304, 6, 2)])
+def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score):
+    """The routed gate/up entry point gives ws_moe_topk's picks and weights
+    and ws_expert_glu_quant_x's hq / hs on them, bit for bit."""
+    rng = np.random.default_rng(760 + E + dim)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(760 + dim)
+    P = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
+    logits = dev(rng.standard_normal(E).astype(np.float32))
+    bias = dev((rng.standard_normal(E) * 0.1).astype(np.float32))
+    x = dev(rng.standard_normal(dim).astype(np.float32))
+    announce("expert_glu_quant_route E=%d dim=%d inter=%d k=%d score=%d" % (E, dim, inter, k, score))
+    idx1 = torch.empty(k, dtype=torch.int32, device=DEV)
+    w1_ = torch.empty(k, dtype=torch.float32, device=DEV)
+    L.moe_topk(logits, bias, None, idx1, w1_, 1, E, k, score, 1.0, True, 1.0)
+    hq1 = torch.zeros((k, inter), dtype=torch.uint8, device=DEV)
+    hs1 = torch.zeros((k, inter // 32), dtype=torch.uint8, device=DEV)
+    L.expert_glu_quant_x(x, idx1, w1_, P[0], P[1], P[2], P[3], hq1, hs1, inter, dim, E, k)
+    idx2 = torch.full((k,), -5, dtype=torch.int32, device=DEV)
+    w2_ = torch.zeros(k, dtype=torch.float32, device=DEV)
+    hq2 = torch.zeros((k, inter), dtype=torch.uint8, device=DEV)
+    hs2 = torch.zeros((k, inter // 32), dtype=torch.uint8, device=DEV)
+    L.expert_glu_quant_route(logits, bias, score, 1.0, 1, 1.0, x, P[0], P[1], P[2], P[3], hq2, hs2,
+                             idx2, w2_, dim, inter, E, k)
+    assert torch.equal(idx1, idx2)
+    assert np.array_equal(host(w1_).view(np.uint32), host(w2_).view(np.uint32))
+    assert torch.equal(hq1, hq2) and torch.equal(hs1, hs2)

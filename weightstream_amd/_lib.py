@@ -77,6 +77,7 @@ SIGNATURES = {
                                   C.c_size_t, _p]),
     "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_x": (_i, [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
+    "ws_expert_glu_quant_route": (_i, [_p, _p, _i, _f, _i, _f] + [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_reduce": (_i, [_p] * 6 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
     "ws_moe_decode": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),

@@ -612,6 +612,30 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
                       inter, n_experts, top_k, swiglu_limit, stream);
 }
 
+int ws_expert_glu_quant_route(const float *logits, const float *bias, int score_func,
+                              float gate_temp, int norm_topk_prob, float route_scale,
+                              const float *x, const uint8_t *w1, const uint8_t *s1,
+                              const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
+                              int32_t *topk_idx, float *topk_w, int64_t dim, int64_t inter,
+                              int64_t n_experts, int64_t top_k, float swiglu_limit,
+                              ws_stream_t stream) {
+    if (!logits || !bias || !x || !w1 || !s1 || !w3 || !s3 || !hq || !hs || !topk_idx || !topk_w)
+        return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExperts || top_k > kMaxTopk || top_k > n_experts) return WS_ERR_SHAPE;
+    if (score_func != WS_SCORE_SIGMOID && score_func != WS_SCORE_SQRTSOFTPLUS)
+        return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (dim > kMaxDimF32) return WS_ERR_SHAPE;
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
+        ((uintptr_t)s3 & 7))
+        return WS_ERR_INVALID_ARG;
+    const RouteArgs ra{logits, bias, score_func, gate_temp, norm_topk_prob, route_scale,
+                       topk_idx, topk_w};
+    return glu_launch(nullptr, nullptr, x, nullptr, nullptr, &ra, w1, s1, w3, s3, hq, hs, dim,
+                      inter, n_experts, top_k, swiglu_limit, stream);
+}
+
 int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
                      const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim, int64_t inter,
                      int64_t n_experts, int64_t top_k, ws_stream_t stream) {

@@ -264,6 +264,17 @@ def expert_glu_quant_x(x, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slots, s_slots
           swiglu_limit, _s(stream))
 
 
+def expert_glu_quant_route(logits, bias, score_func, gate_temp, norm_topk_prob, route_scale, x,
+                           w1, s1, w3, s3, hq, hs, topk_idx, topk_w, dim, inter, n_experts, top_k,
+                           swiglu_limit=10.0, stream=None):
+    """The gate/up kernel of moe_decode_route on its own: routing from the
+    logits fused in; picks to topk_idx / topk_w, hidden states to hq / hs."""
+    _call("ws_expert_glu_quant_route", _ptr(logits), _ptr(bias), int(score_func), float(gate_temp),
+          int(norm_topk_prob), float(route_scale), _ptr(x), _ptr(w1), _ptr(s1), _ptr(w3),
+          _ptr(s3), _ptr(hq), _ptr(hs), _ptr(topk_idx), _ptr(topk_w), dim, inter, n_experts,
+          top_k, swiglu_limit, _s(stream))
+
+
 def expert_reduce(act_slots, act_s_slots, w2, w2_s, gate_idx, y, dim, inter, n_experts, top_k,
                   stream=None):
     _call("ws_expert_reduce", _ptr(act_slots), _ptr(act_s_slots), _ptr(gate_idx), _ptr(w2),
