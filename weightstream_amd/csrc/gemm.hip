@@ -770,15 +770,6 @@ static int launch_al(const uint8_t *a, const void *sa, const uint8_t *b, const v
     if ((size_t)kAlWaves * kAlRows * 16 * NF * 4 > lds) return -1;  // the partials reuse it
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + kAlRows - 1) / kAlRows));
     const bool exact = math_mode() != WS_MATH_NATIVE;
-    const void *fn = exact ? (const void *)gemm_al_kernel<NF, SMODE, OMODE, true>
-                           : (const void *)gemm_al_kernel<NF, SMODE, OMODE, false>;
-    static bool attr_set[2] = {false, false};
-    if (!attr_set[exact]) {
-        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
-            hipSuccess)
-            return -1;
-        attr_set[exact] = true;
-    }
     if (exact)
         hipLaunchKernelGGL((gemm_al_kernel<NF, SMODE, OMODE, true>), grid, dim3(64 * kAlWaves), lds,
                            stream, a, sa, b, sb, out, m, n, k);

@@ -51,10 +51,13 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
 #pragma unroll
         for (int ww = 0; ww < kDispThreads / 64; ww++) wcnt[ww][t] = 0;
         __syncthreads();
+        // the wave's routes of the same expert: lane l's expert read as a
+        // scalar (readlane), not through an LDS permute
         int inrank = 0, cnt = 0;
+#pragma unroll 8
         for (int l = 0; l < 64; l++) {
-            int el = __shfl(e, l, 64);
-            bool same = el == e;
+            const int el = __builtin_amdgcn_readlane(e, l);
+            const bool same = el == e;
             cnt += same;
             inrank += (same && l < lane);
         }
