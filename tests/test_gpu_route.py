@@ -57,11 +57,13 @@ def test_device_expf_equals_glibc_on_every_input():
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("m,dim,E", [(3, 4096, 384), (1, 4096, 384), (40, 1024, 100), (1, 1000, 64), (5, 768, 50),
-                                     (17, 256, 33)])
+                                     (17, 256, 33), (6, 5120, 384), (8, 4096, 384), (9, 4096, 384),
+                                     (2, 512, 7)])
 def test_gate_logits_bit_exact(bf16, m, dim, E):
-    """dim % 256 == 0: the pipelined kernel (4 x 1, 16 x 4 or 8 x 8 blocks of
-    experts x tokens, partial ones at the edges); otherwise the per-lane
-    kernel."""
+    """dim % 256 == 0: up to 8 tokens the producer/consumer kernel (4 experts
+    per workgroup), more tokens the pipelined kernel (8 x 8 blocks of experts
+    x tokens), partial blocks at the edges; otherwise the per-lane kernel.
+    (6, 5120, 384): the DS4.1F gate for a verify batch."""
     rng = np.random.default_rng(200 + bf16 + m + dim)
     x = rng.standard_normal((m, dim)).astype(np.float32)
     w = (rng.standard_normal((E, dim)) * 0.02).astype(np.float32)
