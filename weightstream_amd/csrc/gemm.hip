@@ -1218,7 +1218,10 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         // 64-row blocks (M=128, N=4096) or 32-row blocks (M=128, N=2048;
         // M=64, N=4096). Measured at K=4096: 16.4 us (kp) and 10.0 us (A in
         // LDS; kp 11.3) against 19.7 and 15.7 for the split-K kernel.
-        if (M > 16 && N % 32 == 0) {
+        // (measured at M=128: for K = 5120, or N = 5120 with K = 2048-2304,
+        // the split-K pipeline is faster: 17.8 against 27.8 us at N=2304,
+        // K=5120; 16.5 against 22.0 at N=5120, K=2304)
+        if (M > 16 && N % 32 == 0 && K <= 4096 && N <= 4096) {
             const long cus = cu_count();
             const long wg64 = (long)(N / 32) * ((M + 63) / 64), wg32 = (long)(N / 32) * ((M + 31) / 32);
             if (wg64 * 4 >= cus * 3 && wg64 * 2 <= cus * 3) {
