@@ -397,8 +397,9 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     with its own weights: FP8 attention output projection (K=8192 -> 4096)
     added to the residual, f32 gate GEMV (384 x 4096), top-8 sigmoid routing,
     the 384 routed FP4 experts (M=1: ws_moe_decode_route; M>1: ws_moe_topk +
-    the grouped ws_moe_prefill), the shared FP8 expert (inter 2048) and the
-    two acc_f32 adds. Routed layers 2..4 are device copies of layer 1's packed
+    the grouped ws_moe_prefill), the shared FP8 expert (inter 2048; w1 and w3
+    fused into one w13 matrix as the engine loads them, engine.rs:1520, one
+    gate/up GEMM as at :4067) and the two acc_f32 adds. Routed layers 2..4 are device copies of layer 1's packed
     experts (distinct memory, so no layer reads another's weights from
     cache). Reported per layer; bytes = weights touched once."""
     import numpy as np
@@ -416,7 +417,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     for li in range(layers):
         routed = packed if li == 0 else tuple(t.clone() for t in packed)
         lay.append({"routed": routed, "wo": fp8(DIM, OD),
-                    "shared": fp8(SI, DIM) + fp8(SI, DIM) + fp8(DIM, SI),
+                    "shared": fp8(2 * SI, DIM) + fp8(DIM, SI),
                     "gate": torch.empty((E, DIM), dtype=torch.float32, device=dev).normal_(
                         0.0, 0.02, generator=gen),
                     "bias": torch.randn((E,), device=dev, generator=gen) * 0.1})
@@ -457,7 +458,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
                                L.SCORE_SIGMOID, 1.0, True, 1.0, stream=st)
                     L.moe_prefill(h, idx[li], wts[li], *w["routed"], yr, M, DIM, INTER, E, TOPK,
                                   pws, stream=st)
-                L.shared_expert_fp8(h, *w["shared"], ys, M, DIM, SI, sws, stream=st)
+                L.shared_expert_fp8_w13(h, *w["shared"], ys, M, DIM, SI, sws, stream=st)
                 L.acc_f32(ys, yr, M * DIM, stream=st)
                 L.acc_f32(yr, h, M * DIM, stream=st)
 

@@ -197,6 +197,16 @@ int ws_shared_expert_fp8(const float *x, const uint8_t *w1, const uint8_t *s1, c
                          const uint8_t *s3, const uint8_t *w2, const uint8_t *s2, float *y,
                          int64_t m, int64_t dim, int64_t inter, float swiglu_limit,
                          void *workspace, size_t workspace_bytes, ws_stream_t stream);
+/* The shared expert with w1 and w3 fused row-wise into one FP8 matrix
+ * w13 [2 * inter, dim] (rows 0..inter-1 = w1, inter.. = w3; UE8M0 scales
+ * [2 * inter / 32, dim / 32]), as the engine loads it
+ * (engine.rs:1520-1530 load_q8_combined_rows) and runs it (engine.rs:4067
+ * moe_shared_step: one GEMM of N = 2 * inter, gate = its first inter
+ * columns, up = the rest). Same workspace as ws_shared_expert_fp8. */
+int ws_shared_expert_fp8_w13(const float *x, const uint8_t *w13, const uint8_t *s13,
+                             const uint8_t *w2, const uint8_t *s2, float *y, int64_t m,
+                             int64_t dim, int64_t inter, float swiglu_limit, void *workspace,
+                             size_t workspace_bytes, ws_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Packed FP4 expert weights. The routed-expert entry points below read FP4

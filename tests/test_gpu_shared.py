@@ -62,6 +62,32 @@ def test_shared_expert_matches_oracle(m, dim, inter, limit, split_k):
     assert_close(got, want, TOL, "shared_expert_fp8 m=%d dim=%d inter=%d" % (m, dim, inter))
 
 
+@pytest.mark.parametrize("m,dim,inter", [(1, 4096, 2048), (6, 5120, 2304), (64, 1024, 512)])
+def test_shared_expert_w13_matches_oracle(m, dim, inter):
+    """w1 and w3 fused row-wise (the engine's shared_w13): the same expert."""
+    rng = np.random.default_rng(7100 + m + dim)
+    w1, s1 = _fp8_weights(rng, inter, dim)
+    w3, s3 = _fp8_weights(rng, inter, dim)
+    w2, s2 = _fp8_weights(rng, dim, inter)
+    x = (rng.standard_normal((m, dim)) * 4.0).astype(np.float32)
+    want = np.stack([O.shared_fp8(w1, s1, w3, s3, w2, s2, dim, inter, x[t], 10.0)
+                     for t in range(m)])
+    announce("shared_expert_fp8_w13 m=%d dim=%d inter=%d" % (m, dim, inter))
+    gws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)
+    L.set_gemm_workspace(gws)
+    try:
+        ws = torch.empty(L.shared_expert_workspace_size(m, dim, inter), dtype=torch.uint8,
+                         device=DEV)
+        y = torch.full((m, dim), float("nan"), dtype=torch.float32, device=DEV)
+        L.shared_expert_fp8_w13(dev(x), dev(np.concatenate([w1, w3])), dev(np.concatenate([s1, s3])),
+                                dev(w2), dev(s2), y, m, dim, inter, ws)
+        got = host(y)
+    finally:
+        torch.cuda.synchronize()
+        L.set_gemm_workspace(None)
+    assert_close(got, want, TOL, "shared_expert_fp8_w13 m=%d dim=%d inter=%d" % (m, dim, inter))
+
+
 def test_shared_expert_rejects_bad_shapes():
     ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
     b = torch.zeros(1 << 16, dtype=torch.uint8, device=DEV)

@@ -15,17 +15,20 @@ namespace ws {
 
 // h = silu(min(g, L)) * clamp(u, -L, L) (moe.rs:187-201 with weight 1; L <= 0
 // disables both clamps), then the 1x32 FP8 quantisation of actquant.rs:21-45.
-// One thread per element; a 32-lane half-wave is one scale block.
+// One thread per element of h [rows, inter]; gate and up rows are `ld`
+// floats apart (inter for separate buffers, 2 * inter for the fused w13
+// output); a 32-lane half-wave is one scale block.
 __global__ __launch_bounds__(256) void swiglu_emit8_kernel(const float *__restrict__ gate,
                                                            const float *__restrict__ up,
                                                            uint8_t *__restrict__ hq,
                                                            uint8_t *__restrict__ hs, int64_t n,
-                                                           float limit) {
+                                                           int inter, int ld, float limit) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const bool live = i < n;  // n % 32 == 0: a half-wave is all live or all dead
     float h = 0.0f;
     if (live) {
-        float g = gate[i], u = up[i];
+        const int64_t o = (i / inter) * ld + i % inter;
+        float g = gate[o], u = up[o];
         if (limit > 0.0f) {
             u = rclamp(u, -limit, limit);
             g = fminf(g, limit);
@@ -115,7 +118,31 @@ int ws_shared_expert_fp8(const float *x, const uint8_t *w1, const uint8_t *s1, c
     if (rc) return rc;
     const int64_t n = m * inter;
     hipLaunchKernelGGL(swiglu_emit8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       g, u, hq, hs, n, swiglu_limit);
+                       g, u, hq, hs, n, (int)inter, (int)inter, swiglu_limit);
+    rc = launch_status();
+    if (rc) return rc;
+    return ws_fp8_gemm(hq, hs, w2, s2, y, m, dim, inter, stream);
+}
+
+int ws_shared_expert_fp8_w13(const float *x, const uint8_t *w13, const uint8_t *s13,
+                             const uint8_t *w2, const uint8_t *s2, float *y, int64_t m,
+                             int64_t dim, int64_t inter, float swiglu_limit, void *workspace,
+                             size_t workspace_bytes, ws_stream_t stream) {
+    if (!x || !w13 || !s13 || !w2 || !s2 || !y || !workspace) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || dim <= 0 || inter <= 0 || dim % 128 || inter % 128) return WS_ERR_SHAPE;
+    const SharedLayout l = shared_layout(m, dim, inter);
+    if (workspace_bytes < l.total || ((uintptr_t)workspace & 255)) return WS_ERR_INVALID_ARG;
+    uint8_t *ws = (uint8_t *)workspace;
+    uint8_t *xq = ws + l.xq, *xs = ws + l.xs, *hq = ws + l.hq, *hs = ws + l.hs;
+    // gate|up rows [m, 2 * inter] span the two adjacent f32 regions
+    float *gu = (float *)(ws + l.g);
+    int rc = ws_emit8(x, xq, xs, m * dim, stream);
+    if (rc) return rc;
+    rc = ws_fp8_gemm(xq, xs, w13, s13, gu, m, 2 * inter, dim, stream);
+    if (rc) return rc;
+    const int64_t n = m * inter;
+    hipLaunchKernelGGL(swiglu_emit8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       gu, gu + inter, hq, hs, n, (int)inter, (int)(2 * inter), swiglu_limit);
     rc = launch_status();
     if (rc) return rc;
     return ws_fp8_gemm(hq, hs, w2, s2, y, m, dim, inter, stream);

@@ -237,6 +237,15 @@ def shared_expert_workspace_size(m, dim, inter):
     return int(_lib.load().ws_shared_expert_workspace_size(m, dim, inter))
 
 
+def shared_expert_fp8_w13(x, w13, s13, w2, s2, y, m, dim, inter, workspace, swiglu_limit=10.0,
+                          stream=None):
+    """The shared expert with w1 / w3 fused row-wise into w13 [2 * inter, dim]
+    (engine.rs:1520 load_q8_combined_rows, :4067 one GEMM for gate and up)."""
+    _call("ws_shared_expert_fp8_w13", _ptr(x), _ptr(w13), _ptr(s13), _ptr(w2), _ptr(s2), _ptr(y),
+          m, dim, inter, swiglu_limit, _ptr(workspace),
+          workspace.numel() * workspace.element_size(), _s(stream))
+
+
 def shared_expert_fp8(x, w1, s1, w3, s3, w2, s2, y, m, dim, inter, workspace,
                       swiglu_limit=10.0, stream=None):
     """moe.rs:210-250 shared_expert_hidden for m tokens (engine.rs:4063
