@@ -233,7 +233,8 @@ def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
     assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
 
 
-@pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (384, 5120, 2304, 6, 2)])
+@pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (384, 5120, 2304, 6, 2),
+                                                 (64, 1024, 512, 4, 1), (100, 2048, 768, 6, 2)])
 def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score):
     """The routed gate/up entry point gives ws_moe_topk's picks and weights
     and ws_expert_glu_quant_x's hq / hs on them, bit for bit."""
