@@ -245,11 +245,18 @@ void or_fp8_act_emit(const float *x, size_t n, uint8_t *q, uint8_t *s) {
 }
 
 /* actquant.rs:110-138: per 32-K block, blk += qa*(w*s_b) in K order; acc += blk. */
+/* Threads for the row loops of the GEMVs (1 = the reference's scalar loop).
+ * Rows are independent and each keeps its sequential sum, so the results do
+ * not depend on the count; only the timing baseline uses more than one. */
+static int g_threads = 1;
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+
 void or_fp8_gemv(const uint8_t *w, const uint8_t *s, size_t rows, size_t cols, const float *x, float *y) {
     size_t kbn = cols / 32;
     float *qa = (float *)malloc(cols * sizeof(float));
     memcpy(qa, x, cols * sizeof(float));
     or_fp8_snap(qa, cols, 32);
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t n = 0; n < rows; n++) {
         const uint8_t *row = w + n * cols;
         size_t srow = (n / 32) * kbn;
@@ -274,6 +281,7 @@ void or_fp4_gemv(const uint8_t *w, const uint8_t *s, size_t rows, size_t cols, c
     float *qa = (float *)malloc(cols * sizeof(float));
     memcpy(qa, x, cols * sizeof(float));
     or_fp8_snap(qa, cols, 32);
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t n = 0; n < rows; n++) {
         const uint8_t *row = w + n * half;
         float acc = 0.0f;

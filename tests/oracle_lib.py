@@ -72,6 +72,7 @@ _sigs = {
                              _f32p, _sz, C.c_float, _f32p]),
     "or_dispatch": (None, [_i32p, _f32p, _sz, _sz, _sz, _i32p, _f32p, _i32p, _i32p, _i32p,
                            _i32p, _i32p, _i32p]),
+    "or_set_threads": (None, [C.c_int]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(lib, _n)
@@ -93,6 +94,11 @@ sigmoid = lib.or_sigmoid
 silu = lib.or_silu
 softplus = lib.or_softplus
 expf = lib.or_expf
+
+
+def set_threads(n):
+    """Threads for the oracle's GEMV row loops (1 = the reference's scalar loop)."""
+    lib.or_set_threads(int(n))
 
 
 def fp4_value(nib):

@@ -195,3 +195,22 @@ def test_dispatch_invariants_zipf():
     assert nt == ((cnt + 31) // 32).sum() <= tiles
     te = d["tile_expert"]
     assert np.all(te[nt:] == -1) and np.all(np.diff(te[:nt]) >= 0)
+
+
+def test_threaded_oracle_is_bit_identical():
+    """The timing baseline's threaded GEMV rows give the scalar loop's bits."""
+    rng = np.random.default_rng(31)
+    E, dim, inter, k = 8, 512, 256, 4
+    w1, s1 = O.weight_quant_fp4((rng.standard_normal((E * inter, dim)) * 0.02).astype(np.float32))
+    w3, s3 = O.weight_quant_fp4((rng.standard_normal((E * inter, dim)) * 0.02).astype(np.float32))
+    w2, s2 = O.weight_quant_fp4((rng.standard_normal((E * dim, inter)) * 0.02).astype(np.float32))
+    x = rng.standard_normal(dim).astype(np.float32)
+    idx = np.array([5, 1, 7, 2], np.int32)
+    w = np.array([0.4, 0.3, 0.2, 0.1], np.float32)
+    want = O.moe_routed(w1, s1, w3, s3, w2, s2, dim, inter, x, idx, w)
+    try:
+        O.set_threads(4)
+        got = O.moe_routed(w1, s1, w3, s3, w2, s2, dim, inter, x, idx, w)
+    finally:
+        O.set_threads(1)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
