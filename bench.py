@@ -249,6 +249,62 @@ def cpu_baseline_moe(res, seconds, threads=1):
     return step_bytes * n / spent / 1e9, n, spent, worst, route_ok
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_gemm(L, torch, dev, threads):
+    """Configs 1 and 2 on the CPU: the C oracle's block-scaled FP8 GEMM
+    (restating weightstream-ref actquant.rs fp8_gemv, the reference order) on
+    the same UE8M0 data as the GPU bench, 1 thread (the reference's loop) and
+    `threads` OpenMP threads over output columns (same bits)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    K, N = 4096, 4096
+    w = torch.randn((N, K), device=dev, generator=gen) * 0.02
+    wq = torch.empty((N, K), dtype=torch.uint8, device=dev)
+    ws = torch.empty((N // 32, K // 32), dtype=torch.uint8, device=dev)
+    L.weight_quant_fp8(w, wq, ws, N, K)
+    x = torch.randn((128, K), device=dev, generator=gen)
+    aq = torch.empty((128, K), dtype=torch.uint8, device=dev)
+    asc = torch.empty((128, K // 32), dtype=torch.uint8, device=dev)
+    L.emit8(x, aq, asc, 128 * K)
+    torch.cuda.synchronize()
+    hw, hs, ha, has = (t.cpu().numpy() for t in (wq, ws, aq, asc))
+    out = {}
+    for name, M in (("config1_gemv_m1", 1), ("config2_gemm_m128_n4096", 128)):
+        bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 4
+        flops = 2.0 * M * N * K
+        res = {}
+        for th in (1, threads):
+            if M == 128 and th == 1:
+                continue  # ~5 s per call on one thread
+            O.set_threads(th)
+            calls, t0 = 0, time.perf_counter()
+            while True:
+                O.gemm_q(ha[:M], has[:M], M, hw, hs, N, K, False)
+                calls += 1
+                spent = time.perf_counter() - t0
+                if spent > 1.5 or calls >= 50:
+                    break
+            O.set_threads(1)
+            us = spent / calls * 1e6
+            res["%d_threads" % th] = {"us_per_call": us, "GB/s": bytes_ / (us * 1e-6) / 1e9,
+                                      "GFLOP/s": flops / (us * 1e-6) / 1e9, "calls": calls}
+        out[name] = res
+    out["cpu"] = "%s, %d threads" % (cpu_model(), threads)
+    return out
+
+
 def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
     """Configs 1 (M=1 GEMV, N=4096) and 2 (M=128, N in {4096, 12288, 2048}):
     K=4096 FP8 block-scaled GEMM, both scale formats (UE8M0 1x32/32x32 and
@@ -558,7 +614,7 @@ def main():
                          "weightstream-ref moe.rs/actquant.rs, GEMV rows on %d OpenMP threads "
                          "(same bits as the scalar loop); host has %d CPUs"
                          % (n, spent, threads, multiprocessing.cpu_count()),
-               "tokens_per_s": n / spent,
+               "tokens_per_s": n / spent, "cpu_model": cpu_model(),
                "single_thread": {"value": gbs1, "tokens": n1, "seconds": spent1,
                                  "tokens_per_s": n1 / spent1,
                                  "note": "the reference's scalar loop (no threading in "
@@ -580,6 +636,10 @@ def main():
         gemv = bench_gemm(L, torch, dev, 100, M=1, Ns=(4096,))
         gemm = bench_gemm(L, torch, dev, 40)
         shapes = bench_model_shapes(L, torch, dev)
+    cpu_gemm = None
+    if not args.no_cpu and not args.no_gemm:
+        import multiprocessing
+        cpu_gemm = cpu_baseline_gemm(L, torch, dev, max(1, min(16, multiprocessing.cpu_count())))
 
     line = {
         "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
@@ -608,6 +668,7 @@ def main():
                         "note": "FP4xFP8 scaled MFMA; ~13-bit internal accumulation"},
         "fp8_gemv_m1": gemv,
         "fp8_gemm_m128": gemm,
+        "cpu_baseline_gemm": cpu_gemm,
         "fp8_gemm_model_shapes": shapes,
         "moe_prefill_m132": prefill,
         "moe_prefill_m132_zipf_quarter": prefill_mild,

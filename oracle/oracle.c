@@ -311,6 +311,7 @@ void or_gemm_q(const uint8_t *aq, const uint8_t *as, size_t M,
     for (size_t m = 0; m < M; m++) {
         for (size_t c = 0; c < K; c++)
             qa[c] = or_e4m3_to_f32(aq[m * K + c]) * or_e8m0_to_f32(as[m * kbn + c / 32]);
+#pragma omp parallel for num_threads(g_threads) if (g_threads > 1) schedule(static)
         for (size_t n = 0; n < N; n++) {
             float acc = 0.0f;
             for (size_t kb = 0; kb < kbn; kb++) {
