@@ -261,3 +261,18 @@ def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score):
     assert torch.equal(idx1, idx2)
     assert np.array_equal(host(w1_).view(np.uint32), host(w2_).view(np.uint32))
     assert torch.equal(hq1, hq2) and torch.equal(hs1, hs2)
+
+
+def test_expert_glu_quant_route_rejects_softmax_and_bad_shapes():
+    """Softmax scores need the sequential sum over E (ws_moe_topk); shapes the
+    kernel cannot run are rejected before anything is launched."""
+    E, dim, inter, k = 64, 1024, 512, 4
+    f = torch.zeros(1 << 16, dtype=torch.float32, device=DEV)
+    b = torch.zeros(1 << 16, dtype=torch.uint8, device=DEV)
+    i = torch.zeros(16, dtype=torch.int32, device=DEV)
+    with pytest.raises(RuntimeError):
+        L.expert_glu_quant_route(f, f, O.SCORE_SOFTMAX, 1.0, 1, 1.0, f, b, b, b, b, b, b, i, f,
+                                 dim, inter, E, k)
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        L.expert_glu_quant_route(f, f, O.SCORE_SIGMOID, 1.0, 1, 1.0, f, b, b, b, b, b, b, i, f,
+                                 1000, inter, E, k)  # dim % 128

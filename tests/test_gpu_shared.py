@@ -108,3 +108,13 @@ def test_acc_f32_bit_exact(n):
     L.acc_f32(dev(x), dy, n)
     want = (y0 + x).astype(np.float32)
     assert np.array_equal(host(dy).view(np.uint32), want.view(np.uint32))
+
+
+def test_shared_expert_w13_rejects_bad_shapes():
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    b = torch.zeros(1 << 16, dtype=torch.uint8, device=DEV)
+    f = torch.zeros(1 << 14, dtype=torch.float32, device=DEV)
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        L.shared_expert_fp8_w13(f, b, b, b, b, f, 1, 128, 100, ws)  # inter % 128
+    with pytest.raises(RuntimeError):
+        L.shared_expert_fp8_w13(f, b, b, b, b, f, 1, 128, 128, ws[:16])  # workspace too small
