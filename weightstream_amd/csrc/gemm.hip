@@ -1197,9 +1197,13 @@ static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const 
     return launch_status();
 }
 
+// read once per process (a measurement knob, like WS_PIPE_S and WS_PIPE_BN)
 static int forced_cfg() {
-    const char *e = getenv("WS_GEMM_CFG");
-    return e ? atoi(e) : -1;
+    static const int forced = [] {
+        const char *e = getenv("WS_GEMM_CFG");
+        return e ? atoi(e) : -1;
+    }();
+    return forced;
 }
 
 template <bool BFP4, int SMODE, int OMODE>
