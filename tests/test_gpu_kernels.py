@@ -29,7 +29,8 @@ def _init():
 @pytest.fixture(params=["single_pass", "split_k"])
 def gemm_path(request):
     """Run a GEMM test with no split-K workspace (single-pass kernels) and
-    with one (M > 16 splits K across workgroups)."""
+    with one (M > 64, and M <= 16 when the column strips leave CUs idle,
+    split K across workgroups)."""
     ws = None
     if request.param == "split_k":
         ws = torch.empty(64 << 20, dtype=torch.uint8, device=DEV)

@@ -272,7 +272,8 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                                                                 const uint8_t *__restrict__ B,
                                                                 const void *__restrict__ SB,
                                                                 void *__restrict__ C, int M,
-                                                                int N, int K) {
+                                                                int N, int K, int S,
+                                                                float *__restrict__ part_out) {
     constexpr int kRows = 16 * MF * GMH;
     constexpr int kCols = 16 * NF;
     // UE8M0 activation scales: staged in LDS for blocks of rows; a single
@@ -289,7 +290,10 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     const int mb = blockIdx.y * kRows;           // workgroup's first row
     const int ml = wm * 16 * MF;                 // wave's first row within the workgroup
     const int ksteps = K / 128;
-    const int k0 = wk * ksteps / GK, k1 = (wk + 1) * ksteps / GK;
+    // K split S ways over blockIdx.z (S > 1: f32 partial planes, added in
+    // split order by split_reduce_kernel), then over the GK waves
+    const int kz0 = blockIdx.z * ksteps / S, kzn = (blockIdx.z + 1) * ksteps / S - kz0;
+    const int k0 = kz0 + wk * kzn / GK, k1 = kz0 + (wk + 1) * kzn / GK;
     const int kbn = K / 32, kb128 = K / 128;
 
     // activation scales of the workgroup's rows, one 32-bit word per (row,
@@ -500,14 +504,39 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
         float sum = part[rl * kCols + c];
 #pragma unroll
         for (int q = 1; q < GK; q++) sum = sum + part[(q * kRows + rl) * kCols + c];
-        if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + n0 + c] = sum;
+        if (S > 1) part_out[((size_t)blockIdx.z * M + row) * N + n0 + c] = sum;
+        else if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + n0 + c] = sum;
         else ((uint16_t *)C)[(size_t)row * N + n0 + c] = f32_to_bf16(sum);
+    }
+}
+
+// out = the S partial planes [S][M][N] summed in plane order (deterministic)
+template <int OMODE>
+__global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restrict__ part,
+                                                          void *__restrict__ C, int64_t mn,
+                                                          int S) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;  // mn % 4 == 0 (N % 16 == 0)
+    float4 acc = *(const float4 *)(part + i);
+    for (int z = 1; z < S; z++) {
+        const float4 v = *(const float4 *)(part + (size_t)z * mn + i);
+        acc.x = acc.x + v.x;
+        acc.y = acc.y + v.y;
+        acc.z = acc.z + v.z;
+        acc.w = acc.w + v.w;
+    }
+    if (OMODE == kOutF32) {
+        *(float4 *)((float *)C + i) = acc;
+    } else {
+        uint16_t *o = (uint16_t *)C + i;
+        *(uint2 *)o = uint2{(uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16),
+                            (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16)};
     }
 }
 
 template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U>
 static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
-                     int m, int n, int k, hipStream_t stream) {
+                     int m, int n, int k, hipStream_t stream, int S = 1, float *part = nullptr) {
     constexpr int rows = 16 * MF * GMH, threads = 64 * GMH * GK;
     if (n % (16 * NF)) return -1;
     const int ksteps = k / 128;
@@ -515,14 +544,37 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     if (stage && rows * ksteps > threads * kKpMaxSaWords)
         return -1;  // caller falls back to the general kernel
     size_t lds = (size_t)GK * rows * 16 * NF * 4 + (size_t)ksteps * rows * 4;
-    dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows));
+    if (S < 1 || (S > 1 && !part)) return -1;
+    dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows), (unsigned)S);
     if (math_mode() == WS_MATH_NATIVE)
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k);
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part);
     else
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k);
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part);
+    int rc = launch_status();
+    if (rc || S == 1) return rc;
+    const int64_t mn = (int64_t)m * n;
+    hipLaunchKernelGGL((split_reduce_kernel<OMODE>), dim3((unsigned)((mn / 4 + 255) / 256)),
+                       dim3(256), 0, stream, part, out, mn, S);
     return launch_status();
+}
+
+// K splits for a 16-column-strip GEMM of at most 16 rows: enough to give
+// every CU a workgroup when the strips alone leave most of the chip idle and
+// each wave would otherwise chain more than 8 steps of 128 K (K > 8192),
+// each split at least one step per wave (8 waves); 1 when no split pays or
+// the workspace is too small. Measured at M=1: N=1280, K=15360 10.2 against
+// 15.2 us; at K=5120 (N = 512, 1280) the reduction launch costs more than
+// the split gains (7.3 against 6.9 us).
+static int strip_splits(int M, int N, int K, size_t ws_bytes) {
+    const int wgs = N / 16, ksteps = K / 128;
+    if (ksteps <= 8 * 8) return 1;
+    int S = cu_count() / (wgs > 0 ? wgs : 1);
+    if (S > ksteps / 8) S = ksteps / 8;
+    if (S < 2) return 1;
+    if ((size_t)S * M * N * 4 > ws_bytes) return 1;
+    return S;
 }
 
 // ---- A-resident GEMM: a 32-row block of A in LDS, K split over 8 waves ----
@@ -1248,7 +1300,12 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         if (rc >= 0) return rc;
         // 3. 16-column strips (no split-K workspace, or shapes the others
         // do not stage)
-        if (M <= 16) rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream);
+        if (M <= 16) {
+            SkWorkspace &wsp = sk_ws();
+            const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
+            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream, S,
+                                                               (float *)wsp.ptr);
+        }
         else if (M <= 32) rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         else if (M <= 64) rc = launch_kp<4, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
         else rc = launch_kp<4, 1, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
@@ -1279,6 +1336,10 @@ size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
         const int S = pipe_splits((int)m, (int)n, (int)k, bn, (size_t)-1);
         const size_t tiles = (size_t)((m + kPM - 1) / kPM) * ((n + bn - 1) / bn);
         const size_t need = S > 1 ? (size_t)S * tiles * kPM * bn * 4 : 0;
+        if (need > best) best = need;
+    }
+    if (m <= 16) {  // the split 16-column strips
+        const size_t need = (size_t)strip_splits((int)m, (int)n, (int)k, (size_t)-1) * m * n * 4;
         if (need > best) best = need;
     }
     return best;
