@@ -111,7 +111,12 @@ def _host_experts(slabs, experts, E, dim, inter):
                                                     (132, 384, 4096, 2048, 8, 6),
                                                     (5, 16, 512, 256, 4, 5),
                                                     (96, 64, 5120, 2304, 6, 6),
-                                                    (33, 8, 8192, 4096, 2, 4)])
+                                                    (33, 8, 8192, 4096, 2, 4),
+                                                    # >= 192 tiles: two bands per wave; dim
+                                                    # % 256 == 128 leaves the last down unit
+                                                    # half empty
+                                                    (40, 256, 640, 384, 6, 10),
+                                                    (64, 256, 5120, 2304, 6, 6)])
 def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
     rng = np.random.default_rng(900 + m + E)
     gen = torch.Generator(device=DEV)
@@ -223,7 +228,8 @@ def test_moe_prefill_rejects_oversized_shapes():
             L.moe_prefill(f, idx, w, b, b, b, b, b, b, f, 4, dim, inter, E, k, ws)
 
 
-@pytest.mark.parametrize("m,E,dim,inter,k", [(40, 64, 1024, 512, 6), (9, 16, 512, 256, 4)])
+@pytest.mark.parametrize("m,E,dim,inter,k", [(40, 64, 1024, 512, 6), (9, 16, 512, 256, 4),
+                                             (40, 256, 640, 384, 6)])
 def test_prefill_stages_compose_to_moe_prefill(m, E, dim, inter, k):
     """emit8 -> dispatch -> grouped gate/up -> grouped down (every slot) ->
     combine through the public entry points gives the bits of ws_moe_prefill

@@ -230,6 +230,82 @@ __device__ __forceinline__ void g_compute(const Fp4Stage &st, v4f acc[NF], const
     }
 }
 
+// The same for two bands (s0, s1) against the same A fragments: each A
+// fragment is converted once for both. Per band the MFMA sequence is that of
+// g_compute (the same sums, bit for bit).
+// (NF <= 2 fragments of acc[band][fragment] are used)
+template <bool EXACT, int NF>
+__device__ __forceinline__ void g_compute2(const Fp4Stage &s0, const Fp4Stage &s1,
+                                           v4f acc[2][2], const uint8_t *a_l,
+                                           const uint8_t *as_l, int K, int ks0, int kend,
+                                           int lane) {
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        const int ks = ks0 + u;
+        if (ks >= kend) continue;  // uniform
+        const uint32_t sb0 = stage_scale(s0, u), sb1 = stage_scale(s1, u);
+        if (EXACT) {
+            // one 8-value group j of the weights and of each A fragment at a
+            // time (few registers live); per band and fragment the MFMAs run
+            // in group order, as in mfma_bf16_k128
+            const float f0 = e8m0_to_f32(sb0), f1 = e8m0_to_f32(sb1);
+            const uint32_t q0[4] = {s0.w[u].x, s0.w[u].y, s0.w[u].z, s0.w[u].w};
+            const uint32_t q1[4] = {s1.w[u].x, s1.w[u].y, s1.w[u].z, s1.w[u].w};
+            uint4 alo[NF], ahi[NF];
+            float sa[NF];
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                const int slot = i * 16 + r;
+                const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 32;
+                alo[i] = *(const uint4 *)ap;
+                ahi[i] = *(const uint4 *)(ap + 16);
+                sa[i] = e8m0_to_f32(as_l[slot * (K / 32) + ks * 4 + g]);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const v8bf b0 = __builtin_bit_cast(
+                    v8bf, pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 0),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 1),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 2),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 3)));
+                const v8bf b1 = __builtin_bit_cast(
+                    v8bf, pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 0),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 1),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 2),
+                              __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 3)));
+#pragma unroll
+                for (int i = 0; i < NF; i++) {
+                    const uint32_t wa[8] = {alo[i].x, alo[i].y, alo[i].z, alo[i].w,
+                                            ahi[i].x, ahi[i].y, ahi[i].z, ahi[i].w};
+                    const v8bf aj = __builtin_bit_cast(
+                        v8bf, pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[2 * j], sa[i], false),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[2 * j], sa[i], true),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[2 * j + 1], sa[i], false),
+                                  __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wa[2 * j + 1], sa[i], true)));
+                    acc[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, b0, acc[0][i], 0, 0, 0);
+                    acc[1][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aj, b1, acc[1][i], 0, 0, 0);
+                }
+            }
+        } else {
+            const v8i b0 = frag_from4(s0.w[u]), b1 = frag_from4(s1.w[u]);
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                const int slot = i * 16 + r;
+                const uint8_t *ap = a_l + slot * (K + 16) + ks * 128 + g * 16;
+                const v8i a = frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64));
+                const int sa = (int)as_l[slot * (K / 32) + ks * 4 + g];
+                acc[0][i] = mfma_scaled<kFmtFp8, kFmtFp4>(a, b0, acc[0][i], sa, (int)sb0);
+                acc[1][i] = mfma_scaled<kFmtFp8, kFmtFp4>(a, b1, acc[1][i], sa, (int)sb1);
+            }
+        }
+    }
+}
+
+struct Fp4Pair {
+    Fp4Stage h[2];
+};
+
 __device__ __forceinline__ int g_expert(const int32_t *tile_expert, int tile, int n_experts) {
     const int e = tile_expert[tile];
     return e < 0 ? 0 : (e >= n_experts ? n_experts - 1 : e);
@@ -248,12 +324,15 @@ struct ChunkStream {
 };
 
 // ---- grouped gate/up + SwiGLU + FP8 re-quantisation -----------------------
-// Unit = (A block, 32 intermediate columns nt). Wave w: matrix (w>>1)&1
-// (w1|w3), 16-row half w&1 of the 32 columns, K part w>>2 (k_part8 halves
-// rounded to 8-step stages). The K parts meet in LDS (gu), added in part
-// order; then a half-wave per slot row applies SwiGLU, the routing weight and
-// the FP8 1x32 quantisation (one block = the 32 columns of the unit).
-template <bool EXACT, int ROWS>
+// Unit = (A block, 32 * CB intermediate columns nt), K part w>>2 (k_part8
+// halves rounded to 8-step stages). CB == 1: wave w streams matrix (w>>1)&1
+// (w1|w3), 16-row band w&1 of the unit. CB == 2: matrix w&1, both 16-row
+// bands of 32-column block (w>>1)&1, each A fragment converted once for the
+// two (half the A conversions per column; wider units, so for many tiles).
+// The K parts meet in LDS (gu: part 0 stores, part 1 adds); then a half-wave
+// per (slot row, 32-column block) applies SwiGLU, the routing weight and the
+// FP8 1x32 quantisation (one block = 32 columns).
+template <bool EXACT, int ROWS, int CB>
 __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     const uint8_t *xq, const uint8_t *xs, const int32_t *__restrict__ order,
     const float *__restrict__ layout_w, const int32_t *__restrict__ tile_expert,
@@ -265,17 +344,19 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     extern __shared__ __align__(16) uint8_t g_lds[];
     uint8_t *a_l = g_lds;                              // [ROWS][dim + 16]
     uint8_t *as_l = g_lds + g_a_lds(ROWS, dim);        // [ROWS][dim/32] (+ padding)
-    __shared__ float gu[2][2][ROWS][kGCols + 1];
+    constexpr int UC = kGCols * CB;                   // columns per unit
+    __shared__ float gu[2][ROWS][UC + 1];             // [matrix][slot row][column]
     __shared__ float rw_l[ROWS];  // routing weight of each slot of the block (0: padding)
     __shared__ int pad_l[ROWS];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const uint64_t tab = ws_lane_exp2f_tab(lane);
     const int r = lane & 15, g = lane >> 4;
-    const int mat = (w >> 1) & 1, half = w & 1, kpart = w >> 2;
+    const int mat = CB == 2 ? (w & 1) : ((w >> 1) & 1), sub = CB == 2 ? ((w >> 1) & 1) : (w & 1);
+    const int kpart = w >> 2;
     ChunkStream cs;
     k_part8(dim / 128, kpart, 2, cs.k0, cs.k1);
     cs.nch = ((dim / 128 + kU - 1) / kU + 1) / 2;  // chunks of the longer K part
-    const int NT = inter / kGCols;
+    const int NT = inter / UC;
     const int units = *num_tiles * H * NT;
     cs.u0 = (int)((long)blockIdx.x * units / gridDim.x);
     const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
@@ -285,21 +366,26 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
     const uint8_t *wm = mat ? w3 : w1;
     const uint8_t *sm = mat ? s3 : s1;
-    auto band_of = [&](int u) {
+    // band h of the wave in unit u, and its first column within the unit
+    auto band_of = [&](int u, int h) {
         const int e = g_expert(tile_expert, u / (H * NT), n_experts);
-        return fp4_band(wm + (size_t)e * wmat, sm + (size_t)e * smat, (u % NT) * 2 + half, dim,
-                        lane);
+        return fp4_band(wm + (size_t)e * wmat, sm + (size_t)e * smat,
+                        (u % NT) * 2 * CB + sub * CB + h, dim, lane);
     };
-    auto load_q = [&](Fp4Stage &st, int q) { fp4_load(st, band_of(cs.unit(q)), cs.cb(q), cs.ce(q)); };
-    Fp4Stage st0, st1;
+    auto load_q = [&](Fp4Pair &st, int q) {
+        const int u = cs.unit(q);
+#pragma unroll
+        for (int h = 0; h < CB; h++) fp4_load(st.h[h], band_of(u, h), cs.cb(q), cs.ce(q));
+    };
+    Fp4Pair st0, st1;
     load_q(st0, 0);
     mem_order();
     load_q(st1, 1);
     mem_order();
     int cur_blk = -1;
     bool low_only = false;  // the block's slots 16.. are all padding (a 32-row block)
-    v4f acc[NF];
-    auto step = [&](Fp4Stage &st, int q) {
+    v4f acc[2][2];  // [band][16-row fragment]
+    auto step = [&](Fp4Pair &st, int q) {
         const int u = cs.unit(q), c = q % cs.nch;
         const int blk = u / NT, nt = u % NT;
         const int slot0 = (blk / H) * kTile + (blk % H) * ROWS;
@@ -326,27 +412,46 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
                 cur_blk = blk;
             }
 #pragma unroll
-            for (int i = 0; i < NF; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+            for (int h = 0; h < 2; h++) acc[h][0] = acc[h][1] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        if (low_only)  // uniform; the upper fragment's sums stay 0 (padding slots)
-            g_compute<EXACT, 1>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
-        else
-            g_compute<EXACT, NF>(st, acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        // uniform; with low_only the upper fragment's sums stay 0 (padding slots)
+        if (CB == 2) {
+            if (low_only)
+                g_compute2<EXACT, 1>(st.h[0], st.h[1], acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute2<EXACT, NF>(st.h[0], st.h[1], acc, a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        } else {
+            if (low_only)
+                g_compute<EXACT, 1>(st.h[0], acc[0], a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute<EXACT, NF>(st.h[0], acc[0], a_l, as_l, dim, cs.cb(q), cs.ce(q), lane);
+        }
         load_q(st, q + 2);
         if (c == cs.nch - 1) {  // the unit's K parts are complete: epilogue
+            // K part 0 stores, part 1 adds (the sum p0 + p1)
 #pragma unroll
-            for (int i = 0; i < NF; i++)
+            for (int kp = 0; kp < 2; kp++) {
+                if (kpart == kp) {  // uniform
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    gu[kpart][mat][i * 16 + 4 * g + v][half * 16 + r] = acc[i][v];
-            lds_barrier();
-            // a half-wave per slot row (32 values = one FP8 block)
+                    for (int h = 0; h < CB; h++)
+#pragma unroll
+                        for (int i = 0; i < NF; i++)
+#pragma unroll
+                            for (int v = 0; v < 4; v++) {
+                                float &o = gu[mat][i * 16 + 4 * g + v][(sub * CB + h) * 16 + r];
+                                o = kp == 0 ? acc[h][i][v] : o + acc[h][i][v];
+                            }
+                }
+                lds_barrier();
+            }
+            // a half-wave per (slot row, 32-column block): one FP8 block
             const int col = t & 31;
-            for (int srow = t >> 5; srow < ROWS; srow += kGThreads / 32) {
+            for (int it = t >> 5; it < CB * ROWS; it += kGThreads / 32) {
+                const int srow = it / CB, cbk = it % CB;
                 const int slot = slot0 + srow;
                 const bool pad = pad_l[srow] != 0;
-                float gv = gu[0][0][srow][col] + gu[1][0][srow][col];
-                float uv = gu[0][1][srow][col] + gu[1][1][srow][col];
+                float gv = gu[0][srow][cbk * 32 + col];
+                float uv = gu[1][srow][cbk * 32 + col];
                 if (limit > 0.0f) {
                     uv = rclamp(uv, -limit, limit);
                     gv = fminf(gv, limit);
@@ -356,8 +461,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
                 const float h = pad ? 0.0f : sg * uv * rw_l[srow];
                 uint32_t sbyte;
                 const uint32_t qb = quant_fp8_block32(h, &sbyte);
-                hq[(size_t)slot * inter + nt * kGCols + col] = (uint8_t)qb;
-                if (col == 0) hs[(size_t)slot * (inter / 32) + nt] = (uint8_t)sbyte;
+                hq[(size_t)slot * inter + nt * UC + cbk * 32 + col] = (uint8_t)qb;
+                if (col == 0) hs[(size_t)slot * (inter / 32) + nt * CB + cbk] = (uint8_t)sbyte;
             }
             lds_barrier();
         }
@@ -371,10 +476,13 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 }
 
 // ---- grouped down ---------------------------------------------------------
-// Unit = (tile, 128 output columns nt); wave w owns columns nt*128 + 16w ..
-// over the whole K = inter (chunk stream of 8-step chunks), so each output is
-// one wave's sum and is written straight from registers. f32 out[slot, dim].
-template <bool EXACT>
+// Unit = (tile, 128 * CB output columns nt); wave w owns the CB 16-column
+// bands from nt*128*CB + 16*CB*w over the whole K = inter (chunk stream of
+// 8-step chunks; with CB == 2 each A fragment is converted once for both
+// bands), so each output is one wave's sum and is written straight from
+// registers. f32 out[slot, dim]. With CB == 2 and dim % 256 == 128 the last
+// unit's upper waves have no band (clamped loads, no stores).
+template <bool EXACT, int CB>
 __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
     const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ order,
@@ -389,7 +497,7 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     cs.k0 = 0;
     cs.k1 = inter / 128;
     cs.nch = (cs.k1 + kU - 1) / kU;
-    const int NT = dim / 128;
+    const int NT = (dim + 128 * CB - 1) / (128 * CB), nbands = dim / 16;
     const int units = *num_tiles * NT;
     cs.u0 = (int)((long)blockIdx.x * units / gridDim.x);
     const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
@@ -397,13 +505,17 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     cs.total = (u1 - cs.u0) * cs.nch;
     const size_t wmat = (size_t)dim * (inter / 2);
     const size_t smat = (size_t)packed_fp4_scale_bytes(dim, inter);
-    auto band_of = [&](int u) {
+    auto band_of = [&](int u, int h) {
         const int e = g_expert(tile_expert, u / NT, n_experts);
-        return fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, (u % NT) * 8 + w, inter,
-                        lane);
+        return fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat,
+                        min((u % NT) * 8 * CB + w * CB + h, nbands - 1), inter, lane);
     };
-    auto load_q = [&](Fp4Stage &st, int q) { fp4_load(st, band_of(cs.unit(q)), cs.cb(q), cs.ce(q)); };
-    Fp4Stage s0, s1;
+    auto load_q = [&](Fp4Pair &st, int q) {
+        const int u = cs.unit(q);
+#pragma unroll
+        for (int h = 0; h < CB; h++) fp4_load(st.h[h], band_of(u, h), cs.cb(q), cs.ce(q));
+    };
+    Fp4Pair s0, s1;
     load_q(s0, 0);
     mem_order();
     load_q(s1, 1);
@@ -413,8 +525,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     // those rows are written, and a tile whose slots 16.. are all padding
     // copies and multiplies 16 rows. Without it every slot counts.
     uint32_t real = 0xFFFFFFFFu;
-    v4f acc[2];
-    auto step = [&](Fp4Stage &st, int q) {
+    v4f acc[2][2];  // [band][16-row fragment]
+    auto step = [&](Fp4Pair &st, int q) {
         const int u = cs.unit(q), c = q % cs.nch;
         const int tile = u / NT, nt = u % NT;
         const int slot0 = tile * kTile;
@@ -432,22 +544,35 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
                 lds_barrier();
                 cur_tile = tile;
             }
-            acc[0] = acc[1] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int h = 0; h < 2; h++) acc[h][0] = acc[h][1] = v4f{0.f, 0.f, 0.f, 0.f};
         }
-        if ((real >> 16) == 0)  // uniform
-            g_compute<EXACT, 1>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
-        else
-            g_compute<EXACT, 2>(st, acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        const bool lo16 = (real >> 16) == 0;  // uniform
+        if (CB == 2) {
+            if (lo16)
+                g_compute2<EXACT, 1>(st.h[0], st.h[1], acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute2<EXACT, 2>(st.h[0], st.h[1], acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        } else {
+            if (lo16)
+                g_compute<EXACT, 1>(st.h[0], acc[0], a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute<EXACT, 2>(st.h[0], acc[0], a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
+        }
         load_q(st, q + 2);
-        if (c == cs.nch - 1) {
-            const int col = nt * 128 + w * 16 + r;
+        const int b0 = nt * 8 * CB + w * CB;
+        if (c == cs.nch - 1 && b0 < nbands) {  // uniform
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int h = 0; h < CB; h++) {
+                const int col = (b0 + h) * 16 + r;
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int row = i * 16 + 4 * g + v;
-                    if ((real >> row) & 1) out[(size_t)(slot0 + row) * dim + col] = acc[i][v];
-                }
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int row = i * 16 + 4 * g + v;
+                        if ((real >> row) & 1) out[(size_t)(slot0 + row) * dim + col] = acc[h][i][v];
+                    }
+            }
         }
     };
     int q = 0;
@@ -492,6 +617,14 @@ static inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 static inline bool al4(const void *p) { return ((uintptr_t)p & 3) == 0; }
 static inline bool al8(const void *p) { return ((uintptr_t)p & 7) == 0; }
 static size_t a256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Two bands per wave (wider units, each A fragment converted once for both)
+// when the tile capacity is large; one band per wave (twice the units) for
+// few tiles, where the unit count limits the spread over the CUs. Measured
+// with 384 experts: M=132 prefill 294 -> 266 us and M=64 279 -> 270 us wide;
+// M=8 (66 tiles) 167 us narrow against 179 wide.
+constexpr int64_t kWideTiles = 192;
+static inline bool wide_units(int64_t tiles) { return tiles >= kWideTiles; }
 
 static int64_t tiles_for(int64_t routes, int64_t n_experts) {
     return (routes + kTile - 1) / kTile + (routes < n_experts ? routes : n_experts);
@@ -539,19 +672,21 @@ int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t
     // 16-row halves of each tile up to 8192
     if (dim > 8192) return WS_ERR_SHAPE;
     dim3 grid((unsigned)cu_count());
-#define WS_GLU(E, R)                                                                          \
-    hipLaunchKernelGGL((grouped_glu_quant_kernel<E, R>), grid, dim3(kGThreads),              \
+#define WS_GLU(E, R, CB)                                                                      \
+    hipLaunchKernelGGL((grouped_glu_quant_kernel<E, R, CB>), grid, dim3(kGThreads),          \
                        g_tile_lds(R, (int)dim), stream, xq, xs, order, layout_w, tile_expert,  \
                        num_tiles, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter,              \
                        (int)n_experts, (int)top_k, swiglu_limit)
+#define WS_GLU_CB(E, R)                       \
+    if (wide_units(tiles)) WS_GLU(E, R, 2);   \
+    else WS_GLU(E, R, 1);
     const bool exact = math_mode() == WS_MATH_EXACT;
     if (dim <= 4096) {
-        if (exact) WS_GLU(true, 32);
-        else WS_GLU(false, 32);
+        if (exact) { WS_GLU_CB(true, 32) } else { WS_GLU_CB(false, 32) }
     } else {
-        if (exact) WS_GLU(true, 16);
-        else WS_GLU(false, 16);
+        if (exact) { WS_GLU_CB(true, 16) } else { WS_GLU_CB(false, 16) }
     }
+#undef WS_GLU_CB
 #undef WS_GLU
     return launch_status();
 }
@@ -579,17 +714,19 @@ static int grouped_down_launch(const uint8_t *hq, const uint8_t *hs, const int32
                                const int32_t *num_tiles, const int32_t *order, const uint8_t *w2,
                                const uint8_t *s2, float *out, int64_t dim, int64_t inter,
                                int64_t n_experts, int64_t tiles, ws_stream_t stream) {
-    (void)tiles;
     const size_t lds = g_tile_lds(kTile, (int)inter);
     dim3 grid((unsigned)cu_count());
-    if (math_mode() == WS_MATH_EXACT)
-        hipLaunchKernelGGL(grouped_down_kernel<true>, grid, dim3(kGThreads), lds, stream, hq, hs,
-                           tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,
-                           (int)n_experts);
-    else
-        hipLaunchKernelGGL(grouped_down_kernel<false>, grid, dim3(kGThreads), lds, stream, hq, hs,
-                           tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,
-                           (int)n_experts);
+#define WS_DOWN(E, CB)                                                                         \
+    hipLaunchKernelGGL((grouped_down_kernel<E, CB>), grid, dim3(kGThreads), lds, stream, hq, hs, \
+                       tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,        \
+                       (int)n_experts)
+    const bool wide = wide_units(tiles);
+    if (math_mode() == WS_MATH_EXACT) {
+        if (wide) WS_DOWN(true, 2); else WS_DOWN(true, 1);
+    } else {
+        if (wide) WS_DOWN(false, 2); else WS_DOWN(false, 1);
+    }
+#undef WS_DOWN
     return launch_status();
 }
 
