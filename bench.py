@@ -379,7 +379,7 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
 
 
 def bench_model_shapes(L, torch, dev, reps=40, Ms=(1, 128)):
-    """the engine's other FP8 projections at their real (N, K)
+    """The engine's other FP8 projections at their real (N, K)
     (weightstream-gpu engine.rs:3388-3398), UE8M0 scales, exact math, bf16
     out, weights rotated over > 400 MB of copies (cold)."""
     shapes = {"q_a": (1280, 5120), "q_b": (8192, 1280), "wkv": (512, 5120),
@@ -423,7 +423,8 @@ def bench_prefill(L, torch, dev, packed, reps, m=132, zipf_scale=1.0):
     """Config 4: grouped prefill of m tokens through the same 384-expert layer,
     router logits skewed by Zipf(1.1) popularity (zipf_scale * log p_e added
     to N(0,1) logits, popularity order a seeded permutation; at scale 1 about
-    45 experts are touched, at 0.25 about 250, the regime the SURVEY expects).
+    45 experts are touched, at 0.25 about 250: the 250-330 touched experts
+    expected of real routing).
     Timed: top-k routing + the whole grouped MoE (quantise, dispatch, grouped
     gate/up, grouped down, combine). Algorithmic bytes: the touched experts'
     weights once."""
