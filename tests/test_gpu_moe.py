@@ -233,19 +233,35 @@ def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
     assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
 
 
-@pytest.mark.parametrize("E,dim,inter,k,score", [(384, 4096, 2048, 8, 1), (384, 5120, 2304, 6, 2),
-                                                 (64, 1024, 512, 4, 1), (100, 2048, 768, 6, 2)])
-def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score):
+@pytest.mark.parametrize("E,dim,inter,k,score,kind", [(384, 4096, 2048, 8, 1, "normal"),
+                                                      (384, 5120, 2304, 6, 2, "normal"),
+                                                      (64, 1024, 512, 4, 1, "normal"),
+                                                      (100, 2048, 768, 6, 2, "normal"),
+                                                      (384, 1024, 512, 8, 1, "ties_cut"),
+                                                      (384, 1024, 512, 8, 2, "ties_low"),
+                                                      (64, 1024, 512, 4, 1, "ties_cut")])
+def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score, kind):
     """The routed gate/up entry point gives ws_moe_topk's picks and weights
-    and ws_expert_glu_quant_x's hq / hs on them, bit for bit."""
+    and ws_expert_glu_quant_x's hq / hs on them, bit for bit. `ties_cut`:
+    three distinct logits and no bias, so equal scores straddle the top-k
+    cut (ties broken by the lower expert id); `ties_low`: distinct top
+    scores above many equal low ones."""
     rng = np.random.default_rng(760 + E + dim)
     gen = torch.Generator(device=DEV)
     gen.manual_seed(760 + dim)
     P = _packed(_slabs(gen, E, dim, inter), E, dim, inter)
-    logits = dev(rng.standard_normal(E).astype(np.float32))
-    bias = dev((rng.standard_normal(E) * 0.1).astype(np.float32))
+    lg = rng.standard_normal(E).astype(np.float32)
+    bs = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    if kind == "ties_cut":
+        lg = (rng.integers(0, 3, E) * 0.5).astype(np.float32)
+        bs[:] = 0.0
+    elif kind == "ties_low":
+        bs[:] = 0.0
+        lg[np.argsort(lg)[: E // 2]] = -3.0
+    logits, bias = dev(lg), dev(bs)
     x = dev(rng.standard_normal(dim).astype(np.float32))
-    announce("expert_glu_quant_route E=%d dim=%d inter=%d k=%d score=%d" % (E, dim, inter, k, score))
+    announce("expert_glu_quant_route E=%d dim=%d inter=%d k=%d score=%d %s"
+             % (E, dim, inter, k, score, kind))
     idx1 = torch.empty(k, dtype=torch.int32, device=DEV)
     w1_ = torch.empty(k, dtype=torch.float32, device=DEV)
     L.moe_topk(logits, bias, None, idx1, w1_, 1, E, k, score, 1.0, True, 1.0)
