@@ -100,8 +100,9 @@ int ws_weight_quant_fp8(const float *w, uint8_t *q, uint8_t *s, int64_t rows, in
  * ------------------------------------------------------------------- */
 /* Split-K workspace of the FP8/FP4 GEMMs (no counterpart in the reference,
  * whose kernels keep the whole K of a tile in one block). Once a workspace is
- * set for the current device, GEMMs with M > 16 split K across workgroups
- * and a second kernel adds the f32 partials in split order (deterministic);
+ * set for the current device, GEMMs with M > 64 (and M <= 16 with few
+ * column strips and K > 8192) split K across workgroups and a second kernel
+ * adds the f32 partials in split order (deterministic);
  * without one they use the single-pass kernels. The workspace is shared by
  * every GEMM call on the device: calls that may run concurrently (different
  * streams) need it not to be set, or must be serialised.
