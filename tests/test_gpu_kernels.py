@@ -269,3 +269,30 @@ def test_split_k_is_deterministic_and_reusable():
         torch.cuda.synchronize()
         L.set_gemm_workspace(None)
     del rng
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1280, 15360), (6, 512, 12288)])
+def test_long_k_strip_split_matches_single_pass(m, n, k):
+    """M <= 16 with few column strips and K > 8192 splits K over workgroups
+    when a workspace is set: the same sums up to f32 reassociation (within
+    the GEMM tolerance of the single-pass result), and repeated calls give
+    the same bits."""
+    aq, as_, wq, ws_ = _quantised_case(np.random.default_rng(4100 + m + n), m, n, k, False)
+    announce("strip split m=%d n=%d k=%d" % (m, n, k))
+    args = [dev(aq), dev(as_), dev(wq), dev(ws_)]
+    single = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm(*args, single, m, n, k)
+    ws = torch.empty(max(L.gemm_workspace_size(m, n, k), 256), dtype=torch.uint8, device=DEV)
+    L.set_gemm_workspace(ws)
+    try:
+        outs = []
+        for _ in range(2):
+            out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+            L.fp8_gemm(*args, out, m, n, k)
+            outs.append(host(out))
+    finally:
+        torch.cuda.synchronize()
+        L.set_gemm_workspace(None)
+    assert L.gemm_workspace_size(m, n, k) > 0
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert_close(outs[0], host(single), GEMM_TOL, "strip split m=%d n=%d k=%d" % (m, n, k))
