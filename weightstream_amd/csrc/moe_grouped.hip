@@ -35,7 +35,22 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     float *__restrict__ layout_w, int32_t *__restrict__ route_pos,
     int32_t *__restrict__ tile_expert, int32_t *__restrict__ count_out,
     int32_t *__restrict__ offset_out, int32_t *__restrict__ psum_out,
-    int32_t *__restrict__ num_tiles_out, int routes, int tiles, int n_experts) {
+    int32_t *__restrict__ num_tiles_out, int routes, int tiles, int n_experts,
+    const float *__restrict__ xf, uint8_t *__restrict__ xq, uint8_t *__restrict__ xs, int64_t nx) {
+    if (blockIdx.x > 0) {
+        // workgroups 1..: the tokens' FP8 1x32 quantisation (the act_quant
+        // rule, a 32-lane half-wave per block; nx % 32 == 0), independent of
+        // the dispatch and run beside it in the same launch
+        const int64_t i = (int64_t)(blockIdx.x - 1) * kDispThreads + threadIdx.x;
+        const bool live = i < nx;
+        uint32_t sb;
+        const uint32_t qb = quant_fp8_block32(live ? xf[i] : 0.0f, &sb);
+        if (live) {
+            xq[i] = (uint8_t)qb;
+            if ((threadIdx.x & 31) == 0) xs[i / 32] = (uint8_t)sb;
+        }
+        return;
+    }
     __shared__ int32_t base[kMaxExpertsG];
     __shared__ int32_t wcnt[kDispThreads / 64][kMaxExpertsG];
     __shared__ int32_t scan[kMaxExpertsG];
@@ -636,6 +651,22 @@ using namespace ws;
 
 extern "C" {
 
+// The dispatch on workgroup 0; with nx > 0 workgroups 1.. quantise the nx
+// token values xf into xq / xs (ws_emit8) in the same launch.
+static int dispatch_launch(const int32_t *topk_idx, const float *topk_w, int32_t *order,
+                           float *layout_w, int32_t *route_pos, int32_t *tile_expert,
+                           int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
+                           int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
+                           int64_t n_experts, const float *xf, uint8_t *xq, uint8_t *xs,
+                           int64_t nx, ws_stream_t stream) {
+    const int64_t qblocks = (nx + kDispThreads - 1) / kDispThreads;
+    hipLaunchKernelGGL(dispatch_kernel, dim3((unsigned)(1 + qblocks)), dim3(kDispThreads), 0,
+                       stream, topk_idx, topk_w, order, layout_w, route_pos, tile_expert,
+                       expert_count, expert_offset, expert_psum, num_tiles, (int)(rows * top_k),
+                       (int)tiles, (int)n_experts, xf, xq, xs, nx);
+    return launch_status();
+}
+
 int ws_moe_dispatch(const int32_t *topk_idx, const float *topk_w, int32_t *order,
                     float *layout_w, int32_t *route_pos, int32_t *tile_expert,
                     int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
@@ -647,10 +678,9 @@ int ws_moe_dispatch(const int32_t *topk_idx, const float *topk_w, int32_t *order
     if (rows <= 0 || top_k <= 0 || tiles <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
     if (n_experts > kMaxExpertsG || rows * top_k > (1 << 26) || tiles > (1 << 24))
         return WS_ERR_SHAPE;
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, stream, topk_idx, topk_w,
-                       order, layout_w, route_pos, tile_expert, expert_count, expert_offset,
-                       expert_psum, num_tiles, (int)(rows * top_k), (int)tiles, (int)n_experts);
-    return launch_status();
+    return dispatch_launch(topk_idx, topk_w, order, layout_w, route_pos, tile_expert, expert_count,
+                           expert_offset, expert_psum, num_tiles, rows, top_k, tiles, n_experts,
+                           nullptr, nullptr, nullptr, 0, stream);
 }
 
 int ws_moe_grouped_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *order,
@@ -786,10 +816,11 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
     uint8_t *hq = take(slots * inter);
     uint8_t *hs = take(slots * (inter / 32));
     float *down = (float *)take(slots * dim * 4);
-    int rc = ws_emit8(x, xq, xs, rows * dim, stream);
-    if (rc) return rc;
-    rc = ws_moe_dispatch(topk_idx, topk_w, order, layout_w, route_pos, tile_expert, cnt, off, psum,
-                         ntiles, rows, top_k, tiles, n_experts, stream);
+    // the dispatch and the tokens' quantisation in one launch
+    if (n_experts > kMaxExpertsG || routes > (1 << 26) || tiles > (1 << 24)) return WS_ERR_SHAPE;
+    int rc = dispatch_launch(topk_idx, topk_w, order, layout_w, route_pos, tile_expert, cnt, off,
+                             psum, ntiles, rows, top_k, tiles, n_experts, x, xq, xs, rows * dim,
+                             stream);
     if (rc) return rc;
     rc = ws_moe_grouped_glu_quant(xq, xs, order, layout_w, tile_expert, ntiles, w1, s1, w3, s3, hq,
                                   hs, dim, inter, n_experts, top_k, tiles, swiglu_limit, stream);
