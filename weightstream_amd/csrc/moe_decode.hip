@@ -327,16 +327,26 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     // the slot's expert: with the routing in the kernel, the top-k rounds
     // up to this slot's run before the weight loads go out and the rest
     // while they are in flight (the same rounds in the same order)
+    // (wave 0 alone runs the rounds, so that they do not share its SIMD with
+    // another wave's copy; the picks reach the other waves through LDS)
     int e;
     float rw;
     WavePicks wp;
     WaveTopk<(CPL > 0 ? CPL : 1)> tk;
+    __shared__ int e_l;
+    __shared__ int pk_l[kMaxTopkDec];
+    __shared__ float pw_l[kMaxTopkDec];
     if constexpr (CPL > 0) {
-        float sc[CPL];
-        wave_scores_of<CPL>(rin.v, ra.score_func, ra.gate_temp, lane, sc);
-        tk.init(sc, rin.b, n_experts, lane);
-        e = 0;
-        for (int k = 0; k <= slot; k++) e = tk.round(k, lane);
+        if (w == 0) {
+            float sc[CPL];
+            wave_scores_of<CPL>(rin.v, ra.score_func, ra.gate_temp, lane, sc);
+            tk.init(sc, rin.b, n_experts, lane);
+            e = 0;
+            for (int k = 0; k <= slot; k++) e = tk.round(k, lane);
+            if (lane == 0) e_l = e;
+        }
+        lds_barrier();
+        e = e_l;
     } else {
         e = idx[slot];
         rw = topk_w[slot];
@@ -359,20 +369,28 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
 
     // the routing weight and the picks' ranks
     if constexpr (CPL > 0) {
-        for (int k = slot + 1; k < top_k; k++) tk.round(k, lane);
-        const int pk = tk.pick;
-        const float pw = tk.weight(top_k, ra.norm, ra.route_scale);
-        rw = readlane_f(pw, slot);
-        wp = wave_picks_of(pk, top_k, n_experts, lane);
-        if (blockIdx.x == 0 && slot == 0 && w == 0 && lane < top_k) {
-            ra.idx_out[lane] = pk;
-            ra.w_out[lane] = pw;
+        if (w == 0) {
+            for (int k = slot + 1; k < top_k; k++) tk.round(k, lane);
+            const int pk = tk.pick;
+            const float pw = tk.weight(top_k, ra.norm, ra.route_scale);
+            if (lane < top_k) {
+                pk_l[lane] = pk;
+                pw_l[lane] = pw;
+                if (blockIdx.x == 0 && slot == 0) {
+                    ra.idx_out[lane] = pk;
+                    ra.w_out[lane] = pw;
+                }
+            }
         }
     }
 
     if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
     else share_store_fp8<EXACT>(tr.b, tc0, tc1, lane, x_l, xq_l, xs_l);
     lds_barrier();
+    if constexpr (CPL > 0) {
+        rw = pw_l[slot];
+        wp = wave_picks_of(lane < top_k ? pk_l[lane] : 0, top_k, n_experts, lane);
+    }
 
     {
         v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1);
