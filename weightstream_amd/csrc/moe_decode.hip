@@ -270,9 +270,10 @@ __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, i
     }
 }
 
-// Routing computed inside the gate/up kernel (moe_select fused in): every
-// wave runs wave_scores + wave_select on the token's logits, and workgroup
-// (0, 0) publishes the picks for the down kernel and the caller.
+// Routing computed inside the gate/up kernel (moe_select fused in): wave 0
+// of every workgroup scores the token's logits and runs the top-k rounds
+// (WaveTopk, the rounds of wave_select), and workgroup (0, 0) publishes the
+// picks for the down kernel and the caller.
 struct RouteArgs {
     const float *logits, *bias;
     int score_func;
