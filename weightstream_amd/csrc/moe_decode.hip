@@ -338,9 +338,21 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     __shared__ int pk_l[kMaxTopkDec];
     __shared__ float pw_l[kMaxTopkDec];
     if constexpr (CPL > 0) {
+        // the scores column by column over the waves (expert lane + 64 c on
+        // wave c % 8), through LDS to wave 0
+        __shared__ float sc_l[CPL][64];
+        for (int c = w; c < CPL; c += kGluStreamWaves) {
+            float v[1] = {0.0f}, o[1];
+#pragma unroll
+            for (int j = 0; j < CPL; j++) v[0] = j == c ? rin.v[j] : v[0];  // no indexed load
+            wave_scores_of<1>(v, ra.score_func, ra.gate_temp, lane, o);
+            sc_l[c][lane] = o[0];
+        }
+        lds_barrier();
         if (w == 0) {
             float sc[CPL];
-            wave_scores_of<CPL>(rin.v, ra.score_func, ra.gate_temp, lane, sc);
+#pragma unroll
+            for (int c = 0; c < CPL; c++) sc[c] = sc_l[c][lane];
             tk.init(sc, rin.b, n_experts, lane);
             e = 0;
             for (int k = 0; k <= slot; k++) e = tk.round(k, lane);
