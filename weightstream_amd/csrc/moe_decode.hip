@@ -270,10 +270,11 @@ __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, i
     }
 }
 
-// Routing computed inside the gate/up kernel (moe_select fused in): wave 0
-// of every workgroup scores the token's logits and runs the top-k rounds
-// (WaveTopk, the rounds of wave_select), and workgroup (0, 0) publishes the
-// picks for the down kernel and the caller.
+// Routing computed inside the gate/up kernel (moe_select fused in): the
+// waves of every workgroup score the token's logits (a column of 64 experts
+// each), wave 0 runs the top-k rounds (WaveTopk, the rounds of wave_select),
+// and workgroup (0, 0) publishes the picks for the down kernel and the
+// caller.
 struct RouteArgs {
     const float *logits, *bias;
     int score_func;
@@ -329,7 +330,8 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     // up to this slot's run before the weight loads go out and the rest
     // while they are in flight (the same rounds in the same order)
     // (wave 0 alone runs the rounds, so that they do not share its SIMD with
-    // another wave's copy; the picks reach the other waves through LDS)
+    // another wave's copy; the scores come to it and the picks go to the
+    // other waves through LDS)
     int e;
     float rw;
     WavePicks wp;
