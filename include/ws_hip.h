@@ -65,6 +65,12 @@ int ws_get_math_mode(void);
 /* Device ws_expf over the 32-bit patterns [lo, lo+n): out[i] = bits(expf(x)).
  * Test hook for the exhaustive host/device expf agreement check. */
 int ws_expf_probe(uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);
+/* Device math over the 32-bit patterns [lo, lo+n): fn 0 out[i] =
+ * bits(ws_logf(x)), fn 1 bits of the sqrtsoftplus score sqrt(softplus(x))
+ * (num.rs:82-88, moe.rs:38-42). Test hook for the exhaustive host/device
+ * agreement checks; 0x7fbadbad marks an input where the routing kernels'
+ * wave variant disagrees. */
+int ws_math_probe(int fn, uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);
 
 /* ---------------------------------------------------------------------
  * Activation quantisation (weightstream-cuda/kernels/actquant.cu).

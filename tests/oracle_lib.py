@@ -320,4 +320,10 @@ def expfcheck():
         _expf_lib.glibc_expf_digest.argtypes = [C.c_uint64, C.c_uint64]
         _expf_lib.glibc_expf_bits.restype = None
         _expf_lib.glibc_expf_bits.argtypes = [C.c_uint32, C.c_uint32, C.c_void_p]
+        _expf_lib.ws_math_mismatches.restype = C.c_uint64
+        _expf_lib.ws_math_mismatches.argtypes = [C.c_int, C.c_uint64, C.c_uint64]
+        _expf_lib.glibc_math_digest.restype = C.c_uint64
+        _expf_lib.glibc_math_digest.argtypes = [C.c_int, C.c_uint64, C.c_uint64]
+        _expf_lib.glibc_math_bits.restype = None
+        _expf_lib.glibc_math_bits.argtypes = [C.c_int, C.c_uint32, C.c_uint32, C.c_void_p]
     return _expf_lib

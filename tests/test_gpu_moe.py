@@ -233,16 +233,22 @@ def test_moe_decode_route_matches_topk_then_decode(E, dim, inter, k, score):
     assert np.array_equal(host(y1).view(np.uint32), host(y2).view(np.uint32))
 
 
-@pytest.mark.parametrize("E,dim,inter,k,score,kind", [(384, 4096, 2048, 8, 1, "normal"),
-                                                      (384, 5120, 2304, 6, 2, "normal"),
-                                                      (64, 1024, 512, 4, 1, "normal"),
-                                                      (100, 2048, 768, 6, 2, "normal"),
-                                                      (384, 1024, 512, 8, 1, "ties_cut"),
-                                                      (384, 1024, 512, 8, 2, "ties_low"),
-                                                      (64, 1024, 512, 4, 1, "ties_cut")])
-def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score, kind):
+@pytest.mark.parametrize("E,dim,inter,k,score,kind,temp", [(384, 4096, 2048, 8, 1, "normal", 1.0),
+                                                           (384, 5120, 2304, 6, 2, "normal", 1.0),
+                                                           (64, 1024, 512, 4, 1, "normal", 1.0),
+                                                           (100, 2048, 768, 6, 2, "normal", 1.0),
+                                                           (384, 1024, 512, 8, 1, "ties_cut", 1.0),
+                                                           (384, 1024, 512, 8, 2, "ties_low", 1.0),
+                                                           (64, 1024, 512, 4, 1, "ties_cut", 1.0),
+                                                           (512, 1024, 256, 8, 1, "normal", 1.7),
+                                                           (1024, 1024, 256, 16, 2, "normal", 0.6),
+                                                           (1024, 1024, 256, 8, 1, "ties_cut", 1.3)])
+def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score, kind, temp):
     """The routed gate/up entry point gives ws_moe_topk's picks and weights
-    and ws_expert_glu_quant_x's hq / hs on them, bit for bit. `ties_cut`:
+    (and the oracle's) and ws_expert_glu_quant_x's hq / hs on them, bit for
+    bit. E = 512 and 1024 run 8 and 16 expert columns per lane (two columns
+    per wave in the in-kernel scoring at E = 1024); temp != 1 divides the
+    logits by gate_temp first. `ties_cut`:
     three distinct logits and no bias, so equal scores straddle the top-k
     cut (ties broken by the lower expert id); `ties_low`: distinct top
     scores above many equal low ones."""
@@ -264,7 +270,10 @@ def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score, k
              % (E, dim, inter, k, score, kind))
     idx1 = torch.empty(k, dtype=torch.int32, device=DEV)
     w1_ = torch.empty(k, dtype=torch.float32, device=DEV)
-    L.moe_topk(logits, bias, None, idx1, w1_, 1, E, k, score, 1.0, True, 1.0)
+    L.moe_topk(logits, bias, None, idx1, w1_, 1, E, k, score, temp, True, 1.0)
+    ri, rw = O.route(O.score(lg, score, temp), bs, k)
+    assert np.array_equal(host(idx1), ri)
+    assert np.array_equal(host(w1_).view(np.uint32), rw.view(np.uint32))
     hq1 = torch.zeros((k, inter), dtype=torch.uint8, device=DEV)
     hs1 = torch.zeros((k, inter // 32), dtype=torch.uint8, device=DEV)
     L.expert_glu_quant_x(x, idx1, w1_, P[0], P[1], P[2], P[3], hq1, hs1, inter, dim, E, k)
@@ -272,7 +281,7 @@ def test_expert_glu_quant_route_matches_topk_then_glu(E, dim, inter, k, score, k
     w2_ = torch.zeros(k, dtype=torch.float32, device=DEV)
     hq2 = torch.zeros((k, inter), dtype=torch.uint8, device=DEV)
     hs2 = torch.zeros((k, inter // 32), dtype=torch.uint8, device=DEV)
-    L.expert_glu_quant_route(logits, bias, score, 1.0, 1, 1.0, x, P[0], P[1], P[2], P[3], hq2, hs2,
+    L.expert_glu_quant_route(logits, bias, score, temp, 1, 1.0, x, P[0], P[1], P[2], P[3], hq2, hs2,
                              idx2, w2_, dim, inter, E, k)
     assert torch.equal(idx1, idx2)
     assert np.array_equal(host(w1_).view(np.uint32), host(w2_).view(np.uint32))

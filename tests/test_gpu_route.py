@@ -1,7 +1,7 @@
-"""GPU parity of MoE routing (weightstream-ref moe.rs:20-69): device expf,
-gate logits, scores, top-k selection and weights are bit-exact with the C
-oracle for sigmoid and softmax; sqrtsoftplus picks the same experts with
-weights within a few ulp (device logf is not glibc's)."""
+"""GPU parity of MoE routing (weightstream-ref moe.rs:20-69): device expf and
+logf, gate logits, scores, top-k selection and weights are bit-exact with the
+C oracle for sigmoid, softmax and sqrtsoftplus, ties and near-ties at the
+top-k cut included."""
 import numpy as np
 import pytest
 import torch
@@ -100,7 +100,7 @@ def _rows_with_ties(rng, m, E, score_func):
     return logits, bias
 
 
-@pytest.mark.parametrize("score_func", [O.SCORE_SIGMOID, O.SCORE_SOFTMAX])
+@pytest.mark.parametrize("score_func", [O.SCORE_SIGMOID, O.SCORE_SOFTMAX, O.SCORE_SQRTSOFTPLUS])
 @pytest.mark.parametrize("E,k", [(384, 8), (256, 6), (64, 1), (1000, 16)])
 def test_topk_bit_exact(score_func, E, k):
     rng = np.random.default_rng(300 + E + k + score_func)
@@ -123,26 +123,84 @@ def test_topk_bit_exact(score_func, E, k):
         assert np.array_equal(gw[r].view(np.uint32), rw.view(np.uint32))
 
 
-def test_topk_sqrtsoftplus_same_experts():
-    rng = np.random.default_rng(400)
-    m, E, k = 64, 384, 6
+def _near_tied_rows(rng, m, E, k, score_func):
+    """Rows whose top-k cut falls between score+bias values 0 and 1 ulp apart
+    (and 2 ulp, and ties across several experts), set through the bias from
+    the oracle's scores so that the tie is exact in f32."""
     logits = rng.standard_normal((m, E)).astype(np.float32)
-    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
-    announce("moe_topk sqrtsoftplus")
-    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
-    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
-    sc = torch.empty((m, E), dtype=torch.float32, device=DEV)
-    L.moe_topk(dev(logits), dev(bias), sc, idx, w, m, E, k, O.SCORE_SQRTSOFTPLUS, 1.0, True, 1.5)
-    gi, gw, gs = host(idx), host(w), host(sc)
+    bias = np.zeros((m, E), np.float32)
     for r in range(m):
-        s = O.score(logits[r], O.SCORE_SQRTSOFTPLUS)
-        ulp = np.abs(gs[r].view(np.int32) - s.view(np.int32))
-        assert ulp.max() <= 2
-        ri, rw = O.route(s, bias, k, True, 1.5)
-        b = np.sort(s + bias)[::-1]
-        if b[k - 1] - b[k] > 1e-5:                   # no near-tie at the cut
-            assert np.array_equal(np.sort(gi[r]), np.sort(ri))
-            np.testing.assert_allclose(gw[r], rw, rtol=1e-6)
+        s = O.score(logits[r], score_func)
+        order = np.argsort(-s, kind="stable")
+        a, b = order[k - 1], order[k]           # last pick, first non-pick
+        target = np.float32(s[a])
+        gap = r % 4                              # 0: tie, 1-2: ulps apart, 3: b above
+        want = target
+        for _ in range(gap if gap < 3 else 1):
+            want = np.nextafter(want, np.float32(-np.inf) if gap < 3 else np.float32(np.inf))
+        bb = np.float32(want - s[b])
+        # adjust so that s[b] + bb lands exactly on want in f32
+        for _ in range(8):
+            got = np.float32(s[b] + bb)
+            if got == want:
+                break
+            bb = np.nextafter(bb, np.float32(np.inf) if got < want else np.float32(-np.inf))
+        bias[r, b] = bb
+    return logits, bias
+
+
+@pytest.mark.parametrize("score_func", [O.SCORE_SQRTSOFTPLUS, O.SCORE_SIGMOID])
+@pytest.mark.parametrize("E,k", [(384, 6), (384, 8), (1000, 16)])
+def test_topk_near_ties_at_the_cut_bit_exact(score_func, E, k):
+    """ws_moe_topk picks and weights equal the oracle's bit for bit when the
+    k-th and (k+1)-th score+bias are tied or 1-2 ulp apart (the bias is per
+    row here, so each row runs as its own one-token call)."""
+    rng = np.random.default_rng(400 + E + k + score_func)
+    m = 16
+    logits, bias = _near_tied_rows(rng, m, E, k, score_func)
+    announce("moe_topk near ties E=%d k=%d f=%d" % (E, k, score_func))
+    for r in range(m):
+        idx = torch.empty(k, dtype=torch.int32, device=DEV)
+        w = torch.empty(k, dtype=torch.float32, device=DEV)
+        sc = torch.empty(E, dtype=torch.float32, device=DEV)
+        L.moe_topk(dev(logits[r]), dev(bias[r]), sc, idx, w, 1, E, k, score_func, 1.0, True, 1.5)
+        s = O.score(logits[r], score_func)
+        assert np.array_equal(host(sc).view(np.uint32), s.view(np.uint32))
+        ri, rw = O.route(s, bias[r], k, True, 1.5)
+        assert np.array_equal(host(idx), ri), (r, host(idx), ri)
+        assert np.array_equal(host(w).view(np.uint32), rw.view(np.uint32))
+
+
+def test_device_logf_and_sqrtsoftplus_equal_glibc_on_every_input():
+    """All 2^32 inputs: the digests of the device ws_logf and of the
+    sqrtsoftplus score (score_fn and the routing kernels' wave variant) equal
+    the host glibc digests; 2^24 inputs are also compared value by value."""
+    lib = L._lib.load()
+    chunk = 1 << 28
+    out = torch.empty(chunk, dtype=torch.int32, device=DEV)
+    stream = torch.cuda.current_stream().cuda_stream
+    for fn in (0, 1):
+        total = 0
+        for c in range(16):
+            lo = c * chunk
+            announce("math probe fn %d chunk %d" % (fn, c))
+            L._lib.check("ws_math_probe", lib.ws_math_probe(fn, lo, chunk, out.data_ptr(), stream))
+            assert int((out == 0x7FBADBAD).sum().item()) == 0
+            r = out.to(torch.int64) & 0xFFFFFFFF
+            nan = ((r & 0x7F800000) == 0x7F800000) & ((r & 0x7FFFFF) != 0)
+            r = torch.where(nan, torch.full_like(r, 0x7FC00000), r)
+            u = torch.arange(lo, lo + chunk, dtype=torch.int64, device=DEV)
+            mixed = (r ^ ((u * 0x9E3779B1) & 0xFFFFFFFF)) * (2 * u + 1)
+            total = (total + int(mixed.sum().item())) & ((1 << 64) - 1)
+        assert total == O.expfcheck().glibc_math_digest(fn, 0, 1 << 32), fn
+        lo, n = 0x3E000000 if fn == 0 else 0xC0000000, 1 << 24
+        L._lib.check("ws_math_probe", lib.ws_math_probe(fn, lo, n, out.data_ptr(), stream))
+        got = host(out[:n]).view(np.uint32)
+        ref = np.empty(n, np.uint32)
+        O.expfcheck().glibc_math_bits(fn, lo, n, ref.ctypes.data)
+        nan = (got & 0x7F800000 == 0x7F800000) & (got & 0x7FFFFF != 0)
+        got = np.where(nan, np.uint32(0x7FC00000), got)
+        assert np.array_equal(got, ref), fn
 
 
 def test_reference_gate_select_route_contract():
@@ -172,7 +230,7 @@ def test_reference_gate_select_route_contract():
     assert np.array_equal(host(w2).view(np.uint32), rw.view(np.uint32))
     wdense = (wb.astype(np.uint32) << 16).view(np.float32)
     ref_s = O.score(O.gemv_f32(wdense, x), O.SCORE_SQRTSOFTPLUS)
-    assert np.abs(s.view(np.int32) - ref_s.view(np.int32)).max() <= 2
+    assert np.array_equal(s.view(np.uint32), ref_s.view(np.uint32))
 
 
 def test_swiglu_bit_exact():

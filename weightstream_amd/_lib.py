@@ -45,6 +45,7 @@ SIGNATURES = {
     "ws_built_with_hip": (_i, []),
     "ws_error_string": (C.c_char_p, [_i]),
     "ws_expf_probe": (_i, [_u32, _u32, _p, _p]),
+    "ws_math_probe": (_i, [_i, _u32, _u32, _p, _p]),
     "ws_set_math_mode": (_i, [_i]),
     "ws_get_math_mode": (_i, []),
     "ws_snap8": (_i, [_p, _i64, _p]),

@@ -465,6 +465,26 @@ __global__ __launch_bounds__(256) void score_kernel(float *__restrict__ v, int64
     if (i < n) v[i] = score_fn(v[i], score_func, 1.0f);
 }
 
+// Device math over the 32-bit patterns lo .. lo+n-1 (exhaustive host/device
+// agreement checks): fn 0 logf, fn 1 the sqrtsoftplus score of score_fn.
+// Each also evaluates the wave-lane variant the top-k kernels use
+// (wave_scores_of) and reports a difference as 0x7fbadbad.
+__global__ __launch_bounds__(256) void math_probe_kernel(int fn, uint32_t lo, uint32_t n,
+                                                         uint32_t *out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    const float x = __uint_as_float(lo + min(i, n - 1));
+    uint32_t a, b;
+    if (fn == 0) {
+        a = b = __float_as_uint(ws_logf(x));
+    } else {
+        a = __float_as_uint(score_fn(x, WS_SCORE_SQRTSOFTPLUS, 1.0f));
+        float v[1] = {x}, o[1];
+        wave_scores_of<1>(v, WS_SCORE_SQRTSOFTPLUS, 1.0f, threadIdx.x & 63, o);
+        b = __float_as_uint(o[0]);
+    }
+    if (i < n) out[i] = a == b ? a : 0x7fbadbadu;
+}
+
 static int gate_logits_launch(const float *x, const void *gw, int bf16, float *logits, int64_t m,
                               int64_t dim, int64_t n_experts, hipStream_t stream) {
     if (!x || !gw || !logits) return WS_ERR_INVALID_ARG;
@@ -516,6 +536,13 @@ static int topk_launch(const float *logits, const float *bias, float *scores_out
 using namespace ws;
 
 extern "C" {
+
+int ws_math_probe(int fn, uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream) {
+    if (!out || n == 0 || fn < 0 || fn > 1) return WS_ERR_INVALID_ARG;
+    hipLaunchKernelGGL(math_probe_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, fn, lo, n,
+                       out);
+    return launch_status();
+}
 
 int ws_moe_gate_logits(const float *x, const void *gate_w, int w_bf16, float *logits, int64_t m,
                        int64_t dim, int64_t n_experts, ws_stream_t stream) {

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include "ws_expf.h"
+#include "ws_logf.h"
 
 namespace ws {
 

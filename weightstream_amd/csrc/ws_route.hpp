@@ -14,8 +14,7 @@ __device__ __forceinline__ float score_fn(float v, int score_func, float gate_te
     if (gate_temp != 1.0f) v = v / gate_temp;
     if (score_func == WS_SCORE_SIGMOID) return ws_sigmoid(v);
     if (score_func == WS_SCORE_SQRTSOFTPLUS) {
-        float sp = v > 20.0f ? v : logf(1.0f + ws_expf(v));
-        return sqrtf(sp);
+        return sqrtf(ws_softplus(v));
     }
     return v;  // softmax handled by the caller, identity for given scores
 }
@@ -97,7 +96,7 @@ __device__ __forceinline__ void wave_scores_of(const float lg[CPL], int score_fu
 #pragma unroll
         for (int c = 0; c < CPL; c++) {
             const float ex = ws_expf_lanes(v[c], tab);
-            sc[c] = sqrtf(v[c] > 20.0f ? v[c] : logf(1.0f + ex));
+            sc[c] = sqrtf(v[c] > 20.0f ? v[c] : ws_logf(1.0f + ex));
         }
     } else {
 #pragma unroll
