@@ -390,6 +390,8 @@ void or_weight_quant_fp8_f32s(const float *w, size_t N, size_t K, size_t block, 
 void or_gemm_f32s(const uint8_t *aq, const float *as, size_t M,
                   const uint8_t *w, const float *ws, size_t N, size_t K, size_t block, float *y) {
     size_t kbn = K / block;
+    /* outputs are independent sequential sums: threads change no bits */
+#pragma omp parallel for collapse(2) num_threads(g_threads) if (g_threads > 1) schedule(static)
     for (size_t m = 0; m < M; m++)
         for (size_t n = 0; n < N; n++) {
             float acc = 0.0f;

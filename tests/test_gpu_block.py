@@ -1,0 +1,212 @@
+"""GPU parity of the full synthetic MoE block of BASELINE config 5, layers
+stacked, against the C oracle composed the same way (the reference gates its
+whole engine against the CPU path, weightstream-gpu/src/tests.rs:411, and
+layer by layer at :1603).
+
+One layer, per token row (every stage is row-independent):
+  o  = fp8_gemm(emit8(attn), wo)                 out-projection, K=8192 -> 4096
+  h  = h + o                                     acc_f32 (gemv.cu:63)
+  lg = gate . h                                  f32 gate GEMV, sequential dots
+  picks, weights = top-8 of sigmoid(lg) + bias   moe.rs:22-69
+  yr = routed FP4 experts (moe.rs:75-84,162-208) M=1: ws_moe_decode_route;
+                                                 M>1: ws_moe_topk + ws_moe_prefill
+  ys = shared FP8 expert, w1/w3 fused as w13     moe.rs:210-250, engine.rs:4063
+  h  = h + (yr + ys)                             two acc_f32 adds
+Weights follow the BASELINE recipe: N(0, 0.02) encoded to e2m1 + UE8M0 per
+1x32 (routed) and e4m3 + 32x32 UE8M0 (FP8), by the device encoders, which are
+bit-exact with the oracle's (test_gpu_kernels.py).
+
+Checks, on sampled rows of every layer, with the oracle fed the GPU's input
+to that layer (as the reference's per-layer gate does): the gate logits and
+the routing bit for bit; o, yr, ys and the layer output within max relative
+error 1e-3 (floor at 1% of the output scale). The end-to-end drift of the
+oracle's own chain over the stacked layers is printed beside it."""
+import numpy as np
+import pytest
+import torch
+
+import oracle_lib as O
+from gpu_util import DEV, announce, assert_close, host, rel_err_stats
+from weightstream_amd import launch as L
+
+pytestmark = pytest.mark.gpu
+
+E, TOPK, DIM, INTER = 384, 8, 4096, 2048
+OD, SI = 8192, 2048          # out-projection K, shared expert intermediate
+LAYERS = 2
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _init():
+    L.Hip.global_()
+
+
+def _fp8(gen, rows, cols):
+    w = torch.empty((rows, cols), dtype=torch.float32, device=DEV).normal_(0.0, 0.02,
+                                                                          generator=gen)
+    q = torch.empty((rows, cols), dtype=torch.uint8, device=DEV)
+    s = torch.empty((rows // 32, cols // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(w, q, s, rows, cols)
+    return q, s
+
+
+def _fp4_slab(gen, rows, cols, chunk=64):
+    """E expert matrices [rows, cols] N(0, 0.02) -> packed e2m1 + UE8M0 per
+    1x32, encoded `chunk` experts at a time."""
+    q = torch.empty((E * rows, cols // 2), dtype=torch.uint8, device=DEV)
+    s = torch.empty((E * rows, cols // 32), dtype=torch.uint8, device=DEV)
+    for e0 in range(0, E, chunk):
+        n = min(chunk, E - e0) * rows
+        w = torch.empty((n, cols), dtype=torch.float32, device=DEV).normal_(0.0, 0.02,
+                                                                           generator=gen)
+        r0 = e0 * rows
+        L.weight_quant_fp4(w, q[r0:r0 + n], s[r0:r0 + n], n, cols)
+        del w
+    return q, s
+
+
+@pytest.fixture(scope="module")
+def block():
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(5000)
+    announce("config 5 block: building %d layers of weights" % LAYERS)
+    lay = []
+    for _ in range(LAYERS):
+        raw = _fp4_slab(gen, INTER, DIM) + _fp4_slab(gen, INTER, DIM) + _fp4_slab(gen, DIM, INTER)
+        packed = (L.prepack_fp4_new(raw[0], raw[1], E * INTER, DIM)
+                  + L.prepack_fp4_new(raw[2], raw[3], E * INTER, DIM)
+                  + L.prepack_fp4_new(raw[4], raw[5], E * DIM, INTER))
+        lay.append({"raw": raw, "packed": packed, "wo": _fp8(gen, DIM, OD),
+                    "w13": _fp8(gen, 2 * SI, DIM), "w2": _fp8(gen, DIM, SI),
+                    "gate": torch.empty((E, DIM), dtype=torch.float32, device=DEV).normal_(
+                        0.0, 0.02, generator=gen),
+                    "bias": torch.randn((E,), device=DEV, generator=gen) * 0.1})
+    torch.cuda.synchronize()
+    yield lay
+    del lay
+    torch.cuda.empty_cache()
+
+
+def _run_gpu(lay, M, attn, h0):
+    """The bench's block step, one layer at a time, keeping each stage."""
+    st = torch.cuda.current_stream()
+    h = h0.clone()
+    aq = torch.empty((M, OD), dtype=torch.uint8, device=DEV)
+    asc = torch.empty((M, OD // 32), dtype=torch.uint8, device=DEV)
+    sws = torch.empty(L.shared_expert_workspace_size(M, DIM, SI), dtype=torch.uint8, device=DEV)
+    dws = torch.empty(L.moe_decode_workspace_size(DIM, INTER, TOPK), dtype=torch.uint8,
+                      device=DEV)
+    pws = torch.empty(L.moe_prefill_workspace_size(M, DIM, INTER, TOPK, E), dtype=torch.uint8,
+                      device=DEV)
+    stages = []
+    for li, w in enumerate(lay):
+        s = {"h_in": host(h)}
+        o = torch.empty((M, DIM), dtype=torch.float32, device=DEV)
+        lg = torch.empty((M, E), dtype=torch.float32, device=DEV)
+        idx = torch.empty((M, TOPK), dtype=torch.int32, device=DEV)
+        wts = torch.empty((M, TOPK), dtype=torch.float32, device=DEV)
+        yr = torch.empty((M, DIM), dtype=torch.float32, device=DEV)
+        ys = torch.empty((M, DIM), dtype=torch.float32, device=DEV)
+        L.emit8(attn[li], aq, asc, M * OD, stream=st)
+        L.fp8_gemm(aq, asc, *w["wo"], o, M, DIM, OD, stream=st)
+        L.acc_f32(o, h, M * DIM, stream=st)
+        s["o"], s["h_mid"] = host(o), host(h)
+        L.moe_gate_logits(h, w["gate"], lg, M, DIM, E, stream=st)
+        if M == 1:
+            L.moe_decode_route(lg, w["bias"], L.SCORE_SIGMOID, 1.0, 1, 1.0, h, *w["packed"], yr,
+                               idx, wts, DIM, INTER, E, TOPK, dws, stream=st)
+        else:
+            L.moe_topk(lg, w["bias"], None, idx, wts, M, E, TOPK, L.SCORE_SIGMOID, 1.0, True, 1.0,
+                       stream=st)
+            L.moe_prefill(h, idx, wts, *w["packed"], yr, M, DIM, INTER, E, TOPK, pws, stream=st)
+        L.shared_expert_fp8_w13(h, *w["w13"], *w["w2"], ys, M, DIM, SI, sws, stream=st)
+        s.update(lg=host(lg), idx=host(idx), w=host(wts), yr=host(yr), ys=host(ys))
+        L.acc_f32(ys, yr, M * DIM, stream=st)
+        L.acc_f32(yr, h, M * DIM, stream=st)
+        s["h_out"] = host(h)
+        stages.append(s)
+    return stages
+
+
+class _HostLayer:
+    """Host copies of one layer's weights; routed experts fetched on demand."""
+
+    def __init__(self, w):
+        self.w = w
+        self.wo = [host(t) for t in w["wo"]]
+        w13, s13 = (host(t) for t in w["w13"])
+        self.sh = (w13[:SI], s13[:SI // 32], w13[SI:], s13[SI // 32:]) + tuple(
+            host(t) for t in w["w2"])
+        self.gate = host(w["gate"])
+        self.bias = host(w["bias"])
+        self._experts = {}
+
+    def expert(self, e):
+        if e not in self._experts:
+            r = self.w["raw"]
+            a, b = e * INTER, (e + 1) * INTER
+            c, d = e * DIM, (e + 1) * DIM
+            self._experts[e] = (host(r[0][a:b]), host(r[1][a:b]), host(r[2][a:b]),
+                                host(r[3][a:b]), host(r[4][c:d]), host(r[5][c:d]))
+        return self._experts[e]
+
+    def routed(self, x, idx, wts):
+        """The oracle's routed MoE on a compact slab of the picked experts
+        (ascending expert id kept, so the summation order is the same)."""
+        uniq = sorted(set(int(e) for e in idx))
+        slab = [np.concatenate([self.expert(e)[i] for e in uniq]) for i in range(6)]
+        remap = np.array([uniq.index(int(e)) for e in idx], np.int32)
+        return O.moe_routed(*slab, DIM, INTER, x, remap, wts)
+
+
+def _oracle_layer(hl, attn_row, h_in):
+    aq, asc = O.fp8_act_emit(attn_row)
+    o = O.gemm_q(aq, asc, 1, hl.wo[0], hl.wo[1], DIM, OD, False)[0]
+    h_mid = (h_in + o).astype(np.float32)
+    lg = O.gemv_f32(hl.gate, h_mid)
+    idx, wts = O.route(O.score(lg, O.SCORE_SIGMOID), hl.bias, TOPK)
+    return dict(o=o, h_mid=h_mid, lg=lg, idx=idx, w=wts)
+
+
+@pytest.mark.parametrize("M,rows", [(1, [0]), (8, [0, 5, 7]), (64, [0, 31, 50, 63])])
+def test_config5_block_matches_oracle(block, M, rows):
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(5100 + M)
+    attn = torch.randn((LAYERS, M, OD), device=DEV, generator=gen)
+    h0 = torch.randn((M, DIM), device=DEV, generator=gen)
+    announce("config 5 block M=%d layers=%d" % (M, LAYERS))
+    stages = _run_gpu(block, M, attn, h0)
+    attn_h = host(attn)
+    hls = [_HostLayer(w) for w in block]
+    O.set_threads(16)
+    try:
+        chain = {r: host(h0)[r] for r in rows}
+        for li, (s, hl) in enumerate(zip(stages, hls)):
+            for r in rows:
+                what = "M=%d layer %d row %d" % (M, li, r)
+                ref = _oracle_layer(hl, attn_h[li, r], s["h_in"][r])
+                assert_close(s["o"][r], ref["o"], TOL, what + " out-proj")
+                # gate and routing on the GPU's h, bit for bit
+                ref_lg = O.gemv_f32(hl.gate, s["h_mid"][r])
+                assert np.array_equal(s["lg"][r].view(np.uint32), ref_lg.view(np.uint32)), what
+                ri, rw = O.route(O.score(ref_lg, O.SCORE_SIGMOID), hl.bias, TOPK)
+                assert np.array_equal(s["idx"][r], ri), (what, s["idx"][r], ri)
+                assert np.array_equal(s["w"][r].view(np.uint32), rw.view(np.uint32)), what
+                yr = hl.routed(s["h_mid"][r], ri, rw)
+                assert_close(s["yr"][r], yr, TOL, what + " routed")
+                ys = O.shared_fp8(*hl.sh, DIM, SI, s["h_mid"][r])
+                assert_close(s["ys"][r], ys, TOL, what + " shared")
+                h_out = (s["h_mid"][r] + (yr + ys).astype(np.float32)).astype(np.float32)
+                assert_close(s["h_out"][r], h_out, TOL, what + " layer output")
+                # the oracle's own chain (its h, its routing) for the drift report
+                c = _oracle_layer(hl, attn_h[li, r], chain[r])
+                cy = hl.routed(c["h_mid"], c["idx"], c["w"]) + O.shared_fp8(*hl.sh, DIM, SI,
+                                                                             c["h_mid"])
+                chain[r] = (c["h_mid"] + cy.astype(np.float32)).astype(np.float32)
+                mx, p50, _ = rel_err_stats(s["h_out"][r], chain[r])
+                same = np.array_equal(np.sort(c["idx"]), np.sort(s["idx"][r]))
+                print("[%s] end-to-end vs the oracle's chain: rel err max %.3g p50 %.3g, "
+                      "same experts %s" % (what, mx, p50, same), flush=True)
+    finally:
+        O.set_threads(1)

@@ -181,6 +181,53 @@ def test_fp8_gemm_f32s_matches_oracle(m, n, k, gemm_path):
 
 
 @pytest.mark.parametrize("n", [4096, 12288, 2048])
+def test_config2_fp8_gemm_f32s_full_size_matches_oracle(n, gemm_path):
+    """BASELINE config 2 in its own scale scheme at full size: M=128, K=4096,
+    N in {4096, 12288, 2048}; weights N(0, 0.02) quantised with 128x128 f32
+    scales amax/448 (or_weight_quant_fp8_f32s), activations N(0, 1) with 1%
+    outliers x20 quantised per 1x128 on the device (bit-exact with the
+    oracle); f32 and bf16 outputs against the oracle's sequential
+    dequantise-then-f32-accumulate GEMM (or_gemm_f32s) on every row. Runs
+    with and without the split-K workspace (the 128 x 256 split-K pipeline at
+    N = 12288, the 64 x 32 strips at N = 4096, the A-resident kernel at
+    N = 2048)."""
+    m, k = 128, 4096
+    rng = np.random.default_rng(3100 + n)
+    x = activations(rng, m, k)
+    wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    wq, ws = O.weight_quant_fp8_f32s(wf, 128)
+    del wf
+    aq_ref, as_ref = O.act_quant_f32s(x, 128)
+    O.set_threads(16)
+    try:
+        want = O.gemm_f32s(aq_ref, as_ref, wq, ws, 128)
+    finally:
+        O.set_threads(1)
+    announce("config 2 act_quant_f32s + fp8_gemm_f32s %s m=%d n=%d k=%d" % (gemm_path, m, n, k))
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    as_ = torch.empty((m, k // 128), dtype=torch.float32, device=DEV)
+    L.act_quant_f32s(dev(x), aq, as_, m, k)
+    assert np.array_equal(host(aq), aq_ref)
+    assert np.array_equal(host(as_).view(np.uint32), as_ref.view(np.uint32))
+    dwq, dws = dev(wq), dev(ws)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm_f32s(aq, as_, dwq, dws, out, m, n, k)
+    assert_close(host(out), want, GEMM_TOL, "config 2 f32s %dx%dx%d f32 out" % (m, n, k))
+    ob = torch.empty((m, n), dtype=torch.int16, device=DEV)
+    L.fp8_gemm_f32s(aq, as_, dwq, dws, ob, m, n, k, out_bf16=True)
+    bits = host(ob).astype(np.uint16)
+    got = (bits.astype(np.uint32) << 16).view(np.float32)
+    assert_close(got, want, 2.0 ** -8 + GEMM_TOL, "config 2 f32s %dx%dx%d bf16 out" % (m, n, k))
+    # bf16 out is the f32 result rounded to nearest even (quant.rs:95-101):
+    # equal to the oracle's f32 rounded to bf16 except at rounding boundaries
+    wb = want.view(np.uint32)
+    want_b = ((wb + (((wb >> 16) & 1) + 0x7FFF)) >> 16).astype(np.uint16)
+    same = np.mean(bits == want_b)
+    print("[config 2 bf16 n=%d] %.5f of outputs equal bf16(oracle)" % (n, same), flush=True)
+    assert same >= 0.999, same
+
+
+@pytest.mark.parametrize("n", [4096, 12288, 2048])
 def test_fp8_gemm_full_size_vs_fp64_dequant(n, gemm_path):
     """BASELINE config 2 shapes (M=128, K=4096) against an f64 matmul of the
     dequantised operands on the device (too large for the scalar oracle)."""
