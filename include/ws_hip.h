@@ -36,10 +36,12 @@ typedef struct ihipStream_t *ws_stream_t;
 #define WS_ERR_SHAPE 1002         /* shape outside what the kernels support */
 #define WS_ERR_NO_DEVICE 1003     /* no gfx950 device */
 
-/* Math modes of the GEMM-type kernels (ws_set_math_mode). EXACT (default):
- * FP8/FP4 operands are dequantised exactly to bf16 in registers and multiplied
- * with f32-accumulating bf16 MFMAs -- the reference's dequantise-then-f32-
- * accumulate product, rounding aside. NATIVE: the CDNA4 FP8 / MXFP4 scaled
+/* Math modes of the GEMM-type kernels, fixed when the library is built (no
+ * call changes the numerics of another). EXACT (libweightstream_hip.so):
+ * FP8/FP4 operands are dequantised exactly to bf16 in registers and
+ * multiplied with f32-accumulating bf16 MFMAs -- the reference's
+ * dequantise-then-f32-accumulate product, rounding aside. NATIVE
+ * (libweightstream_hip_native.so, same ABI): the CDNA4 FP8 / MXFP4 scaled
  * MFMAs, faster but their internal accumulation keeps about 13 bits
  * (relative error up to ~2^-12 of the sum of |products| per 128-K step). */
 #define WS_MATH_EXACT 0
@@ -58,9 +60,8 @@ typedef struct ihipStream_t *ws_stream_t;
 int ws_init(void);
 int ws_built_with_hip(void);
 const char *ws_error_string(int code);
-/* Process-wide math mode of every later launch (no reference counterpart:
- * weightstream-cuda has one precision). Returns the previous mode. */
-int ws_set_math_mode(int mode);
+/* The math mode this library was built with (no reference counterpart:
+ * weightstream-cuda has one precision). */
 int ws_get_math_mode(void);
 /* Device ws_expf over the 32-bit patterns [lo, lo+n): out[i] = bits(expf(x)).
  * Test hook for the exhaustive host/device expf agreement check. */
@@ -105,16 +106,18 @@ int ws_weight_quant_fp8(const float *w, uint8_t *q, uint8_t *s, int64_t rows, in
  * fp8_gemm_tile (M-batch) and the TileLang gemm_mxfp8 kernels.
  * ------------------------------------------------------------------- */
 /* Split-K workspace of the FP8/FP4 GEMMs (no counterpart in the reference,
- * whose kernels keep the whole K of a tile in one block). Once a workspace is
- * set for the current device, GEMMs with M > 64 (and M <= 16 with few
- * column strips and K > 8192) split K across workgroups and a second kernel
- * adds the f32 partials in split order (deterministic);
- * without one they use the single-pass kernels. The workspace is shared by
- * every GEMM call on the device: calls that may run concurrently (different
- * streams) need it not to be set, or must be serialised.
+ * whose kernels keep the whole K of a tile in one block), registered per
+ * (device, stream): GEMMs issued on `stream` (NULL = the default stream) of
+ * the current device use the workspace registered for that stream, so GEMMs
+ * on different streams never share one. With a workspace, GEMMs with M > 64
+ * (and M <= 16 with few column strips and K > 8192) split K across
+ * workgroups and a second kernel adds the f32 partials in split order
+ * (deterministic); without one they use the single-pass kernels. Calls on one
+ * stream are ordered by the stream, so they may share its workspace.
  * ws_gemm_workspace_size gives the bytes a shape needs; a smaller workspace
- * makes that shape use the single-pass kernel. Workspace NULL unsets it;
- * 256-byte aligned; `stream` is unused (kept for the launch convention). */
+ * makes that shape use the single-pass kernel. Workspace NULL unregisters the
+ * stream's; 256-byte aligned. The caller keeps the buffer alive while it is
+ * registered. */
 size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k);
 int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream);
 /* launch.rs:717-742 fp8_gemm(_on) (fp8_gemm.cu:9): A e4m3 + sa[M,K/32],
@@ -124,9 +127,29 @@ int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uin
 /* launch.rs:744-767 fp8_gemm_tile (fp8_gemm_tile.cu:28): same contract. */
 int ws_fp8_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                      float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
-/* launch.rs:344-377 fp8_gemm_tl(_on) takes packed u32 scale words and a
- * shape enum; this entry takes the raw UE8M0 bytes of fp8_gemm and any
- * (N,K), and writes bf16 (RNE, quant.rs:95-101) instead of f32. */
+/* launch.rs:341-377 fp8_gemm_tl(_on) (TileLang gemm_mxfp8_kernel): the
+ * shape comes from the TlGemm kind (WS_TL_*: (N, K) of engine.rs:3387-3398),
+ * a e4m3 [m, K], sa the activation's packed scale words [m, K/128] (the
+ * packed-word half that ws_emit8_packed writes at s + round_up(m*K/32, 16):
+ * four UE8M0 bytes per word, so its bytes are the [m, K/32] scales), b e4m3
+ * [N, K], sb the weight's upload-time packed table [N, K/128]
+ * (engine.rs:842-853 pack_weight_scales: row r holds the words of its
+ * 32-row block), out f32 [m, N]. */
+#define WS_TL_QA 0                 /* (1280, 5120) */
+#define WS_TL_QB 1                 /* (8192, 1280) */
+#define WS_TL_WKV 2                /* (512, 5120) */
+#define WS_TL_WO_A 3               /* (2048, 4096) */
+#define WS_TL_WO_B 4               /* (5120, 2048) */
+#define WS_TL_SHARED_W13 5         /* (2304, 5120) */
+#define WS_TL_SHARED_W13_FUSED 6   /* (4608, 5120) */
+#define WS_TL_SHARED_W2 7          /* (5120, 2304) */
+#define WS_TL_ENGRAM_WKV 8         /* (25600, 5120) */
+#define WS_TL_DRAFTER_MAIN_PROJ 9  /* (1280, 15360) */
+int ws_tl_gemm_shape(int kind, int64_t *n, int64_t *k);
+int ws_fp8_gemm_tl(int kind, const uint8_t *a, const uint32_t *sa, const uint8_t *b,
+                   const uint32_t *sb, float *out, int64_t m, ws_stream_t stream);
+/* fp8_gemm with bf16 output (RNE, quant.rs:95-101) instead of f32 (no
+ * reference counterpart: BASELINE config 2's bf16-out GEMM). */
 int ws_fp8_gemm_bf16(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                      uint16_t *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
 /* f32-scale block scheme (no reference counterpart; generalises fp8_gemm to
@@ -234,17 +257,51 @@ int ws_prepack_fp4(const uint8_t *w, const uint8_t *s, int64_t rows, int64_t col
                    uint8_t *ps, ws_stream_t stream);
 
 /* ---------------------------------------------------------------------
- * Routed experts, M = 1 decode (moe.rs:75-84,162-208; moe_grouped.cu:61-224).
+ * Routed experts, M = 1 decode (moe.rs:75-84,162-208; moe_grouped.cu:23-236).
  * Expert slabs (packed, see ws_prepack_fp4): w1/w3 [E, inter, dim] and
- * w2 [E, dim, inter]. topk_idx/topk_w as ws_moe_topk
- * writes them (top-k order); kernels sort the picks by ascending expert id.
+ * w2 [E, dim, inter]. The hidden state of a pick is stored in row `slot` of
+ * hq [top_k, inter] / hs [top_k, inter/32] (slot = the pick's position in
+ * the gate output), as the reference's expert_quant writes q_slots; the down
+ * projection sums the picks in ascending expert id (then slot).
  * Shapes: dim % 128 == 0, inter % 128 == 0, dim <= 16384, top_k <= 16,
  * top_k * inter <= 32768; WS_ERR_SHAPE otherwise.
  * ------------------------------------------------------------------- */
-/* Fused expert_glu + expert_quant (moe_grouped.cu:61,128): for each pick p
- * (rank r by ascending expert id) h = silu(min(w1.x,L)) * clamp(w3.x,+-L) * w_p,
- * then FP8 1x32 quantisation of h: hq[r, inter] e4m3, hs[r, inter/32].
- * x is the quantised token (xq[dim], xs[dim/32], as ws_emit8 writes). */
+/* launch.rs:89-112 moe_local_slots (moe_grouped.cu:23): the gate's picks
+ * gate_idx[top_k] (global expert ids) that fall in [e_start, e_start+e_len),
+ * sorted by ascending expert id (stable): local_slots[i] = their slot,
+ * local_experts[i] = id - e_start, *local_count = how many. */
+int ws_moe_local_slots(const int32_t *gate_idx, int32_t *local_slots, int32_t *local_experts,
+                       int32_t *local_count, int64_t top_k, int64_t e_start, int64_t e_len,
+                       ws_stream_t stream);
+/* launch.rs:658-670 moe_dispatch_ids (moe_grouped.cu:226): dispatch_idx[s] =
+ * gate_idx[s] - e_start if it falls in [e_start, e_start+e_len), else -1
+ * (int64, the input of ws_moe_dispatch_tl). */
+int ws_moe_dispatch_ids(const int32_t *gate_idx, int64_t *dispatch_idx, int64_t top_k,
+                        int64_t e_start, int64_t e_len, ws_stream_t stream);
+/* launch.rs:114-145 expert_glu (moe_grouped.cu:61): for local pick i <
+ * *local_count, h_slots[local_slots[i], 0..n) = silu(min(w1.x, 10)) *
+ * clamp(w3.x, -10, 10) * route_w[local_slots[i]] with w1/w3 = the slab rows of
+ * local expert local_experts[i]; act_x / act_x_s the e4m3 token [k] and its
+ * UE8M0 scales [k/32]. n = inter, k = dim. Trailing e_len (no counterpart:
+ * the reference trusts local_experts) is the slab's expert count; a pick
+ * outside it is skipped instead of read out of bounds. */
+int ws_expert_glu(const uint8_t *act_x, const uint8_t *act_x_s, const uint8_t *w1,
+                  const uint8_t *w1_s, const uint8_t *w3, const uint8_t *w3_s,
+                  const float *route_w, const int32_t *local_slots,
+                  const int32_t *local_experts, const int32_t *local_count, float *h_slots,
+                  int64_t n, int64_t k, int64_t top_k, int64_t e_len, ws_stream_t stream);
+/* launch.rs:147-166 expert_quant (moe_grouped.cu:128): the FP8 1x32 emit
+ * (act_quant_fp8_emit) of each local slot's h row into q_slots [top_k, n] and
+ * s_slots [top_k, n/32]. */
+int ws_expert_quant(const float *h_slots, const int32_t *local_slots, const int32_t *local_count,
+                    uint8_t *q_slots, uint8_t *s_slots, int64_t n, int64_t top_k,
+                    ws_stream_t stream);
+/* Fused expert_glu + expert_quant for the picks of the top-k output
+ * (topk_idx / topk_w [top_k], top-k order; picks outside [0, E) are skipped,
+ * as moe_local_slots drops another rank's experts): for each pick p
+ * h = silu(min(w1.x,L)) * clamp(w3.x,+-L) * w_p, quantised FP8 1x32 into
+ * row p of hq / hs. x is the quantised token (xq[dim], xs[dim/32], as
+ * ws_emit8 writes). */
 int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *topk_idx,
                         const float *topk_w, const uint8_t *w1, const uint8_t *s1,
                         const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs,
@@ -261,7 +318,7 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
  * the gate/up kernel of ws_moe_decode_route on its own. Every workgroup
  * routes the token from logits[E] (+ bias, score_func sigmoid or
  * sqrtsoftplus, gate_temp, norm_topk_prob, route_scale as ws_moe_topk) and
- * writes hq/hs [top_k, inter] (+ [top_k, inter/32]) by pick rank; the picks
+ * writes hq/hs [top_k, inter] (+ [top_k, inter/32]) by pick slot; the picks
  * land in topk_idx / topk_w [top_k]. dim <= 8192, E <= 1024; softmax scores
  * are rejected (WS_ERR_INVALID_ARG: they need the sequential sum). */
 int ws_expert_glu_quant_route(const float *logits, const float *bias, int score_func,
@@ -271,11 +328,15 @@ int ws_expert_glu_quant_route(const float *logits, const float *bias, int score_
                               int32_t *topk_idx, float *topk_w, int64_t dim, int64_t inter,
                               int64_t n_experts, int64_t top_k, float swiglu_limit,
                               ws_stream_t stream);
-/* expert_reduce (moe_grouped.cu:165, launch.rs:178-206): y[dim] = sum over
- * picks in ascending expert id of w2_e . h_e, one f32 add per expert. */
-int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
-                     const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
-                     int64_t inter, int64_t n_experts, int64_t top_k, ws_stream_t stream);
+/* launch.rs:178-206 expert_reduce (moe_grouped.cu:165): y[dim] = sum over the
+ * local picks in local_slots order (ascending expert id) of w2_e . h_slot,
+ * one f32 add per expert; e = gate_idx[slot] - e_start indexes the slab.
+ * act_slots / act_s_slots are the e4m3 / UE8M0 rows by slot. Trailing e_len
+ * as ws_expert_glu. */
+int ws_expert_reduce(const uint8_t *act_slots, const uint8_t *act_s_slots, const uint8_t *w2,
+                     const uint8_t *w2_s, const int32_t *gate_idx, const int32_t *local_slots,
+                     const int32_t *local_count, float *y, int64_t dim, int64_t inter,
+                     int64_t top_k, int64_t e_start, int64_t e_len, ws_stream_t stream);
 /* Whole routed MoE for one token from f32 x: glu_quant_x -> reduce (two
  * kernels; hq/hs of the picks live in the workspace; for dim > 8192 the
  * token is quantised into the workspace by a third kernel first).
@@ -312,18 +373,51 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
  * 8192 (a 32-slot tile of x, or above 4096 a 16-slot half of it, is staged
  * in LDS), inter <= 4096; WS_ERR_SHAPE otherwise.
  * ------------------------------------------------------------------- */
-/* launch.rs:430-468 moe_dispatch_tl (moe_dispatch.cu:17): per-expert counts,
- * 32-padded offsets in ascending expert id (exclusive scan), psum = offset +
- * count, order[slot] = route or -1 (padding), layout_w[slot] = route weight or
- * 0, route_pos[route] = slot (-1 for an expert id outside [0,E)),
- * tile_expert[t] = expert of 32-slot tile t or -1, num_tiles[0] = used tiles.
- * Inside an expert the routes keep ascending route index. Slots >= tiles*32
- * are not written. topk_idx is int32 (the reference kernel takes int64). */
+/* Dispatch (moe_dispatch.cu:17): per-expert counts, 32-padded offsets in
+ * ascending expert id (exclusive scan), psum = offset + count, order[slot] =
+ * route or -1 (padding), layout_w[slot] = route weight or 0, route_pos[route]
+ * = slot (-1 for an expert id outside [0,E)), tile_expert[t] = expert of
+ * 32-slot tile t or -1, num_tiles[0] = used tiles. Inside an expert the routes
+ * keep ascending route index. Slots >= tiles*32 are not written. This entry
+ * takes int32 ids (as ws_moe_topk writes them); ws_moe_dispatch_tl below is
+ * the reference's int64 form. */
 int ws_moe_dispatch(const int32_t *topk_idx, const float *topk_w, int32_t *order,
                     float *layout_w, int32_t *route_pos, int32_t *tile_expert,
                     int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
                     int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
                     int64_t n_experts, ws_stream_t stream);
+/* launch.rs:430-468 moe_dispatch_tl: the same with the int64 local ids that
+ * ws_moe_dispatch_ids writes (-1 = not this rank's), in launch.rs's argument
+ * order. Trailing n_experts (the TileLang kernel hard-codes its expert
+ * count) bounds the ids. */
+int ws_moe_dispatch_tl(const int64_t *topk_idx, const float *topk_weights, int32_t *order,
+                       float *layout_weights, int32_t *route_pos, int32_t *tile_expert,
+                       int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
+                       int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
+                       int64_t n_experts, ws_stream_t stream);
+/* launch.rs:470-580 moe_grouped_tl(_cached)(_on) (TileLang
+ * moe_grouped_fp8_fp4_gemm_kernel): out[slot, 0..n) f32 = A row . w_e^T for
+ * every slot of every used tile (tile_expert[t] >= 0; e = tile_expert[t]),
+ * K = k. kind GATE_UP: the A row of a slot is token order[slot] / top_k of
+ * a [tokens, k] (one of w1 or w3 per call, as the engine issues them);
+ * DOWN: the A row is row `slot` of a [tiles*32, k]. a is e4m3 with UE8M0
+ * scales sfa [rows, k/32] (the packed-word half written by ws_emit8_packed
+ * holds the same bytes, so either may be passed). weights / sfb are a packed
+ * expert slab [n_experts, n, k] (ws_prepack_fp4) in place of the TMA
+ * tensor map and its scale table. Rows of padding slots (order[slot] < 0)
+ * are not written. The TlMoe enum's hard-coded shapes become n, k (k <=
+ * 4096: the 32 x k A tile is staged in LDS) and the expert count n_experts. */
+#define WS_TL_MOE_GATE_UP 0
+#define WS_TL_MOE_DOWN 1
+int ws_moe_grouped_tl(int kind, const uint8_t *a, const uint8_t *sfa, const uint8_t *weights,
+                      const uint8_t *sfb, const int32_t *order, const int32_t *tile_expert,
+                      float *out, int64_t tiles, int64_t tokens, int64_t top_k, int64_t n,
+                      int64_t k, int64_t n_experts, ws_stream_t stream);
+/* launch.rs:672-687 moe_swiglu_route (moe_grouped.cu:239): out[row, n] =
+ * silu(min(gate,10)) * clamp(up,-10,10) * weights[row], or 0 where
+ * weights[row] == 0; rows = tiles * 32 slots. out may alias gate. */
+int ws_moe_swiglu_route(const float *gate, const float *up, const float *weights, float *out,
+                        int64_t inter, int64_t rows, ws_stream_t stream);
 /* Grouped gate/up (moe_grouped_tl GateUp) fused with moe_swiglu_route and the
  * FP8 emit: for every used tile, the 32 slots' tokens (xq [rows, dim] e4m3,
  * xs [rows, dim/32]) against the expert's w1/w3 rows; h = silu(min(g,L)) *
@@ -341,11 +435,13 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
                         const int32_t *num_tiles, const uint8_t *w2, const uint8_t *s2,
                         float *out, int64_t dim, int64_t inter, int64_t n_experts, int64_t tiles,
                         ws_stream_t stream);
-/* moe_combine_f32 (moe_grouped.cu:260): y[row] = sum of out[route_pos[row,
- * j]] over j, added in ascending slot order, i.e. ascending expert id (the
- * reference kernel adds in top-k order; moe.rs:76-84 adds by expert id). */
-int ws_moe_combine(const float *down, const int32_t *route_pos, float *y, int64_t rows,
-                   int64_t dim, int64_t top_k, int64_t tiles, ws_stream_t stream);
+/* launch.rs:689-703 moe_combine_f32 (moe_grouped.cu:260): out[row] = sum of
+ * y[route_pos[row, j]] over the row's routes (slots outside [0, tiles*32)
+ * skipped), added in ascending slot order, i.e. ascending expert id: the
+ * reference CPU order of moe.rs:76-84 (the reference kernel adds in top-k
+ * order). Trailing tiles (no counterpart) bounds the slots. */
+int ws_moe_combine_f32(const float *y, const int32_t *route_pos, float *out, int64_t dim,
+                       int64_t top_k, int64_t rows, int64_t tiles, ws_stream_t stream);
 /* Whole routed MoE for `rows` tokens from f32 x [rows, dim] and routing
  * (topk_idx/topk_w [rows, top_k]): emit8 -> dispatch -> grouped glu_quant ->
  * grouped down -> combine into y [rows, dim]. tiles = ceil(rows*top_k/32) +

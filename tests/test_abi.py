@@ -54,3 +54,23 @@ def test_workspace_sizes(lib):
     n = lib.ws_moe_decode_workspace_size(4096, 2048, 8)
     assert n >= 8 * 2048 + 8 * 64
     assert n % 256 == 0
+
+
+def test_native_build_exports_the_same_abi():
+    """The NATIVE-math build is the same ABI; each build reports its mode."""
+    native = _lib.load(native=True)
+    exact = _lib.load()
+    assert not [s for s in _lib.header_symbols() if not hasattr(native, s)]
+    assert exact.ws_get_math_mode() == 0 and native.ws_get_math_mode() == 1
+
+
+def test_cpp_mirror_compiles_links_and_throws(tmp_path):
+    """include/ws_hip.hpp (the C++ launch.rs mirror) compiles, links against
+    the library and turns rejected arguments into weightstream_hip::Error."""
+    exe = str(tmp_path / "hpp_check")
+    subprocess.check_call(["g++", "-std=c++17", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                           os.path.join(ROOT, "tests", "hpp_check.cpp"), "-o", exe,
+                           "-L", os.path.dirname(_lib.LIB_PATH), "-lweightstream_hip",
+                           "-Wl,-rpath," + os.path.dirname(_lib.LIB_PATH)])
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr

@@ -92,9 +92,10 @@ def test_moe_decode_matches_oracle(E, dim, inter, k):
 
 
 def test_moe_decode_split_entry_points_and_order():
-    """expert_glu_quant writes picks in ascending expert id; expert_reduce
-    sums them in that order; the result equals the one-call moe_decode
-    bit for bit, whatever order the picks arrive in."""
+    """expert_glu_quant writes pick p's hidden state to row p (its gate
+    slot); moe_local_slots orders the picks by ascending expert id and
+    expert_reduce sums them in that order; the result equals the one-call
+    moe_decode bit for bit, whatever order the picks arrive in."""
     rng = np.random.default_rng(710)
     E, dim, inter, k = 32, 1024, 256, 5
     gen = torch.Generator(device=DEV)
@@ -117,19 +118,21 @@ def test_moe_decode_split_entry_points_and_order():
     w1, s1, w3, s3, w2, s2 = packed
     L.expert_glu_quant(xq, xs, dev(ids), dev(wts), w1, s1, w3, s3, hq, hs, inter, dim, E, k)
     y3 = torch.empty(dim, dtype=torch.float32, device=DEV)
-    L.expert_reduce(hq, hs, w2, s2, dev(ids), y3, dim, inter, E, k)
+    ls, le, lc = (torch.empty(n, dtype=torch.int32, device=DEV) for n in (k, k, 1))
+    L.moe_local_slots(dev(ids), ls, le, lc, k, 0, E)
+    assert list(host(ls)) == list(np.argsort(ids, kind="stable")) and int(host(lc)[0]) == k
+    L.expert_reduce(hq, hs, w2, s2, dev(ids), ls, lc, y3, dim, inter, k, 0, E)
     assert np.array_equal(host(y1).view(np.uint32), host(y3).view(np.uint32))
     # the fused-quantisation variant writes the same bytes
     hq2 = torch.empty_like(hq)
     hs2 = torch.empty_like(hs)
     L.expert_glu_quant_x(dev(x), dev(ids), dev(wts), w1, s1, w3, s3, hq2, hs2, inter, dim, E, k)
     assert torch.equal(hq, hq2) and torch.equal(hs, hs2)
-    # row r of hq is the r-th smallest expert id's hidden state
+    # row p of hq is pick p's hidden state
     H = _host_experts(slabs, ids, E, dim, inter)
-    order = np.argsort(ids)
     hq_h, hs_h = host(hq), host(hs)
     table = O.e4m3_decode_table()
-    for r, p in enumerate(order):
+    for r, p in enumerate(range(k)):
         e = ids[p]
         g = O.fp4_gemv(H[0][e].ravel(), H[1][e].ravel(), inter, dim, x)
         u = O.fp4_gemv(H[2][e].ravel(), H[3][e].ravel(), inter, dim, x)

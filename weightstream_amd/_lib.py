@@ -1,7 +1,9 @@
-"""Loader of the in-tree HIP library libweightstream_hip.so.
+"""Loader of the in-tree HIP libraries.
 
-The library is the product: there is no CPU or PyTorch fallback. If it is
-missing, importing any entry point raises.
+libweightstream_hip.so (EXACT math) is the product;
+libweightstream_hip_native.so is the same ABI built with the CDNA4 scaled
+MFMAs (NATIVE math). There is no CPU or PyTorch fallback: if a library is
+missing, loading it raises.
 """
 import ctypes as C
 import os
@@ -10,9 +12,10 @@ import re
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 LIB_PATH = os.path.join(PKG, "libweightstream_hip.so")
+LIB_NATIVE_PATH = os.path.join(PKG, "libweightstream_hip_native.so")
 HEADER = os.path.join(ROOT, "include", "ws_hip.h")
 
-_lib = None
+_libs = {}
 
 
 def header_symbols():
@@ -22,16 +25,19 @@ def header_symbols():
     return sorted(set(re.findall(r"\b(ws_[a-z0-9_]+)\s*\(", txt)))
 
 
-def load():
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
+def load(native=False):
+    """The EXACT library, or with native=True the NATIVE-math build."""
+    lib = _libs.get(native)
+    if lib is None:
+        path = LIB_NATIVE_PATH if native else LIB_PATH
+        if not os.path.exists(path):
             raise RuntimeError(
-                "libweightstream_hip.so is not built (python -m weightstream_amd.build); "
-                "weightstream_amd has no fallback path")
-        _lib = C.CDLL(LIB_PATH)
-        _declare(_lib)
-    return _lib
+                "%s is not built (python -m weightstream_amd.build); "
+                "weightstream_amd has no fallback path" % os.path.basename(path))
+        lib = C.CDLL(path)
+        _declare(lib)
+        _libs[native] = lib
+    return lib
 
 
 _p = C.c_void_p
@@ -46,7 +52,6 @@ SIGNATURES = {
     "ws_error_string": (C.c_char_p, [_i]),
     "ws_expf_probe": (_i, [_u32, _u32, _p, _p]),
     "ws_math_probe": (_i, [_i, _u32, _u32, _p, _p]),
-    "ws_set_math_mode": (_i, [_i]),
     "ws_get_math_mode": (_i, []),
     "ws_snap8": (_i, [_p, _i64, _p]),
     "ws_emit8": (_i, [_p, _p, _p, _i64, _p]),
@@ -62,6 +67,8 @@ SIGNATURES = {
     "ws_fp8_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_bf16": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_f32s": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _p]),
+    "ws_tl_gemm_shape": (_i, [_i, _p, _p]),
+    "ws_fp8_gemm_tl": (_i, [_i, _p, _p, _p, _p, _p, _i64, _p]),
     "ws_act_quant_f32s": (_i, [_p, _p, _p, _i64, _i64, _p]),
     "ws_fp4_gemm": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp4_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
@@ -81,15 +88,22 @@ SIGNATURES = {
     "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_x": (_i, [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_route": (_i, [_p, _p, _i, _f, _i, _f] + [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
-    "ws_expert_reduce": (_i, [_p] * 6 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_local_slots": (_i, [_p] * 4 + [_i64, _i64, _i64, _p]),
+    "ws_moe_dispatch_ids": (_i, [_p, _p, _i64, _i64, _i64, _p]),
+    "ws_expert_glu": (_i, [_p] * 11 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_expert_quant": (_i, [_p] * 5 + [_i64, _i64, _p]),
+    "ws_expert_reduce": (_i, [_p] * 8 + [_i64, _i64, _i64, _i64, _i64, _p]),
     "ws_moe_decode_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
     "ws_moe_decode": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
     "ws_moe_decode_route": (_i, [_p, _p, _i, _f, _i, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                  _i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
     "ws_moe_dispatch": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_dispatch_tl": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_grouped_tl": (_i, [_i] + [_p] * 7 + [_i64] * 6 + [_p]),
+    "ws_moe_swiglu_route": (_i, [_p] * 4 + [_i64, _i64, _p]),
     "ws_moe_grouped_glu_quant": (_i, [_p] * 12 + [_i64, _i64, _i64, _i64, _i64, _f, _p]),
     "ws_moe_grouped_down": (_i, [_p] * 7 + [_i64, _i64, _i64, _i64, _p]),
-    "ws_moe_combine": (_i, [_p] * 3 + [_i64, _i64, _i64, _i64, _p]),
+    "ws_moe_combine_f32": (_i, [_p] * 3 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_prefill_workspace_size": (C.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "ws_moe_prefill": (_i, [_p] * 10 + [_i64] * 5 + [_f, _p, C.c_size_t, _p]),
 }
@@ -106,7 +120,7 @@ def _declare(lib):
 
 class WsError(RuntimeError):
     def __init__(self, fn, code):
-        msg = load().ws_error_string(code).decode()
+        msg = load().ws_error_string(code).decode()  # same strings in both builds
         super().__init__("%s failed: %s (code %d)" % (fn, msg, code))
         self.code = code
 

@@ -1,9 +1,12 @@
-"""Build libweightstream_hip.so (gfx950) in-tree with hipcc.
+"""Build the gfx950 libraries in-tree with hipcc.
 
     python -m weightstream_amd.build
 
-Objects go to weightstream_amd/_build/, the library to
-weightstream_amd/libweightstream_hip.so, where weightstream_amd._lib loads it.
+Objects go to weightstream_amd/_build/. Two libraries share every object but
+the one that fixes the math mode (csrc/math_mode.hip):
+  weightstream_amd/libweightstream_hip.so         WS_MATH_EXACT (the product)
+  weightstream_amd/libweightstream_hip_native.so  WS_MATH_NATIVE (CDNA4 scaled MFMA)
+weightstream_amd._lib loads them.
 """
 import os
 import shutil
@@ -16,6 +19,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libweightstream_hip.so")
+LIB_NATIVE = os.path.join(PKG, "libweightstream_hip_native.so")
 
 SOURCES = ["common.hip", "pack.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip",
            "moe_shared.hip"]
@@ -43,28 +47,37 @@ def hipcc():
     raise RuntimeError("hipcc not found: the gfx950 library cannot be built")
 
 
-def _compile(src):
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(job):
+    src, obj, extra = job
+    cmd = [hipcc()] + HIPCC_FLAGS + extra + ["-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("hipcc failed for %s:\n%s%s" % (src, r.stdout, r.stderr))
     return obj
 
 
-def build(verbose=True):
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+def _link(objs, lib):
+    tmp = lib + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n%s%s" % (r.stdout, r.stderr))
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose=True):
+    os.makedirs(BUILD, exist_ok=True)
+    o = lambda name: os.path.join(BUILD, name)
+    jobs = [(s, o(os.path.splitext(s)[0] + ".o"), []) for s in SOURCES]
+    jobs += [("math_mode.hip", o("math_mode.o"), []),
+             ("math_mode.hip", o("math_mode_native.o"), ["-DWS_NATIVE_MATH"])]
+    with ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        objs = list(ex.map(_compile, jobs))
+    shared = objs[:len(SOURCES)]
+    _link(shared + [o("math_mode.o")], LIB)
+    _link(shared + [o("math_mode_native.o")], LIB_NATIVE)
     if verbose:
-        print("built", LIB)
+        print("built", LIB, "and", LIB_NATIVE)
     return LIB
 
 

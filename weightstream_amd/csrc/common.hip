@@ -139,9 +139,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float *gate, const fl
     out[i] = ws_silu(g) * u * rw;
 }
 
-static std::atomic<int> g_math_mode{WS_MATH_EXACT};
-int math_mode() { return g_math_mode.load(std::memory_order_relaxed); }
-
 int cu_count() {
     static std::atomic<int> cache[64];
     int dev = 0;
@@ -163,12 +160,7 @@ extern "C" {
 
 int ws_built_with_hip(void) { return 1; }
 
-int ws_set_math_mode(int mode) {
-    if (mode != WS_MATH_EXACT && mode != WS_MATH_NATIVE) return -1;
-    return g_math_mode.exchange(mode);
-}
-
-int ws_get_math_mode(void) { return g_math_mode.load(); }
+int ws_get_math_mode(void) { return math_mode(); }
 
 const char *ws_error_string(int code) {
     switch (code) {

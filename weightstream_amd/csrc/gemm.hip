@@ -27,6 +27,8 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+
 namespace ws {
 
 enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
@@ -273,7 +275,8 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                                                                 const void *__restrict__ SB,
                                                                 void *__restrict__ C, int M,
                                                                 int N, int K, int S,
-                                                                float *__restrict__ part_out) {
+                                                                float *__restrict__ part_out,
+                                                                int sb_div) {
     constexpr int kRows = 16 * MF * GMH;
     constexpr int kCols = 16 * NF;
     // UE8M0 activation scales: staged in LDS for blocks of rows; a single
@@ -347,7 +350,8 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
         const int col = n0 + 16 * j + r;
         brow[j] = BFP4 ? B + (size_t)col * (K / 2) + g * 16
                        : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
-        sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / 32) * kbn;
+        // FP8 weight scales: one row per 32-row block, or per row (sb_div 1)
+        sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / sb_div) * kbn;
     }
     const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
 
@@ -536,7 +540,8 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 
 template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U>
 static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
-                     int m, int n, int k, hipStream_t stream, int S = 1, float *part = nullptr) {
+                     int m, int n, int k, hipStream_t stream, int S = 1, float *part = nullptr,
+                     int sb_div = 32) {
     constexpr int rows = 16 * MF * GMH, threads = 64 * GMH * GK;
     if (n % (16 * NF)) return -1;
     const int ksteps = k / 128;
@@ -548,10 +553,12 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows), (unsigned)S);
     if (math_mode() == WS_MATH_NATIVE)
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part);
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
+                           sb_div);
     else
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part);
+                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
+                           sb_div);
     int rc = launch_status();
     if (rc || S == 1) return rc;
     const int64_t mn = (int64_t)m * n;
@@ -1162,17 +1169,54 @@ __global__ __launch_bounds__(256) void pipe_reduce_kernel(const float4 *__restri
     }
 }
 
-// Workspace for the split-K kernel, per device (ws_set_gemm_workspace).
+// Workspaces for the split-K kernels, one per (device, stream)
+// (ws_set_gemm_workspace): GEMMs on different streams never share partials.
 struct SkWorkspace {
     uint8_t *ptr;
     size_t bytes;
 };
-static SkWorkspace g_sk_ws[64];
+struct SkEntry {
+    int dev;
+    hipStream_t stream;
+    SkWorkspace ws;
+};
+constexpr int kMaxSkEntries = 256;
+static std::mutex g_sk_mu;
+static SkEntry g_sk[kMaxSkEntries];
+static int g_sk_n = 0;
 
-static SkWorkspace &sk_ws() {
+static int current_device() {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-    return g_sk_ws[dev];
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    return dev;
+}
+
+// the workspace registered for `stream` on the current device (none: {0, 0})
+static SkWorkspace sk_ws(hipStream_t stream) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_sk_mu);
+    for (int i = 0; i < g_sk_n; i++)
+        if (g_sk[i].dev == dev && g_sk[i].stream == stream) return g_sk[i].ws;
+    return SkWorkspace{nullptr, 0};
+}
+
+static int sk_set(hipStream_t stream, uint8_t *ptr, size_t bytes) {
+    const int dev = current_device();
+    std::lock_guard<std::mutex> lock(g_sk_mu);
+    for (int i = 0; i < g_sk_n; i++) {
+        if (g_sk[i].dev == dev && g_sk[i].stream == stream) {
+            if (ptr) {
+                g_sk[i].ws = SkWorkspace{ptr, bytes};
+            } else {
+                g_sk[i] = g_sk[--g_sk_n];
+            }
+            return WS_OK;
+        }
+    }
+    if (!ptr) return WS_OK;
+    if (g_sk_n == kMaxSkEntries) return WS_ERR_SHAPE;
+    g_sk[g_sk_n++] = SkEntry{dev, stream, SkWorkspace{ptr, bytes}};
+    return WS_OK;
 }
 
 // Splits for the pipelined kernel: K ranges of at most kPMaxSteps steps, and
@@ -1210,9 +1254,8 @@ static int pipe_bn(int M, int N) {
 
 template <int BN, bool BFP4, int SMODE, int OMODE>
 static int launch_pipe(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
-                       int m, int n, int k, hipStream_t stream) {
+                       int m, int n, int k, hipStream_t stream, const SkWorkspace &wsp) {
     using G = PipeGeom<BN, BFP4, SMODE>;
-    SkWorkspace &wsp = sk_ws();
     const int S = pipe_splits(m, n, k, BN, wsp.ptr ? wsp.bytes : 0);
     if (S <= 0) return -1;
     const int ntn = (n + BN - 1) / BN;
@@ -1260,13 +1303,35 @@ static int forced_cfg() {
 
 template <bool BFP4, int SMODE, int OMODE>
 static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb,
-                         void *out, int64_t m, int64_t n, int64_t k, hipStream_t stream) {
+                         void *out, int64_t m, int64_t n, int64_t k, hipStream_t stream,
+                         int sb_div = 32) {
     if (!a || !sa || !b || !sb || !out) return WS_ERR_INVALID_ARG;
     if (m <= 0 || n <= 0 || k <= 0) return WS_ERR_INVALID_ARG;
     if (k % 128 || n % 16 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return WS_ERR_SHAPE;
     if (((uintptr_t)a | (uintptr_t)b) & 15 || ((uintptr_t)sa | (uintptr_t)sb) & 3)
         return WS_ERR_INVALID_ARG;
     int M = (int)m, N = (int)n, K = (int)k;
+    const SkWorkspace wsp = sk_ws(stream);
+    if (sb_div != 32) {
+        // weight scales per row (the reference's packed scale table): the
+        // column-strip kernel only
+        int rc;
+        if (M <= 16) {
+            const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
+            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream, S,
+                                                               (float *)wsp.ptr, sb_div);
+        } else if (M <= 32) {
+            rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
+                                                               nullptr, sb_div);
+        } else if (M <= 64) {
+            rc = launch_kp<4, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
+                                                               nullptr, sb_div);
+        } else {
+            rc = launch_kp<4, 1, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
+                                                               nullptr, sb_div);
+        }
+        return rc < 0 ? WS_ERR_SHAPE : rc;
+    }
     int cfg = forced_cfg();
     if (cfg < 0) {
         int rc = -1;
@@ -1293,15 +1358,14 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         // 2. M > 64: the pipelined split-K kernel (128-row tiles)
         if (M > 64) {
             const int bn = pipe_bn(M, N);
-            rc = bn == 256   ? launch_pipe<256, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
-                 : bn == 128 ? launch_pipe<128, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream)
-                             : launch_pipe<64, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
+            rc = bn == 256   ? launch_pipe<256, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp)
+                 : bn == 128 ? launch_pipe<128, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp)
+                             : launch_pipe<64, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp);
         }
         if (rc >= 0) return rc;
         // 3. 16-column strips (no split-K workspace, or shapes the others
         // do not stage)
         if (M <= 16) {
-            SkWorkspace &wsp = sk_ws();
             const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
             rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream, S,
                                                                (float *)wsp.ptr);
@@ -1346,17 +1410,12 @@ size_t ws_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
 }
 
 int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream) {
-    (void)stream;
-    SkWorkspace &wsp = sk_ws();
     if (!workspace || bytes == 0) {
-        wsp.ptr = nullptr;
-        wsp.bytes = 0;
+        sk_set(stream, nullptr, 0);
         return workspace ? WS_ERR_INVALID_ARG : WS_OK;
     }
     if ((uintptr_t)workspace & 255) return WS_ERR_INVALID_ARG;
-    wsp.ptr = (uint8_t *)workspace;
-    wsp.bytes = bytes;
-    return WS_OK;
+    return sk_set(stream, (uint8_t *)workspace, bytes);
 }
 
 int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
@@ -1379,6 +1438,30 @@ int ws_fp8_gemm_f32s(const uint8_t *a, const float *sa, const uint8_t *b, const 
     if (out_bf16)
         return gemm_dispatch<false, kF32s, kOutBf16>(a, sa, b, sb, out, m, n, k, stream);
     return gemm_dispatch<false, kF32s, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+// launch.rs:325-339 TlGemm: (N, K) of each hard-coded TileLang GEMM
+// (engine.rs:3387-3398; WoA from its kernel's strides)
+static const int kTlShapes[][2] = {{1280, 5120}, {8192, 1280}, {512, 5120},  {2048, 4096},
+                                   {5120, 2048}, {2304, 5120}, {4608, 5120}, {5120, 2304},
+                                   {25600, 5120}, {1280, 15360}};
+
+int ws_tl_gemm_shape(int kind, int64_t *n, int64_t *k) {
+    if (kind < 0 || kind >= (int)(sizeof(kTlShapes) / sizeof(kTlShapes[0])) || !n || !k)
+        return WS_ERR_INVALID_ARG;
+    *n = kTlShapes[kind][0];
+    *k = kTlShapes[kind][1];
+    return WS_OK;
+}
+
+int ws_fp8_gemm_tl(int kind, const uint8_t *a, const uint32_t *sa, const uint8_t *b,
+                   const uint32_t *sb, float *out, int64_t m, ws_stream_t stream) {
+    int64_t n, k;
+    int rc = ws_tl_gemm_shape(kind, &n, &k);
+    if (rc) return rc;
+    // the packed activation words are the UE8M0 bytes [m, k/32] as they lie
+    // in memory; the weight table holds each row's K/32 scale bytes
+    return gemm_dispatch<false, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream, 1);
 }
 
 int ws_fp4_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,

@@ -73,15 +73,54 @@ __device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, i
     return wave_picks_of(lane < top_k ? idx[lane] : -1, top_k, n_experts, lane);
 }
 
-// expert id of the valid pick with rank p (0 if there is none)
-__device__ __forceinline__ int wave_expert_of_rank(const WavePicks &wp, int p) {
-    const unsigned long long m = __ballot(wp.rank == p);
-    return m ? __builtin_amdgcn_readlane(wp.e, __ffsll((long long)m) - 1) : 0;
+// The valid picks in summation order (ascending expert id, then slot), as
+// the down kernel walks them: lane r < nv holds the gate-output slot of the
+// pick of rank r (its row of hq / hs) and its expert's row in the slab.
+struct RankedPicks {
+    int slot;
+    int e;
+    int nv;
+};
+
+// from the top-k output: rank by (expert id, slot) among picks in [0, E)
+__device__ __forceinline__ RankedPicks ranked_from_topk(const int32_t *idx, int top_k,
+                                                        int n_experts, int lane) {
+    const WavePicks wp = wave_picks(idx, top_k, n_experts, lane);
+    RankedPicks rp{0, 0, wp.nv};
+    for (int i = 0; i < top_k; i++) {
+        if (__builtin_amdgcn_readlane(wp.rank, i) == lane) {
+            rp.slot = i;
+            rp.e = __builtin_amdgcn_readlane(wp.e, i);
+        }
+    }
+    return rp;
 }
 
-// rank of pick `slot` (uniform)
-__device__ __forceinline__ int wave_rank_of_slot(const WavePicks &wp, int slot) {
-    return __builtin_amdgcn_readlane(wp.rank, slot);
+// from moe_local_slots' lists (moe_grouped.cu:23-58: slots already in
+// ascending expert id): slot local[r], slab row gate_idx[slot] - e_start.
+// A row outside [0, e_len) (which moe_local_slots never produces) is dropped
+// instead of read out of bounds.
+__device__ __forceinline__ RankedPicks ranked_from_local(const int32_t *local,
+                                                         const int32_t *local_count,
+                                                         const int32_t *gate_idx, int e_start,
+                                                         int e_len, int top_k, int lane) {
+    const int cnt = min(*local_count, top_k);
+    int slot = 0, e = -1;
+    if (lane < cnt) {
+        slot = local[lane];
+        e = (slot >= 0 && slot < top_k) ? gate_idx[slot] - e_start : -1;
+    }
+    const bool valid = lane < cnt && e >= 0 && e < e_len;
+    const unsigned long long vm = __ballot(valid);
+    const int nr = __popcll(vm & ((1ull << lane) - 1));
+    RankedPicks rp{0, 0, (int)__popcll(vm)};
+    for (int i = 0; i < cnt; i++) {
+        if (((vm >> i) & 1) && __builtin_amdgcn_readlane(nr, i) == lane) {
+            rp.slot = __builtin_amdgcn_readlane(slot, i);
+            rp.e = __builtin_amdgcn_readlane(e, i);
+        }
+    }
+    return rp;
 }
 
 // Multiply one register stage of a packed 16-row FP4 band with the operand in
@@ -244,6 +283,23 @@ __device__ __forceinline__ void share_load_fp8(Fp8Share<R> &tr, const uint8_t *q
     }
 }
 
+// As share_load_fp8 over the concatenation of the picks' rows in rank order:
+// byte i of it is byte i % inter of hq row rp.slot of rank i / inter.
+template <int R>
+__device__ __forceinline__ void share_load_ranked(Fp8Share<R> &tr, const uint8_t *q,
+                                                  const uint8_t *s, const RankedPicks &rp,
+                                                  int inter, int c0, int c1, int lane) {
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const int i = max(min(c0 + j * 1024 + lane * 16, c1 - 16), 0);
+        const int r = i / inter, off = i - r * inter;
+        const int row = max(__shfl(rp.slot, r, 64), 0);
+        const size_t a = (size_t)row * inter + off;
+        tr.q[j] = *(const uint4 *)(q + a);
+        tr.s[j] = s[a / 32];
+    }
+}
+
 // ... into LDS: exact bf16 values (EXACT) or the bytes and scales as they are
 template <bool EXACT, int R>
 __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, int c1, int lane,
@@ -285,23 +341,37 @@ struct RouteArgs {
     float *w_out;
 };
 
+// Where the picks come from when the kernel does not route (CPL == 0):
+//  - the top-k output (local == nullptr): workgroup row y is pick (slot) y,
+//    expert idx[y], routing weight w[y];
+//  - the reference's local-slot lists (moe_local_slots, moe_grouped.cu:23):
+//    row y < *local_count is slot local[y] of the gate output, local expert
+//    row local_experts[y], weight w[slot]; rows beyond the count do nothing.
+// Either way h of a pick is written to row `slot` of the output, as the
+// reference's expert_glu / expert_quant write h_slots / q_slots.
+struct PickSrc {
+    const int32_t *idx;
+    const float *w;
+    const int32_t *local, *local_experts, *local_count;
+};
+
 // CPL > 0: route in the kernel (CPL candidates per lane, E <= 64 CPL);
-// CPL == 0: picks from idx / topk_w.
-template <bool EXACT, bool XF32, int CPL>
+// CPL == 0: picks from `ps`. HF32: write h in f32 to hf [slot, inter]
+// (expert_glu) instead of its FP8 1x32 quantisation to hq / hs.
+template <bool EXACT, bool XF32, int CPL, bool HF32 = false>
 __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
-    const uint8_t *xq, const uint8_t *xs, const float *xf,
-    const int32_t *__restrict__ idx, const float *__restrict__ topk_w, RouteArgs ra,
+    const uint8_t *xq, const uint8_t *xs, const float *xf, PickSrc ps, RouteArgs ra,
     const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
-    uint8_t *__restrict__ hs, int dim, int inter, int n_experts, int top_k, float limit,
-    int tpw) {
+    uint8_t *__restrict__ hs, float *__restrict__ hf, int dim, int inter, int n_experts,
+    int top_k, float limit, int tpw) {
     extern __shared__ __align__(16) uint8_t lds[];
     // EXACT: bf16 token (2*dim bytes); native: e4m3 token + scales
     __bf16 *x_l = (__bf16 *)lds;
     uint8_t *xq_l = lds;
     uint8_t *xs_l = lds + dim;
     __shared__ float gu[kGluKParts][2][32];
-    const int slot = blockIdx.y;
+    int slot = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int ksteps = dim / 128;
 
@@ -334,7 +404,6 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     // other waves through LDS)
     int e;
     float rw;
-    WavePicks wp;
     WaveTopk<(CPL > 0 ? CPL : 1)> tk;
     __shared__ int e_l;
     __shared__ int pk_l[kMaxTopkDec];
@@ -362,12 +431,18 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
         }
         lds_barrier();
         e = e_l;
+    } else if (ps.local) {
+        const int i = slot;
+        if (i >= *ps.local_count) return;  // whole workgroup
+        slot = ps.local[i];
+        e = ps.local_experts[i];
+        rw = ps.w[slot];
     } else {
-        e = idx[slot];
-        rw = topk_w[slot];
-        wp = wave_picks(idx, top_k, n_experts, lane);
+        e = ps.idx[slot];
+        rw = ps.w[slot];
     }
-    if (e < 0 || e >= n_experts) return;  // whole workgroup (a pick another rank owns)
+    // whole workgroup: a pick another rank owns (or a row outside the slab)
+    if (e < 0 || e >= n_experts) return;
 
     const int tile = blockIdx.x * tpw + (tpw == 2 ? sub : 0);
     int k0, k1;
@@ -402,10 +477,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
     else share_store_fp8<EXACT>(tr.b, tc0, tc1, lane, x_l, xq_l, xs_l);
     lds_barrier();
-    if constexpr (CPL > 0) {
-        rw = pw_l[slot];
-        wp = wave_picks_of(lane < top_k ? pk_l[lane] : 0, top_k, n_experts, lane);
-    }
+    if constexpr (CPL > 0) rw = pw_l[slot];
 
     {
         v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1);
@@ -432,18 +504,29 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
         g = fminf(g, limit);
     }
     float h = ws_silu(g) * u * rw;
-    uint32_t sb;
-    uint32_t qb = quant_fp8_block32(h, &sb);
-    const int rank = wave_rank_of_slot(wp, slot);
-    if (lane < 32) {
-        hq[(size_t)rank * inter + otile * 32 + n] = (uint8_t)qb;
-        if (n == 0) hs[(size_t)rank * (inter / 32) + otile] = (uint8_t)sb;
+    if constexpr (HF32) {
+        if (lane < 32) hf[(size_t)slot * inter + otile * 32 + n] = h;
+    } else {
+        uint32_t sb;
+        uint32_t qb = quant_fp8_block32(h, &sb);
+        if (lane < 32) {
+            hq[(size_t)slot * inter + otile * 32 + n] = (uint8_t)qb;
+            if (n == 0) hs[(size_t)slot * (inter / 32) + otile] = (uint8_t)sb;
+        }
     }
 }
 
+// Picks of the down kernel: the top-k output (local == nullptr; picks outside
+// [0, E) skipped) or moe_local_slots' lists with the global ids in idx.
+struct ReducePicks {
+    const int32_t *idx;
+    const int32_t *local, *local_count;
+    int e_start;
+};
+
 template <bool EXACT>
 __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
-    const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ idx,
+    const uint8_t *hq, const uint8_t *hs, ReducePicks pk,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
     int inter, int n_experts, int top_k) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -451,14 +534,16 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int row0 = blockIdx.x * 16;
     // every wave ranks the (<= 16) picks itself: no barrier before the loads
-    const WavePicks wp = wave_picks(idx, top_k, n_experts, lane);
-    const int nv = wp.nv;
+    const RankedPicks rp = pk.local ? ranked_from_local(pk.local, pk.local_count, pk.idx,
+                                                        pk.e_start, n_experts, top_k, lane)
+                                    : ranked_from_topk(pk.idx, top_k, n_experts, lane);
+    const int nv = rp.nv;
     // the picks' hidden states (nv rows of inter e4m3 bytes, ascending expert
     // id): every wave converts 1/8 of them into LDS; their loads go first
     const int tot = nv * inter;
     const int c0 = w * (tot / kRedWaves), c1 = c0 + tot / kRedWaves;
     Fp8Share<kRedShareRounds> hr;
-    share_load_fp8(hr, hq, hs, c0, c1, lane);
+    share_load_ranked(hr, hq, hs, rp, inter, c0, c1, lane);
     mem_order();
 
     // work units (pick, K part): a wave streams 16 rows of one expert's w2
@@ -476,7 +561,7 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const bool has = w < nunits;
     int p = has ? w / ksplit : 0, ksp = has ? w % ksplit : 0, k0 = 0, k1 = 0;
     if (has) k_part(ksteps, ksp, ksplit, k0, k1);
-    const int e0 = wave_expert_of_rank(wp, p);
+    const int e0 = __builtin_amdgcn_readlane(rp.e, p);
     Fp4Band band = fp4_band(w2 + (size_t)e0 * wmat, s2 + (size_t)e0 * smat, blockIdx.x, inter,
                             lane);
     Fp4Stage s0, s1;
@@ -506,7 +591,7 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
         p = unit / ksplit;
         ksp = unit % ksplit;
         k_part(ksteps, ksp, ksplit, k0, k1);
-        const int e = wave_expert_of_rank(wp, p);
+        const int e = __builtin_amdgcn_readlane(rp.e, p);
         band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter, lane);
         fp4_load(s0, band, k0, k1);
         fp4_load(s1, band, k0 + kU, k1);
@@ -546,17 +631,13 @@ static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 using namespace ws;
 
-extern "C" {
-
-}  // extern "C"
-
 namespace ws {
 
-static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf,
-                      const int32_t *topk_idx, const float *topk_w, const RouteArgs *ra,
-                      const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
-                      uint8_t *hq, uint8_t *hs, int64_t dim, int64_t inter, int64_t n_experts,
-                      int64_t top_k, float swiglu_limit, hipStream_t stream) {
+static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf, const PickSrc &ps,
+                      const RouteArgs *ra, const uint8_t *w1, const uint8_t *s1,
+                      const uint8_t *w3, const uint8_t *s3, uint8_t *hq, uint8_t *hs, float *hf,
+                      int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                      float swiglu_limit, hipStream_t stream) {
     // two tiles per workgroup when that still gives every CU a workgroup:
     // one resident round of 8-wave workgroups, each wave streaming whole K rows
     const int tpw = (inter / 32) * top_k >= 512 ? 2 : 1;
@@ -564,33 +645,35 @@ static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf,
     const bool exact = math_mode() == WS_MATH_EXACT;
     size_t lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
     const RouteArgs none{};
-#define WS_GLU(EX, XF, CPL, RA)                                                                  \
-    hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF, CPL>), grid, dim3(kDecThreads), lds,      \
-                       stream, xq, xs, xf, topk_idx, topk_w, RA, w1, s1, w3, s3, hq, hs,          \
-                       (int)dim, (int)inter, (int)n_experts, (int)top_k, swiglu_limit, tpw)
+#define WS_GLU(EX, XF, CPL, RA, HF)                                                              \
+    hipLaunchKernelGGL((expert_glu_quant_kernel<EX, XF, CPL, HF>), grid, dim3(kDecThreads), lds,  \
+                       stream, xq, xs, xf, ps, RA, w1, s1, w3, s3, hq, hs, hf, (int)dim,          \
+                       (int)inter, (int)n_experts, (int)top_k, swiglu_limit, tpw)
     if (ra) {  // routed in the kernel (f32 token)
         const int cpl = n_experts <= 128 ? 2 : n_experts <= 256 ? 4 : n_experts <= 384 ? 6
                       : n_experts <= 512 ? 8 : 16;
 #define WS_GLU_R(EX)                                                  \
         switch (cpl) {                                                \
-            case 2: WS_GLU(EX, true, 2, *ra); break;                  \
-            case 4: WS_GLU(EX, true, 4, *ra); break;                  \
-            case 6: WS_GLU(EX, true, 6, *ra); break;                  \
-            case 8: WS_GLU(EX, true, 8, *ra); break;                  \
-            default: WS_GLU(EX, true, 16, *ra); break;                \
+            case 2: WS_GLU(EX, true, 2, *ra, false); break;           \
+            case 4: WS_GLU(EX, true, 4, *ra, false); break;           \
+            case 6: WS_GLU(EX, true, 6, *ra, false); break;           \
+            case 8: WS_GLU(EX, true, 8, *ra, false); break;           \
+            default: WS_GLU(EX, true, 16, *ra, false); break;         \
         }
         if (exact) { WS_GLU_R(true) } else { WS_GLU_R(false) }
 #undef WS_GLU_R
+    } else if (hf) {  // expert_glu: e4m3 token in, f32 h out
+        if (exact) WS_GLU(true, false, 0, none, true); else WS_GLU(false, false, 0, none, true);
     } else if (exact) {
-        if (xf) WS_GLU(true, true, 0, none); else WS_GLU(true, false, 0, none);
+        if (xf) WS_GLU(true, true, 0, none, false); else WS_GLU(true, false, 0, none, false);
     } else {
-        if (xf) WS_GLU(false, true, 0, none); else WS_GLU(false, false, 0, none);
+        if (xf) WS_GLU(false, true, 0, none, false); else WS_GLU(false, false, 0, none, false);
     }
 #undef WS_GLU
     return launch_status();
 }
 
-static int reduce_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
+static int reduce_launch(const uint8_t *hq, const uint8_t *hs, const ReducePicks &pk,
                          const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
                          int64_t inter, int64_t n_experts, int64_t top_k, hipStream_t stream) {
     const bool exact = math_mode() == WS_MATH_EXACT;
@@ -599,18 +682,124 @@ static int reduce_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *to
     dim3 grid((unsigned)(dim / 16));
     if (exact)
         hipLaunchKernelGGL(expert_reduce_kernel<true>, grid, dim3(kRedThreads), lds, stream, hq,
-                           hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
-                           (int)top_k);
+                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k);
     else
         hipLaunchKernelGGL(expert_reduce_kernel<false>, grid, dim3(kRedThreads), lds, stream, hq,
-                           hs, topk_idx, w2, s2, y, (int)dim, (int)inter, (int)n_experts,
-                           (int)top_k);
+                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k);
     return launch_status();
+}
+
+// moe_local_slots (moe_grouped.cu:23-58): one wave; lane s < top_k holds gate
+// slot s; the picks in [e_start, e_start + e_len) are ranked by (expert id,
+// slot), the order of the reference's stable insertion sort.
+__global__ __launch_bounds__(64) void local_slots_kernel(const int32_t *gate_idx,
+                                                         int32_t *local_slots,
+                                                         int32_t *local_experts,
+                                                         int32_t *local_count, int top_k,
+                                                         int e_start, int e_len) {
+    const int lane = threadIdx.x;
+    const int e = lane < top_k ? gate_idx[lane] : 0;
+    const bool in = lane < top_k && e >= e_start && e - e_start < e_len;
+    int rank = 0;
+    for (int i = 0; i < top_k; i++) {
+        const int ei = __builtin_amdgcn_readlane(e, i);
+        const bool vi = ei >= e_start && ei - e_start < e_len;
+        rank += (vi && (ei < e || (ei == e && i < lane))) ? 1 : 0;
+    }
+    if (in) {
+        local_slots[rank] = lane;
+        local_experts[rank] = e - e_start;
+    }
+    const int n = __popcll(__ballot(in));
+    if (lane == 0) *local_count = n;
+}
+
+// moe_dispatch_ids (moe_grouped.cu:226-236): local expert row or -1, int64
+__global__ __launch_bounds__(64) void dispatch_ids_kernel(const int32_t *gate_idx,
+                                                          int64_t *dispatch_idx, int top_k,
+                                                          int e_start, int e_len) {
+    const int s = blockIdx.x * 64 + threadIdx.x;
+    if (s >= top_k) return;
+    const int e = gate_idx[s];
+    dispatch_idx[s] = (e >= e_start && e - e_start < e_len) ? (int64_t)(e - e_start) : -1;
+}
+
+// expert_quant (moe_grouped.cu:128-162): the FP8 1x32 emit of each local
+// slot's h row; one 32-lane group per 1x32 block.
+__global__ __launch_bounds__(256) void expert_quant_kernel(const float *h, const int32_t *local,
+                                                           const int32_t *local_count,
+                                                           uint8_t *q, uint8_t *sc, int n,
+                                                           int top_k) {
+    const int i = blockIdx.y;
+    if (i >= min(*local_count, top_k)) return;
+    const int slot = local[i];
+    if (slot < 0 || slot >= top_k) return;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const bool live = c < n;
+    const size_t at = (size_t)slot * n + min(c, n - 1);
+    uint32_t sb;
+    const uint32_t qb = quant_fp8_block32(h[at], &sb);
+    if (live) {
+        q[at] = (uint8_t)qb;
+        if ((c & 31) == 0) sc[at / 32] = (uint8_t)sb;
+    }
 }
 
 }  // namespace ws
 
 extern "C" {
+
+int ws_moe_local_slots(const int32_t *gate_idx, int32_t *local_slots, int32_t *local_experts,
+                       int32_t *local_count, int64_t top_k, int64_t e_start, int64_t e_len,
+                       ws_stream_t stream) {
+    if (!gate_idx || !local_slots || !local_experts || !local_count) return WS_ERR_INVALID_ARG;
+    if (top_k <= 0 || e_start < 0 || e_len <= 0) return WS_ERR_INVALID_ARG;
+    if (top_k > kMaxTopkDec || e_start + e_len > (1 << 30)) return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(local_slots_kernel, dim3(1), dim3(64), 0, stream, gate_idx, local_slots,
+                       local_experts, local_count, (int)top_k, (int)e_start, (int)e_len);
+    return launch_status();
+}
+
+int ws_moe_dispatch_ids(const int32_t *gate_idx, int64_t *dispatch_idx, int64_t top_k,
+                        int64_t e_start, int64_t e_len, ws_stream_t stream) {
+    if (!gate_idx || !dispatch_idx || top_k <= 0 || e_start < 0 || e_len <= 0)
+        return WS_ERR_INVALID_ARG;
+    if (top_k > (1 << 24) || e_start + e_len > (1 << 30)) return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(dispatch_ids_kernel, dim3((unsigned)((top_k + 63) / 64)), dim3(64), 0,
+                       stream, gate_idx, dispatch_idx, (int)top_k, (int)e_start, (int)e_len);
+    return launch_status();
+}
+
+int ws_expert_glu(const uint8_t *act_x, const uint8_t *act_x_s, const uint8_t *w1,
+                  const uint8_t *w1_s, const uint8_t *w3, const uint8_t *w3_s,
+                  const float *route_w, const int32_t *local_slots,
+                  const int32_t *local_experts, const int32_t *local_count, float *h_slots,
+                  int64_t n, int64_t k, int64_t top_k, int64_t e_len, ws_stream_t stream) {
+    if (!act_x || !act_x_s || !w1 || !w1_s || !w3 || !w3_s || !route_w || !local_slots ||
+        !local_experts || !local_count || !h_slots)
+        return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(k, n, e_len, top_k);
+    if (rc) return rc;
+    if (!aligned16(act_x) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)w1_s & 7) ||
+        ((uintptr_t)w3_s & 7) || ((uintptr_t)h_slots & 3))
+        return WS_ERR_INVALID_ARG;
+    const PickSrc ps{nullptr, route_w, local_slots, local_experts, local_count};
+    return glu_launch(act_x, act_x_s, nullptr, ps, nullptr, w1, w1_s, w3, w3_s, nullptr, nullptr,
+                      h_slots, k, n, e_len, top_k, 10.0f, stream);
+}
+
+int ws_expert_quant(const float *h_slots, const int32_t *local_slots, const int32_t *local_count,
+                    uint8_t *q_slots, uint8_t *s_slots, int64_t n, int64_t top_k,
+                    ws_stream_t stream) {
+    if (!h_slots || !local_slots || !local_count || !q_slots || !s_slots)
+        return WS_ERR_INVALID_ARG;
+    if (n <= 0 || top_k <= 0) return WS_ERR_INVALID_ARG;
+    if (n % 32 || top_k > kMaxTopkDec || n > (1 << 24)) return WS_ERR_SHAPE;
+    dim3 grid((unsigned)((n + 255) / 256), (unsigned)top_k);
+    hipLaunchKernelGGL(expert_quant_kernel, grid, dim3(256), 0, stream, h_slots, local_slots,
+                       local_count, q_slots, s_slots, (int)n, (int)top_k);
+    return launch_status();
+}
 
 int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *topk_idx,
                         const float *topk_w, const uint8_t *w1, const uint8_t *s1,
@@ -624,8 +813,9 @@ int ws_expert_glu_quant(const uint8_t *xq, const uint8_t *xs, const int32_t *top
     if (!aligned16(xq) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
         ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
-    return glu_launch(xq, xs, nullptr, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
-                      inter, n_experts, top_k, swiglu_limit, stream);
+    const PickSrc ps{topk_idx, topk_w, nullptr, nullptr, nullptr};
+    return glu_launch(xq, xs, nullptr, ps, nullptr, w1, s1, w3, s3, hq, hs, nullptr, dim, inter,
+                      n_experts, top_k, swiglu_limit, stream);
 }
 
 int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *topk_w,
@@ -641,7 +831,8 @@ int ws_expert_glu_quant_x(const float *x, const int32_t *topk_idx, const float *
     if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || ((uintptr_t)s1 & 7) ||
         ((uintptr_t)s3 & 7))
         return WS_ERR_INVALID_ARG;
-    return glu_launch(nullptr, nullptr, x, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
+    const PickSrc ps{topk_idx, topk_w, nullptr, nullptr, nullptr};
+    return glu_launch(nullptr, nullptr, x, ps, nullptr, w1, s1, w3, s3, hq, hs, nullptr, dim,
                       inter, n_experts, top_k, swiglu_limit, stream);
 }
 
@@ -665,18 +856,25 @@ int ws_expert_glu_quant_route(const float *logits, const float *bias, int score_
         return WS_ERR_INVALID_ARG;
     const RouteArgs ra{logits, bias, score_func, gate_temp, norm_topk_prob, route_scale,
                        topk_idx, topk_w};
-    return glu_launch(nullptr, nullptr, x, nullptr, nullptr, &ra, w1, s1, w3, s3, hq, hs, dim,
+    return glu_launch(nullptr, nullptr, x, PickSrc{}, &ra, w1, s1, w3, s3, hq, hs, nullptr, dim,
                       inter, n_experts, top_k, swiglu_limit, stream);
 }
 
-int ws_expert_reduce(const uint8_t *hq, const uint8_t *hs, const int32_t *topk_idx,
-                     const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim, int64_t inter,
-                     int64_t n_experts, int64_t top_k, ws_stream_t stream) {
-    if (!hq || !hs || !topk_idx || !w2 || !s2 || !y) return WS_ERR_INVALID_ARG;
-    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+int ws_expert_reduce(const uint8_t *act_slots, const uint8_t *act_s_slots, const uint8_t *w2,
+                     const uint8_t *w2_s, const int32_t *gate_idx, const int32_t *local_slots,
+                     const int32_t *local_count, float *y, int64_t dim, int64_t inter,
+                     int64_t top_k, int64_t e_start, int64_t e_len, ws_stream_t stream) {
+    if (!act_slots || !act_s_slots || !w2 || !w2_s || !gate_idx || !local_slots || !local_count ||
+        !y)
+        return WS_ERR_INVALID_ARG;
+    if (e_start < 0) return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, e_len, top_k);
     if (rc) return rc;
-    if (!aligned16(hq) || !aligned16(w2) || ((uintptr_t)s2 & 7)) return WS_ERR_INVALID_ARG;
-    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+    if (!aligned16(act_slots) || !aligned16(w2) || ((uintptr_t)w2_s & 7))
+        return WS_ERR_INVALID_ARG;
+    const ReducePicks pk{gate_idx, local_slots, local_count, (int)e_start};
+    return reduce_launch(act_slots, act_s_slots, pk, w2, w2_s, y, dim, inter, e_len, top_k,
+                         stream);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -707,18 +905,21 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, 
     uint8_t *hs = hq + align256(top_k * inter);
     if (dim <= kMaxDimF32) {
         // the gate/up kernel quantises x itself (the act_quant_fp8_emit rule)
-        rc = glu_launch(nullptr, nullptr, x, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs,
-                        dim, inter, n_experts, top_k, swiglu_limit, stream);
+        rc = glu_launch(nullptr, nullptr, x, PickSrc{topk_idx, topk_w, nullptr, nullptr, nullptr},
+                        nullptr, w1, s1, w3, s3, hq, hs, nullptr, dim, inter, n_experts, top_k,
+                        swiglu_limit, stream);
     } else {
         uint8_t *xq = hs + align256(top_k * (inter / 32));
         uint8_t *xs = xq + align256(dim);
         rc = ws_emit8(x, xq, xs, dim, stream);
         if (rc) return rc;
-        rc = glu_launch(xq, xs, nullptr, topk_idx, topk_w, nullptr, w1, s1, w3, s3, hq, hs, dim,
-                        inter, n_experts, top_k, swiglu_limit, stream);
+        rc = glu_launch(xq, xs, nullptr, PickSrc{topk_idx, topk_w, nullptr, nullptr, nullptr},
+                        nullptr, w1, s1, w3, s3, hq, hs, nullptr, dim, inter, n_experts, top_k,
+                        swiglu_limit, stream);
     }
     if (rc) return rc;
-    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+    return reduce_launch(hq, hs, ReducePicks{topk_idx, nullptr, nullptr, 0}, w2, s2, y, dim, inter,
+                         n_experts, top_k, stream);
 }
 
 int ws_moe_decode_route(const float *logits, const float *bias, int score_func, float gate_temp,
@@ -753,10 +954,11 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
     uint8_t *hs = hq + align256(top_k * inter);
     const RouteArgs ra{logits, bias, score_func, gate_temp, norm_topk_prob, route_scale,
                        topk_idx, topk_w};
-    rc = glu_launch(nullptr, nullptr, x, nullptr, nullptr, &ra, w1, s1, w3, s3, hq, hs, dim, inter,
-                    n_experts, top_k, swiglu_limit, stream);
+    rc = glu_launch(nullptr, nullptr, x, PickSrc{}, &ra, w1, s1, w3, s3, hq, hs, nullptr, dim,
+                    inter, n_experts, top_k, swiglu_limit, stream);
     if (rc) return rc;
-    return reduce_launch(hq, hs, topk_idx, w2, s2, y, dim, inter, n_experts, top_k, stream);
+    return reduce_launch(hq, hs, ReducePicks{topk_idx, nullptr, nullptr, 0}, w2, s2, y, dim, inter,
+                         n_experts, top_k, stream);
 }
 
 }  // extern "C"

@@ -30,8 +30,18 @@ constexpr int kMaxExpertsG = 1024;
 constexpr int kTile = 32;
 
 // ---- dispatch (one workgroup) -------------------------------------------
+// An expert id as the dispatch sees it: ids outside [0, E) (a pick another
+// rank owns, -1 from moe_dispatch_ids) all become -1.
+__device__ __forceinline__ int id_of(int32_t v, int n_experts) {
+    return v >= 0 && v < n_experts ? v : -1;
+}
+__device__ __forceinline__ int id_of(int64_t v, int n_experts) {
+    return v >= 0 && v < n_experts ? (int)v : -1;
+}
+
+template <typename IdxT>
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
-    const int32_t *__restrict__ idx, const float *__restrict__ wts, int32_t *__restrict__ order,
+    const IdxT *__restrict__ idx, const float *__restrict__ wts, int32_t *__restrict__ order,
     float *__restrict__ layout_w, int32_t *__restrict__ route_pos,
     int32_t *__restrict__ tile_expert, int32_t *__restrict__ count_out,
     int32_t *__restrict__ offset_out, int32_t *__restrict__ psum_out,
@@ -61,7 +71,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     // pass 1: stable rank of every route inside its expert
     for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
         const int r = c0 + t;
-        const int e = r < routes ? idx[r] : -1;
+        const int e = r < routes ? id_of(idx[r], n_experts) : -1;
         const bool valid = e >= 0 && e < n_experts;
 #pragma unroll
         for (int ww = 0; ww < kDispThreads / 64; ww++) wcnt[ww][t] = 0;
@@ -134,7 +144,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
         const int r = c0 + t;
         if (r >= routes) break;
-        const int e = idx[r];
+        const int e = id_of(idx[r], n_experts);
         if (e < 0 || e >= n_experts) {
             route_pos[r] = -1;
             continue;
@@ -497,12 +507,18 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 // bands), so each output is one wave's sum and is written straight from
 // registers. f32 out[slot, dim]. With CB == 2 and dim % 256 == 128 the last
 // unit's upper waves have no band (clamped loads, no stores).
-template <bool EXACT, int CB>
+//
+// GATHER (the gate/up form of moe_grouped_tl): the A rows are the tokens of
+// the tile's routes, row order[slot] / top_k of hq (< tokens), instead of the
+// slot rows. num_tiles == nullptr: the used tiles are counted from
+// tile_expert (the dispatch puts them first, the rest hold -1), as a caller
+// of the reference's grouped GEMM passes no count.
+template <bool EXACT, int CB, bool GATHER = false>
 __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
     const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ order,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
-    int dim, int inter, int n_experts) {
+    int dim, int inter, int n_experts, int tiles, int top_k, int tokens) {
     extern __shared__ __align__(16) uint8_t g_lds[];
     uint8_t *a_l = g_lds;                                // [32][inter + 16]
     uint8_t *as_l = g_lds + g_a_lds(kTile, inter);      // [32][inter/32] (+ padding)
@@ -513,7 +529,17 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     cs.k1 = inter / 128;
     cs.nch = (cs.k1 + kU - 1) / kU;
     const int NT = (dim + 128 * CB - 1) / (128 * CB), nbands = dim / 16;
-    const int units = *num_tiles * NT;
+    int used;
+    if (num_tiles) {
+        used = *num_tiles;
+    } else {
+        used = 0;
+        for (int c = 0; c < tiles; c += 64) {
+            const bool u = c + lane < tiles && tile_expert[min(c + lane, tiles - 1)] >= 0;
+            used += __popcll(__ballot(u));
+        }
+    }
+    const int units = used * NT;
     cs.u0 = (int)((long)blockIdx.x * units / gridDim.x);
     const int u1 = (int)((long)(blockIdx.x + 1) * units / gridDim.x);
     if (cs.u0 >= u1) return;  // whole workgroup
@@ -547,14 +573,24 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
         const int slot0 = tile * kTile;
         if (c == 0) {
             if (tile != cur_tile) {  // uniform: stage the tile's hq rows in LDS
+                int my_row = 0;
                 if (order) {
-                    const bool has = lane < kTile && order[slot0 + min(lane, kTile - 1)] >= 0;
+                    const int route = order[slot0 + min(lane, kTile - 1)];
+                    const bool has = lane < kTile && route >= 0;
                     real = (uint32_t)__ballot(has);
+                    if (GATHER) my_row = has ? min(route / top_k, tokens - 1) : 0;
                 }
                 lds_barrier();       // every wave is done with the previous tile
-                g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
-                           [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); },
-                           (real >> 16) == 0 ? 16 : kTile, inter, w, lane, a_l, as_l);
+                if (GATHER)
+                    g_dma_tile([&](int i) { return hq + (size_t)__shfl(my_row, i, 64) * inter; },
+                               [&](int i) {
+                                   return hs + (size_t)__shfl(my_row, i, 64) * (inter / 32);
+                               },
+                               (real >> 16) == 0 ? 16 : kTile, inter, w, lane, a_l, as_l);
+                else
+                    g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
+                               [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); },
+                               (real >> 16) == 0 ? 16 : kTile, inter, w, lane, a_l, as_l);
                 __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
                 lds_barrier();
                 cur_tile = tile;
@@ -628,6 +664,27 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     y[(size_t)row * dim + d] = acc;
 }
 
+// moe_swiglu_route (moe_grouped.cu:239-256): out = silu(min(g,10)) *
+// clamp(u,-10,10) * w[row], 0 where w[row] == 0 (padding slots); silu in
+// weightstream-ref num.rs:71-79 order on the exact expf.
+__global__ __launch_bounds__(256) void swiglu_route_kernel(const float *__restrict__ gate,
+                                                           const float *__restrict__ up,
+                                                           const float *__restrict__ lw,
+                                                           float *out, int inter) {
+    const int row = blockIdx.y;
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= inter) return;
+    const size_t i = (size_t)row * inter + n;
+    const float wr = lw[row];
+    if (wr == 0.0f) {
+        out[i] = 0.0f;
+        return;
+    }
+    const float g = fminf(gate[i], 10.0f);
+    const float u = rclamp(up[i], -10.0f, 10.0f);
+    out[i] = ws_silu(g) * u * wr;
+}
+
 static inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 static inline bool al4(const void *p) { return ((uintptr_t)p & 3) == 0; }
 static inline bool al8(const void *p) { return ((uintptr_t)p & 7) == 0; }
@@ -660,10 +717,28 @@ static int dispatch_launch(const int32_t *topk_idx, const float *topk_w, int32_t
                            int64_t n_experts, const float *xf, uint8_t *xq, uint8_t *xs,
                            int64_t nx, ws_stream_t stream) {
     const int64_t qblocks = (nx + kDispThreads - 1) / kDispThreads;
-    hipLaunchKernelGGL(dispatch_kernel, dim3((unsigned)(1 + qblocks)), dim3(kDispThreads), 0,
-                       stream, topk_idx, topk_w, order, layout_w, route_pos, tile_expert,
+    hipLaunchKernelGGL(dispatch_kernel<int32_t>, dim3((unsigned)(1 + qblocks)), dim3(kDispThreads),
+                       0, stream, topk_idx, topk_w, order, layout_w, route_pos, tile_expert,
                        expert_count, expert_offset, expert_psum, num_tiles, (int)(rows * top_k),
                        (int)tiles, (int)n_experts, xf, xq, xs, nx);
+    return launch_status();
+}
+
+int ws_moe_dispatch_tl(const int64_t *topk_idx, const float *topk_weights, int32_t *order,
+                       float *layout_weights, int32_t *route_pos, int32_t *tile_expert,
+                       int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
+                       int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
+                       int64_t n_experts, ws_stream_t stream) {
+    if (!topk_idx || !topk_weights || !order || !layout_weights || !route_pos || !tile_expert ||
+        !expert_count || !expert_offset || !expert_psum || !num_tiles)
+        return WS_ERR_INVALID_ARG;
+    if (rows <= 0 || top_k <= 0 || tiles <= 0 || n_experts <= 0) return WS_ERR_INVALID_ARG;
+    if (n_experts > kMaxExpertsG || rows * top_k > (1 << 26) || tiles > (1 << 24))
+        return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(dispatch_kernel<int64_t>, dim3(1), dim3(kDispThreads), 0, stream, topk_idx,
+                       topk_weights, order, layout_weights, route_pos, tile_expert, expert_count,
+                       expert_offset, expert_psum, num_tiles, (int)(rows * top_k), (int)tiles,
+                       (int)n_experts, nullptr, nullptr, nullptr, (int64_t)0);
     return launch_status();
 }
 
@@ -739,34 +814,70 @@ int ws_moe_grouped_down(const uint8_t *hq, const uint8_t *hs, const int32_t *til
                                n_experts, tiles, stream);
 }
 
-// order == nullptr: every slot of a used tile is computed and written
-static int grouped_down_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+// order == nullptr: every slot of a used tile is computed and written.
+// gather: A rows are the routes' tokens (order[slot] / top_k) of hq.
+static int grouped_gemm_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
                                const int32_t *num_tiles, const int32_t *order, const uint8_t *w2,
                                const uint8_t *s2, float *out, int64_t dim, int64_t inter,
-                               int64_t n_experts, int64_t tiles, ws_stream_t stream) {
+                               int64_t n_experts, int64_t tiles, bool gather, int64_t top_k,
+                               int64_t tokens, ws_stream_t stream) {
     const size_t lds = g_tile_lds(kTile, (int)inter);
     dim3 grid((unsigned)cu_count());
-#define WS_DOWN(E, CB)                                                                         \
-    hipLaunchKernelGGL((grouped_down_kernel<E, CB>), grid, dim3(kGThreads), lds, stream, hq, hs, \
-                       tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,        \
-                       (int)n_experts)
+#define WS_DOWN(E, CB, G)                                                                      \
+    hipLaunchKernelGGL((grouped_down_kernel<E, CB, G>), grid, dim3(kGThreads), lds, stream, hq,  \
+                       hs, tile_expert, num_tiles, order, w2, s2, out, (int)dim, (int)inter,    \
+                       (int)n_experts, (int)tiles, (int)top_k, (int)tokens)
     const bool wide = wide_units(tiles);
     if (math_mode() == WS_MATH_EXACT) {
-        if (wide) WS_DOWN(true, 2); else WS_DOWN(true, 1);
+        if (gather) { if (wide) WS_DOWN(true, 2, true); else WS_DOWN(true, 1, true); }
+        else if (wide) WS_DOWN(true, 2, false); else WS_DOWN(true, 1, false);
     } else {
-        if (wide) WS_DOWN(false, 2); else WS_DOWN(false, 1);
+        if (gather) { if (wide) WS_DOWN(false, 2, true); else WS_DOWN(false, 1, true); }
+        else if (wide) WS_DOWN(false, 2, false); else WS_DOWN(false, 1, false);
     }
 #undef WS_DOWN
     return launch_status();
 }
 
-int ws_moe_combine(const float *down, const int32_t *route_pos, float *y, int64_t rows,
-                   int64_t dim, int64_t top_k, int64_t tiles, ws_stream_t stream) {
-    if (!down || !route_pos || !y) return WS_ERR_INVALID_ARG;
+static int grouped_down_launch(const uint8_t *hq, const uint8_t *hs, const int32_t *tile_expert,
+                               const int32_t *num_tiles, const int32_t *order, const uint8_t *w2,
+                               const uint8_t *s2, float *out, int64_t dim, int64_t inter,
+                               int64_t n_experts, int64_t tiles, ws_stream_t stream) {
+    return grouped_gemm_launch(hq, hs, tile_expert, num_tiles, order, w2, s2, out, dim, inter,
+                               n_experts, tiles, false, 1, 1, stream);
+}
+
+int ws_moe_grouped_tl(int kind, const uint8_t *a, const uint8_t *sfa, const uint8_t *weights,
+                      const uint8_t *sfb, const int32_t *order, const int32_t *tile_expert,
+                      float *out, int64_t tiles, int64_t tokens, int64_t top_k, int64_t n,
+                      int64_t k, int64_t n_experts, ws_stream_t stream) {
+    if (!a || !sfa || !weights || !sfb || !order || !tile_expert || !out)
+        return WS_ERR_INVALID_ARG;
+    if (kind != WS_TL_MOE_GATE_UP && kind != WS_TL_MOE_DOWN) return WS_ERR_INVALID_ARG;
+    if (tiles <= 0 || tokens <= 0 || top_k <= 0 || n <= 0 || k <= 0 || n_experts <= 0)
+        return WS_ERR_INVALID_ARG;
+    if (n % 128 || k % 128 || tiles > 65535 || k > 4096 || n > (1 << 20)) return WS_ERR_SHAPE;
+    if (!al16(a) || !al16(weights) || !al4(sfa) || !al8(sfb)) return WS_ERR_INVALID_ARG;
+    return grouped_gemm_launch(a, sfa, tile_expert, nullptr, order, weights, sfb, out, n, k,
+                               n_experts, tiles, kind == WS_TL_MOE_GATE_UP, top_k, tokens, stream);
+}
+
+int ws_moe_swiglu_route(const float *gate, const float *up, const float *weights, float *out,
+                        int64_t inter, int64_t rows, ws_stream_t stream) {
+    if (!gate || !up || !weights || !out || inter <= 0 || rows <= 0) return WS_ERR_INVALID_ARG;
+    if (rows > 65535 || inter > (1 << 24)) return WS_ERR_SHAPE;
+    hipLaunchKernelGGL(swiglu_route_kernel, dim3((unsigned)((inter + 255) / 256), (unsigned)rows),
+                       dim3(256), 0, stream, gate, up, weights, out, (int)inter);
+    return launch_status();
+}
+
+int ws_moe_combine_f32(const float *y, const int32_t *route_pos, float *out, int64_t dim,
+                       int64_t top_k, int64_t rows, int64_t tiles, ws_stream_t stream) {
+    if (!y || !route_pos || !out) return WS_ERR_INVALID_ARG;
     if (rows <= 0 || dim <= 0 || top_k <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
     if (top_k > 16 || rows > 65535) return WS_ERR_SHAPE;
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((dim + 255) / 256), (unsigned)rows),
-                       dim3(256), 0, stream, down, route_pos, y, (int)dim, (int)top_k,
+                       dim3(256), 0, stream, y, route_pos, out, (int)dim, (int)top_k,
                        (int)(tiles * kTile));
     return launch_status();
 }
@@ -830,7 +941,7 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
     rc = grouped_down_launch(hq, hs, tile_expert, ntiles, order, w2, s2, down, dim, inter,
                              n_experts, tiles, stream);
     if (rc) return rc;
-    return ws_moe_combine(down, route_pos, y, rows, dim, top_k, tiles, stream);
+    return ws_moe_combine_f32(down, route_pos, y, dim, top_k, rows, tiles, stream);
 }
 
 }  // extern "C"

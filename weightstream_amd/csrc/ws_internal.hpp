@@ -17,7 +17,8 @@ inline int launch_status() {
     return e == hipSuccess ? WS_OK : (int)e;
 }
 
-// Math mode chosen by ws_set_math_mode (WS_MATH_EXACT by default).
+// Math mode of this library build (math_mode.hip: WS_MATH_EXACT in
+// libweightstream_hip.so, WS_MATH_NATIVE in libweightstream_hip_native.so).
 int math_mode();
 
 // Compute units of the current device (queried once per device).

@@ -44,18 +44,30 @@ def built_with_hip():
 
 MATH_EXACT, MATH_NATIVE = 0, 1
 
+# Which library build the calls below go to. The math mode is fixed inside
+# each library (no C-side state); this host-side choice only picks the build.
+_mode = threading.local()
+
+
+def _native():
+    return getattr(_mode, "native", False)
+
 
 def set_math_mode(mode):
-    """WS_MATH_EXACT (bf16 MFMA on exactly dequantised operands, default) or
-    WS_MATH_NATIVE (FP8/MXFP4 scaled MFMA). Returns the previous mode."""
-    prev = _lib.load().ws_set_math_mode(int(mode))
-    if prev < 0:
+    """Route this thread's later calls to the EXACT library
+    (libweightstream_hip.so, bf16 MFMA on exactly dequantised operands) or to
+    the NATIVE build (FP8/MXFP4 scaled MFMA). Returns the previous mode."""
+    if mode not in (MATH_EXACT, MATH_NATIVE):
         raise ValueError("unknown math mode %r" % (mode,))
+    prev = MATH_NATIVE if _native() else MATH_EXACT
+    _mode.native = mode == MATH_NATIVE
+    _lib.load(native=_mode.native)
     return prev
 
 
 def get_math_mode():
-    return _lib.load().ws_get_math_mode()
+    """The math mode of the library the calls go to (asked of the library)."""
+    return _lib.load(native=_native()).ws_get_math_mode()
 
 
 class math_mode:
@@ -88,7 +100,7 @@ def _s(stream):
 
 
 def _call(name, *args):
-    fn = getattr(_lib.load(), name)
+    fn = getattr(_lib.load(native=_native()), name)
     _lib.check(name, fn(*args))
 
 
@@ -146,7 +158,9 @@ def gemm_workspace_size(m, n, k):
 
 def set_gemm_workspace(ws, stream=None):
     """Register (a uint8 device tensor) or clear (None) the split-K workspace
-    of the current device; the caller keeps `ws` alive while it is set."""
+    of `stream` (default: the current stream) on the current device; GEMMs
+    issued on that stream use it. The caller keeps `ws` alive while it is
+    set."""
     if ws is None:
         _call("ws_set_gemm_workspace", None, 0, _s(stream))
     else:
@@ -165,6 +179,31 @@ def fp8_gemm_on(a, sa, b, sb, out, m, n, k, stream):
 def fp8_gemm_tile(a, sa, b, sb, out, m, n, k, stream=None):
     _call("ws_fp8_gemm_tile", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k,
           _s(stream))
+
+
+# launch.rs:325-339 TlGemm kinds: (N, K) hard-coded per TileLang kernel
+TL_QA, TL_QB, TL_WKV, TL_WO_A, TL_WO_B, TL_SHARED_W13, TL_SHARED_W13_FUSED, TL_SHARED_W2, \
+    TL_ENGRAM_WKV, TL_DRAFTER_MAIN_PROJ = range(10)
+
+
+def tl_gemm_shape(kind):
+    """(N, K) of a TlGemm kind."""
+    import ctypes
+    n, k = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check("ws_tl_gemm_shape", _lib.load().ws_tl_gemm_shape(kind, ctypes.byref(n),
+                                                                 ctypes.byref(k)))
+    return n.value, k.value
+
+
+def fp8_gemm_tl(kind, a, sa, b, sb, out, m, stream=None):
+    """launch.rs:341 fp8_gemm_tl: sa = the activation's packed scale words,
+    sb = the weight's packed per-row scale table (pack_weight_scales)."""
+    _call("ws_fp8_gemm_tl", int(kind), _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m,
+          _s(stream))
+
+
+def fp8_gemm_tl_on(kind, a, sa, b, sb, out, m, stream):
+    fp8_gemm_tl(kind, a, sa, b, sb, out, m, stream=stream)
 
 
 def fp8_gemm_bf16(a, sa, b, sb, out, m, n, k, stream=None):
@@ -256,10 +295,48 @@ def shared_expert_fp8(x, w1, s1, w3, s3, w2, s2, y, m, dim, inter, workspace,
 
 
 # ---- routed experts, decode (launch.rs:89-206) ---------------------------------
+def moe_local_slots(gate_idx, local_slots, local_experts, local_count, top_k, e_start, e_len,
+                    stream=None):
+    """launch.rs:89: the gate's picks in [e_start, e_start + e_len), ascending
+    expert id, as slot indices and local expert rows."""
+    _call("ws_moe_local_slots", _ptr(gate_idx), _ptr(local_slots), _ptr(local_experts),
+          _ptr(local_count), top_k, e_start, e_len, _s(stream))
+
+
+def moe_dispatch_ids(gate_idx, dispatch_idx, top_k, e_start, e_len, stream=None):
+    """launch.rs:658: int64 local expert rows (-1: another rank's)."""
+    _call("ws_moe_dispatch_ids", _ptr(gate_idx), _ptr(dispatch_idx), top_k, e_start, e_len,
+          _s(stream))
+
+
+def expert_glu(act_x, act_x_s, w1, w1_s, w3, w3_s, route_w, local_slots, local_experts,
+               local_count, h_slots, n, k, top_k, e_len, stream=None):
+    """launch.rs:116: f32 h of each local slot (packed w1 / w3 slabs of e_len
+    experts)."""
+    _call("ws_expert_glu", _ptr(act_x), _ptr(act_x_s), _ptr(w1), _ptr(w1_s), _ptr(w3),
+          _ptr(w3_s), _ptr(route_w), _ptr(local_slots), _ptr(local_experts), _ptr(local_count),
+          _ptr(h_slots), n, k, top_k, e_len, _s(stream))
+
+
+def expert_quant(h_slots, local_slots, local_count, q_slots, s_slots, n, top_k, stream=None):
+    """launch.rs:148: FP8 1x32 emit of each local slot's h row."""
+    _call("ws_expert_quant", _ptr(h_slots), _ptr(local_slots), _ptr(local_count), _ptr(q_slots),
+          _ptr(s_slots), n, top_k, _s(stream))
+
+
+def expert_reduce(act_slots, act_s_slots, w2, w2_s, gate_idx, local_slots, local_count, y, dim,
+                  inter, top_k, e_start, e_len, stream=None):
+    """launch.rs:178: y = sum over local_slots (ascending expert id) of
+    w2_e . h_slot."""
+    _call("ws_expert_reduce", _ptr(act_slots), _ptr(act_s_slots), _ptr(w2), _ptr(w2_s),
+          _ptr(gate_idx), _ptr(local_slots), _ptr(local_count), _ptr(y), dim, inter, top_k,
+          e_start, e_len, _s(stream))
+
+
 def expert_glu_quant(act_x, act_x_s, topk_idx, topk_w, w1, w1_s, w3, w3_s, q_slots, s_slots,
                      n, k, n_experts, top_k, swiglu_limit=10.0, stream=None):
-    """expert_glu + expert_quant fused: rows of q_slots/s_slots are the picks
-    in ascending expert id."""
+    """expert_glu + expert_quant fused for the picks of the top-k output: row p
+    of q_slots / s_slots is pick p."""
     _call("ws_expert_glu_quant", _ptr(act_x), _ptr(act_x_s), _ptr(topk_idx), _ptr(topk_w),
           _ptr(w1), _ptr(w1_s), _ptr(w3), _ptr(w3_s), _ptr(q_slots), _ptr(s_slots), k, n,
           n_experts, top_k, swiglu_limit, _s(stream))
@@ -282,12 +359,6 @@ def expert_glu_quant_route(logits, bias, score_func, gate_temp, norm_topk_prob, 
           int(norm_topk_prob), float(route_scale), _ptr(x), _ptr(w1), _ptr(s1), _ptr(w3),
           _ptr(s3), _ptr(hq), _ptr(hs), _ptr(topk_idx), _ptr(topk_w), dim, inter, n_experts,
           top_k, swiglu_limit, _s(stream))
-
-
-def expert_reduce(act_slots, act_s_slots, w2, w2_s, gate_idx, y, dim, inter, n_experts, top_k,
-                  stream=None):
-    _call("ws_expert_reduce", _ptr(act_slots), _ptr(act_s_slots), _ptr(gate_idx), _ptr(w2),
-          _ptr(w2_s), _ptr(y), dim, inter, n_experts, top_k, _s(stream))
 
 
 def moe_decode_workspace_size(dim, inter, top_k):
@@ -322,9 +393,34 @@ def moe_tiles(routes, n_experts):
 def moe_dispatch_tl(topk_idx, topk_weights, order, layout_weights, route_pos, tile_expert,
                     expert_count, expert_offset, expert_psum, num_tiles, rows, top_k, tiles,
                     n_experts, stream=None):
-    _call("ws_moe_dispatch", _ptr(topk_idx), _ptr(topk_weights), _ptr(order),
-          _ptr(layout_weights), _ptr(route_pos), _ptr(tile_expert), _ptr(expert_count),
-          _ptr(expert_offset), _ptr(expert_psum), _ptr(num_tiles), rows, top_k, tiles, n_experts,
+    """launch.rs:430: int64 ids (moe_dispatch_ids) go to ws_moe_dispatch_tl,
+    int32 ids (moe_topk) to ws_moe_dispatch; same outputs."""
+    name = "ws_moe_dispatch_tl" if topk_idx.dtype == torch.int64 else "ws_moe_dispatch"
+    _call(name, _ptr(topk_idx), _ptr(topk_weights), _ptr(order), _ptr(layout_weights),
+          _ptr(route_pos), _ptr(tile_expert), _ptr(expert_count), _ptr(expert_offset),
+          _ptr(expert_psum), _ptr(num_tiles), rows, top_k, tiles, n_experts, _s(stream))
+
+
+TL_MOE_GATE_UP, TL_MOE_DOWN = 0, 1
+
+
+def moe_grouped_tl(kind, a, sfa, weights, sfb, order, tile_expert, out, tiles, tokens, top_k,
+                   n, k, n_experts, stream=None):
+    """launch.rs:478-580 moe_grouped_tl(_cached)(_on): out[slot] = A row .
+    w_e^T for the used tiles; GATE_UP gathers the routes' token rows, DOWN
+    reads the slot rows. weights / sfb: a packed slab (prepack_fp4)."""
+    _call("ws_moe_grouped_tl", int(kind), _ptr(a), _ptr(sfa), _ptr(weights), _ptr(sfb),
+          _ptr(order), _ptr(tile_expert), _ptr(out), tiles, tokens, top_k, n, k, n_experts,
+          _s(stream))
+
+
+moe_grouped_tl_cached = moe_grouped_tl
+moe_grouped_tl_cached_on = moe_grouped_tl
+
+
+def moe_swiglu_route(gate, up, weights, out, inter, rows, stream=None):
+    """launch.rs:673: route-weighted SwiGLU over the grouped layout."""
+    _call("ws_moe_swiglu_route", _ptr(gate), _ptr(up), _ptr(weights), _ptr(out), inter, rows,
           _s(stream))
 
 
@@ -343,8 +439,9 @@ def moe_grouped_down(hq, hs, tile_expert, num_tiles, w2, s2, out, dim, inter, n_
 
 
 def moe_combine_f32(y, route_pos, out, dim, top_k, rows, tiles, stream=None):
-    """launch.rs:689 argument order (y = grouped down output, out = result)."""
-    _call("ws_moe_combine", _ptr(y), _ptr(route_pos), _ptr(out), rows, dim, top_k, tiles,
+    """launch.rs:689 (y = grouped down output, out = result; trailing tiles
+    bounds the slots)."""
+    _call("ws_moe_combine_f32", _ptr(y), _ptr(route_pos), _ptr(out), dim, top_k, rows, tiles,
           _s(stream))
 
 
