@@ -364,6 +364,24 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
                         float swiglu_limit, void *workspace, size_t workspace_bytes,
                         ws_stream_t stream);
 
+/* ws_moe_decode_route with no workspace argument and no allocation. No
+ * counterpart in the reference: for callers that cannot call hipMalloc or
+ * hold a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). The workspace is a fixed device array
+ * inside the library, 64 KiB per GPU, held until the process ends; it
+ * covers every shape ws_moe_decode_route accepts (WS_ERR_SHAPE beyond).
+ * Every call on one GPU shares that GPU's array: calls that may overlap on
+ * one GPU (different streams, no ordering between them) race and must not be
+ * issued; calls ordered on one stream are safe. Same results as
+ * ws_moe_decode_route. */
+int ws_moe_decode_route_noalloc(const float *logits, const float *bias, int score_func,
+                                float gate_temp, int norm_topk_prob, float route_scale,
+                                const float *x, const uint8_t *w1, const uint8_t *s1,
+                                const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                                const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                                int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                                float swiglu_limit, ws_stream_t stream);
+
 /* ---------------------------------------------------------------------
  * Routed experts, M tokens (grouped prefill / batched decode). Replaces the
  * TileLang pipeline of engine.rs:4125-4243 (moe_dispatch_tl launch.rs:430,

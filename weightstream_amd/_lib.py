@@ -97,6 +97,8 @@ SIGNATURES = {
     "ws_moe_decode": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
     "ws_moe_decode_route": (_i, [_p, _p, _i, _f, _i, _f, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                  _i64, _i64, _i64, _i64, _f, _p, C.c_size_t, _p]),
+    "ws_moe_decode_route_noalloc": (_i, [_p, _p, _i, _f, _i, _f] + [_p] * 10 +
+                                    [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_moe_dispatch": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_dispatch_tl": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _p]),
     "ws_moe_grouped_tl": (_i, [_i] + [_p] * 7 + [_i64] * 6 + [_p]),

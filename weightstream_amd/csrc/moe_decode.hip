@@ -27,6 +27,8 @@
 //    16 output rows; each also decodes 1/8 of the picks' hidden states into
 //    LDS; per-expert results meet in LDS and are added in ascending
 //    expert id, one f32 add per expert like the reference's acc_f32 chain.
+#include <mutex>
+
 #include "ws_internal.hpp"
 #include "ws_pack.hpp"
 #include "ws_route.hpp"
@@ -920,6 +922,53 @@ int ws_moe_decode(const float *x, const int32_t *topk_idx, const float *topk_w, 
     if (rc) return rc;
     return reduce_launch(hq, hs, ReducePicks{topk_idx, nullptr, nullptr, 0}, w2, s2, y, dim, inter,
                          n_experts, top_k, stream);
+}
+
+// ---- allocation-free decode step -------------------------------------------
+// Device scratch of ws_moe_decode_route_noalloc: the picks' hidden states
+// (hq, hs) and, for dim > 8192, the quantised token, laid out as the
+// ws_moe_decode workspace. Its largest use under check_decode_shapes is
+// 32768 + 1024 + 16384 + 512 bytes.
+constexpr size_t kDecodeScratchBytes = 64 << 10;
+static __device__ __align__(256) uint8_t scratch[kDecodeScratchBytes];
+
+// The device address of this device's copy of `scratch`, looked up once per
+// device with that device current (the array's name in host code is only a
+// host-side handle, not a device address). nullptr if the lookup fails.
+static uint8_t *decode_scratch() {
+    static std::mutex mu;
+    static uint8_t *ptrs[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+        ptrs[dev] = (uint8_t *)p;
+    }
+    return ptrs[dev];
+}
+
+int ws_moe_decode_route_noalloc(const float *logits, const float *bias, int score_func,
+                                float gate_temp, int norm_topk_prob, float route_scale,
+                                const float *x, const uint8_t *w1, const uint8_t *s1,
+                                const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                                const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                                int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                                float swiglu_limit, ws_stream_t stream) {
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    const size_t need = ws_moe_decode_workspace_size(dim, inter, top_k);
+    if (need == 0) return WS_ERR_INVALID_ARG;
+    if (need > kDecodeScratchBytes) return WS_ERR_SHAPE;
+    uint8_t *ws = decode_scratch();
+    if (!ws) return WS_ERR_NO_DEVICE;
+    // every byte of the scratch that a kernel reads was written by an earlier
+    // kernel of the same call (hq / hs of the valid picks, the quantised
+    // token): nothing has to start at zero
+    return ws_moe_decode_route(logits, bias, score_func, gate_temp, norm_topk_prob, route_scale, x,
+                               w1, s1, w3, s3, w2, s2, y, topk_idx, topk_w, dim, inter, n_experts,
+                               top_k, swiglu_limit, ws, kDecodeScratchBytes, stream);
 }
 
 int ws_moe_decode_route(const float *logits, const float *bias, int score_func, float gate_temp,

@@ -384,6 +384,17 @@ def moe_decode_route(logits, bias, score_func, gate_temp, norm_topk_prob, route_
           workspace.numel() * workspace.element_size(), _s(stream))
 
 
+def moe_decode_route_noalloc(logits, bias, score_func, gate_temp, norm_topk_prob, route_scale, x,
+                             w1, s1, w3, s3, w2, s2, y, topk_idx, topk_w, dim, inter, n_experts,
+                             top_k, swiglu_limit=10.0, stream=None):
+    """moe_decode_route on the library's fixed device scratch (no workspace,
+    no allocation; calls that overlap on one GPU race)."""
+    _call("ws_moe_decode_route_noalloc", _ptr(logits), _ptr(bias), int(score_func),
+          float(gate_temp), int(norm_topk_prob), float(route_scale), _ptr(x), _ptr(w1), _ptr(s1),
+          _ptr(w3), _ptr(s3), _ptr(w2), _ptr(s2), _ptr(y), _ptr(topk_idx), _ptr(topk_w), dim,
+          inter, n_experts, top_k, swiglu_limit, _s(stream))
+
+
 # ---- routed experts, M tokens (launch.rs:430-689) -------------------------------
 def moe_tiles(routes, n_experts):
     """Upper bound on 32-slot tiles (engine.rs:4131, 6232-6233)."""
