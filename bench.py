@@ -150,8 +150,16 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
                                                    wts[t % n_tokens], w1, s1, w3, s3,
                                                    hq[t % n_tokens], hs[t % n_tokens], INTER,
                                                    DIM, E, TOPK, stream=st)
-    red = lambda t, st: L.expert_reduce(hq[t % n_tokens], hs[t % n_tokens], w2, s2, idx[t % n_tokens],
-                                        y[t % n_tokens], DIM, INTER, E, TOPK, stream=st)
+    # the picks in ascending expert id, as moe_local_slots gives them to the
+    # down kernel
+    ls = torch.empty((n_tokens, TOPK), dtype=torch.int32, device=dev)
+    le = torch.empty((n_tokens, TOPK), dtype=torch.int32, device=dev)
+    lc = torch.empty((n_tokens, 1), dtype=torch.int32, device=dev)
+    for t in range(n_tokens):
+        L.moe_local_slots(idx[t], ls[t], le[t], lc[t], TOPK, 0, E, stream=s)
+    red = lambda t, st: L.expert_reduce(hq[t % n_tokens], hs[t % n_tokens], w2, s2,
+                                        idx[t % n_tokens], ls[t % n_tokens], lc[t % n_tokens],
+                                        y[t % n_tokens], DIM, INTER, TOPK, 0, E, stream=st)
     for t in range(n_tokens):
         glu(t, s)
     reps_k = max(100, n_tokens)
@@ -178,12 +186,13 @@ def bench_moe(L, torch, dev, steps, warmup, n_tokens, slabs, gen, packed):
                 steps=done)
 
 
-def graph_time(torch, fn, reps, replays=3):
+def graph_time(torch, fn, reps, replays=3, stream=None):
     """Per-call GPU time of fn(i, stream) for i in range(reps): the reps calls
-    are captured into one HIP graph, so the timed region holds no host launch
-    cost, and the graph is replayed `replays` times between two events on the
-    replay stream. Returns (average, median) in ms per call."""
-    cs = torch.cuda.Stream()
+    are captured into one HIP graph (on `stream`, default a new one), so the
+    timed region holds no host launch cost, and the graph is replayed
+    `replays` times between two events on the replay stream. Returns (average,
+    median) in ms per call."""
+    cs = stream if stream is not None else torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(cs):
         fn(0, cs)
@@ -322,10 +331,12 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
     L.emit8(x, aq8, as8, M * K)
     L.act_quant_f32s(x, aqf, asf, M, K)
     s = torch.cuda.current_stream()
-    # the production configuration: a split-K workspace registered once
+    # the production configuration: a split-K workspace registered once for
+    # the stream the GEMMs run on (the capture stream of the timing graphs)
+    cs = torch.cuda.Stream()
     ws = torch.empty(max(L.gemm_workspace_size(M, N, K) for N in Ns), dtype=torch.uint8,
                      device=dev)
-    L.set_gemm_workspace(ws)
+    L.set_gemm_workspace(ws, stream=cs)
     for N in Ns:
         copies = max(2, math.ceil(400e6 / (N * K)))
         w = torch.randn((N, K), device=dev, generator=gen) * 0.02
@@ -340,6 +351,7 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
         for fmt, mode in (("ue8m0_32", L.MATH_EXACT), ("f32_128", L.MATH_EXACT),
                           ("ue8m0_32_native", L.MATH_NATIVE), ("f32_128_native", L.MATH_NATIVE)):
             L.set_math_mode(mode)
+            L.set_gemm_workspace(ws, stream=cs)  # registered with the library of this mode
             if fmt.startswith("f32_128"):
                 # f32 block scales for the same codes (timing only)
                 wsf.fill_(0.02 / 448)
@@ -351,7 +363,7 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
                     L.fp8_gemm_f32s(aqf, asf, wq[c], wsf[c], y, M, N, K, out_bf16=True, stream=st)
             for c in range(copies):
                 run(c, s)
-            avg_ms, med_ms = graph_time(torch, run, reps)
+            avg_ms, med_ms = graph_time(torch, run, reps, stream=cs)
             avg = avg_ms
             bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 2
             res[fmt] = {"avg_us": avg * 1e3, "median_us": med_ms * 1e3,
@@ -362,7 +374,7 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
         # warm: the same weight copy on every call (L2 / Infinity Cache hits)
         L.set_math_mode(L.MATH_EXACT)
         warm = lambda c, st: L.fp8_gemm_bf16(aq8, as8, wq[0], ws8[0], y, M, N, K, stream=st)
-        avg, med = graph_time(torch, warm, reps)
+        avg, med = graph_time(torch, warm, reps, stream=cs)
         bytes_ = N * K + (N // 32) * (K // 32) + M * K + M * (K // 32) + M * N * 2
         res["ue8m0_32_warm"] = {"avg_us": avg * 1e3, "median_us": med * 1e3,
                                 "TFLOP/s": flops / (avg * 1e-3) / 1e12,
@@ -374,7 +386,9 @@ def bench_gemm(L, torch, dev, reps, M=128, Ns=(4096, 12288, 2048)):
         L.set_math_mode(L.MATH_EXACT)
         del wq, ws8, wsf
     torch.cuda.synchronize()
-    L.set_gemm_workspace(None)
+    for mode in (L.MATH_NATIVE, L.MATH_EXACT):
+        L.set_math_mode(mode)
+        L.set_gemm_workspace(None, stream=cs)
     return out
 
 
@@ -390,7 +404,8 @@ def bench_model_shapes(L, torch, dev, reps=40, Ms=(1, 128)):
     gen.manual_seed(5)
     ws = torch.empty(max(L.gemm_workspace_size(128, n, k) for n, k in shapes.values()) + 256,
                      dtype=torch.uint8, device=dev)
-    L.set_gemm_workspace(ws)
+    cs = torch.cuda.Stream()
+    L.set_gemm_workspace(ws, stream=cs)
     out = {}
     for name, (N, K) in shapes.items():
         copies = max(2, math.ceil(400e6 / (N * K)))
@@ -408,14 +423,14 @@ def bench_model_shapes(L, torch, dev, reps=40, Ms=(1, 128)):
             y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
             run = lambda i, st: L.fp8_gemm_bf16(aq, asc, wq[i % copies], ws8[i % copies], y, M, N,
                                                 K, stream=st)
-            avg, _ = graph_time(torch, run, reps)
+            avg, _ = graph_time(torch, run, reps, stream=cs)
             byts = N * K + (N // 32) * (K // 32) + M * K + M * N * 2
             res["m%d" % M] = {"avg_us": avg * 1e3, "GB/s": byts / (avg * 1e-3) / 1e9,
                               "TFLOP/s": 2.0 * M * N * K / (avg * 1e-3) / 1e12}
         out["%s_%dx%d" % (name, N, K)] = res
         del wq, ws8
     torch.cuda.synchronize()
-    L.set_gemm_workspace(None)
+    L.set_gemm_workspace(None, stream=cs)
     return out
 
 
