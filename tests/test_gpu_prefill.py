@@ -56,7 +56,7 @@ def _dispatch_gpu(idx, w, E, tiles):
 
 
 @pytest.mark.parametrize("m,E,k", [(132, 384, 8), (1, 384, 8), (3, 16, 2), (300, 1024, 8),
-                                   (700, 96, 6)])
+                                   (700, 96, 6), (1100, 384, 8)])
 def test_dispatch_bit_exact(m, E, k):
     rng = np.random.default_rng(800 + m + E)
     logits, bias = zipf_routing(rng, m, E, k)

@@ -28,6 +28,7 @@ namespace ws {
 constexpr int kDispThreads = 1024;
 constexpr int kMaxExpertsG = 1024;
 constexpr int kTile = 32;
+constexpr int kDispHeld = 4;  // route chunks the dispatch keeps in registers
 
 // ---- dispatch (one workgroup) -------------------------------------------
 // An expert id as the dispatch sees it: ids outside [0, E) (a pick another
@@ -67,25 +68,37 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     __shared__ int32_t wsum[kDispThreads / 64];
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     base[t] = 0;
+    // the first kDispHeld chunks of routes are loaded once, up front (one
+    // memory round trip), and kept in registers with their ranks for pass 2
+    int e_h[kDispHeld], rk_h[kDispHeld];
+    float w_h[kDispHeld];
+#pragma unroll
+    for (int h = 0; h < kDispHeld; h++) {
+        const int r = h * kDispThreads + t;
+        e_h[h] = r < routes ? id_of(idx[r], n_experts) : -1;
+        w_h[h] = r < routes ? wts[r] : 0.0f;
+        rk_h[h] = 0;
+    }
     __syncthreads();
-    // pass 1: stable rank of every route inside its expert
-    for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
-        const int r = c0 + t;
-        const int e = r < routes ? id_of(idx[r], n_experts) : -1;
-        const bool valid = e >= 0 && e < n_experts;
+    // pass 1: stable rank of every route inside its expert (chunk by chunk,
+    // in route order)
+    auto rank_chunk = [&](int e) {
+        const bool valid = e >= 0;
 #pragma unroll
         for (int ww = 0; ww < kDispThreads / 64; ww++) wcnt[ww][t] = 0;
         __syncthreads();
-        // the wave's routes of the same expert: lane l's expert read as a
-        // scalar (readlane), not through an LDS permute
-        int inrank = 0, cnt = 0;
-#pragma unroll 8
-        for (int l = 0; l < 64; l++) {
-            const int el = __builtin_amdgcn_readlane(e, l);
-            const bool same = el == e;
-            cnt += same;
-            inrank += (same && l < lane);
+        // the wave's lanes with the same expert: the AND over the id's bits
+        // (n_experts <= 1024: 10 bits, and the sign for -1) of the ballot of
+        // lanes that agree with this lane on that bit
+        uint64_t same = ~0ull;
+#pragma unroll
+        for (int b = 0; b < 11; b++) {
+            const int bit = b < 10 ? (e >> b) & 1 : e < 0;
+            const uint64_t m = __ballot(bit);
+            same &= bit ? m : ~m;
         }
+        const int cnt = __popcll(same);
+        const int inrank = __popcll(same & ((1ull << lane) - 1));
         if (valid && inrank == 0) wcnt[w][e] = cnt;
         __syncthreads();
         if (t < n_experts) {
@@ -99,8 +112,17 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
             base[t] = run;
         }
         __syncthreads();
-        if (valid) route_pos[r] = wcnt[w][e] + inrank;
+        const int rank = valid ? wcnt[w][e] + inrank : -1;
         __syncthreads();
+        return rank;
+    };
+#pragma unroll
+    for (int h = 0; h < kDispHeld; h++)
+        if (h * kDispThreads < routes) rk_h[h] = rank_chunk(e_h[h]);  // uniform
+    for (int c0 = kDispHeld * kDispThreads; c0 < routes; c0 += kDispThreads) {
+        const int r = c0 + t;
+        const int rank = rank_chunk(r < routes ? id_of(idx[r], n_experts) : -1);
+        if (rank >= 0) route_pos[r] = rank;
     }
     // exclusive scan of the 32-padded counts over experts
     const int count = t < n_experts ? base[t] : 0;
@@ -125,36 +147,44 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
         count_out[t] = count;
         offset_out[t] = offset;
         psum_out[t] = offset + count;
-        for (int i = count; i < padded; i++) {
-            int slot = offset + i;
-            if (slot < cap) {
-                order[slot] = -1;
-                layout_w[slot] = 0.0f;
-            }
-        }
-        for (int tt = 0; tt < padded / kTile; tt++) {
-            int ti = offset / kTile + tt;
-            if (ti < tiles) tile_expert[ti] = t;
-        }
     }
     if (t == 0) *num_tiles_out = used;
+    __syncthreads();
+    // every used slot starts as padding (coalesced stores); pass 2
+    // overwrites the slots that hold routes, after the barrier (which waits
+    // for these stores to complete)
+    for (int slot = t; slot < min(used * kTile, cap); slot += kDispThreads) {
+        order[slot] = -1;
+        layout_w[slot] = 0.0f;
+    }
+    if (t < n_experts)
+        for (int tt = 0; tt < padded / kTile; tt++) {
+            const int ti = offset / kTile + tt;
+            if (ti < tiles) tile_expert[ti] = t;
+        }
     for (int ti = used + t; ti < tiles; ti += kDispThreads) tile_expert[ti] = -1;
     __syncthreads();
     // pass 2: slots
-    for (int c0 = 0; c0 < routes; c0 += kDispThreads) {
-        const int r = c0 + t;
-        if (r >= routes) break;
-        const int e = id_of(idx[r], n_experts);
-        if (e < 0 || e >= n_experts) {
+    auto place = [&](int r, int e, int rank, float wr) {
+        if (e < 0) {
             route_pos[r] = -1;
-            continue;
+            return;
         }
-        const int slot = scan[e] + route_pos[r];
+        const int slot = scan[e] + rank;
         if (slot < cap) {
             order[slot] = r;
-            layout_w[slot] = wts[r];
+            layout_w[slot] = wr;
         }
         route_pos[r] = slot;
+    };
+#pragma unroll
+    for (int h = 0; h < kDispHeld; h++) {
+        const int r = h * kDispThreads + t;
+        if (r < routes) place(r, e_h[h], rk_h[h], w_h[h]);
+    }
+    for (int r = kDispHeld * kDispThreads + t; r < routes; r += kDispThreads) {
+        const int e = id_of(idx[r], n_experts);
+        place(r, e, e >= 0 ? route_pos[r] : 0, wts[r]);
     }
 }
 
@@ -716,19 +746,20 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     __shared__ int32_t slots[16];
     __shared__ int32_t ns;
     const int row = blockIdx.y;
-    if (threadIdx.x == 0) {
-        int n = 0;
-        for (int j = 0; j < top_k; j++) {
-            int s = route_pos[(size_t)row * top_k + j];
-            if (s < 0 || s >= cap) continue;
-            int i = n++;
-            while (i > 0 && slots[i - 1] > s) {
-                slots[i] = slots[i - 1];
-                i--;
-            }
-            slots[i] = s;
+    if (threadIdx.x < 64) {
+        // lane j holds route j's slot; the slots of a row are distinct, so a
+        // slot's place in ascending order is the number of smaller ones
+        const int j = threadIdx.x;
+        const int s = j < top_k ? route_pos[(size_t)row * top_k + j] : -1;
+        const bool ok = s >= 0 && s < cap;
+        int place = 0;
+        for (int l = 0; l < top_k; l++) {
+            const int sl = __shfl(s, l, 64);
+            place += (sl >= 0 && sl < cap && sl < s);
         }
-        ns = n;
+        const int n = __popcll(__ballot(ok));
+        if (ok) slots[place] = s;
+        if (j == 0) ns = n;
     }
     __syncthreads();
     const int d = blockIdx.x * 256 + threadIdx.x;
