@@ -489,7 +489,12 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     the 384 routed FP4 experts (M=1: ws_moe_decode_route; M>1: ws_moe_topk +
     the grouped ws_moe_prefill), the shared FP8 expert (inter 2048; w1 and w3
     fused into one w13 matrix as the engine loads them, engine.rs:1520, one
-    gate/up GEMM as at :4067) and the two acc_f32 adds. Routed layers 2..4 are device copies of layer 1's packed
+    gate/up GEMM as at :4067) and the two acc_f32 adds. For M <= 16 the
+    out-projection with its token quantisation and residual add is one launch
+    (ws_fp8_gemv_acc) and the shared gate/up GEMV + SwiGLU runs in
+    the gate logits' launch (ws_moe_gate_shared_w13) and its down GEMV with
+    the adds after the routed experts (ws_shared_expert_down_acc); all give
+    the unfused chain's bits. Routed layers 2..4 are device copies of layer 1's packed
     experts (distinct memory, so no layer reads another's weights from
     cache). Reported per layer; bytes = weights touched once."""
     import numpy as np
@@ -524,6 +529,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
         idx = torch.empty((layers, M, TOPK), dtype=torch.int32, device=dev)
         wts = torch.empty((layers, M, TOPK), dtype=torch.float32, device=dev)
         yr = torch.empty((M, DIM), dtype=torch.float32, device=dev)
+        hsf = torch.empty((M, SI), dtype=torch.float32, device=dev)
         ys = torch.empty((M, DIM), dtype=torch.float32, device=dev)
         sws = torch.empty(L.shared_expert_workspace_size(M, DIM, SI), dtype=torch.uint8,
                           device=dev)
@@ -535,10 +541,17 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
         def step(i, st):
             h.copy_(h0)
             for li, w in enumerate(lay):
-                L.emit8(attn[li], aq, asc, M * OD, stream=st)
-                L.fp8_gemm(aq, asc, *w["wo"], o, M, DIM, OD, stream=st)
-                L.acc_f32(o, h, M * DIM, stream=st)
-                L.moe_gate_logits(h, w["gate"], logits, M, DIM, E, stream=st)
+                if M == 1:  # emit8 + fp8_gemm + acc_f32 in one launch (same bits)
+                    L.fp8_gemv_acc(attn[li], *w["wo"], h, M, DIM, OD, stream=st)
+                else:
+                    L.emit8(attn[li], aq, asc, M * OD, stream=st)
+                    L.fp8_gemm(aq, asc, *w["wo"], o, M, DIM, OD, stream=st)
+                    L.acc_f32(o, h, M * DIM, stream=st)
+                if M == 1:  # gate logits and the shared gate/up + SwiGLU in one launch
+                    L.moe_gate_shared_w13(h, w["gate"], logits, *w["shared"][:2], hsf, M, DIM, E,
+                                          SI, stream=st)
+                else:
+                    L.moe_gate_logits(h, w["gate"], logits, M, DIM, E, stream=st)
                 if M == 1:
                     L.moe_decode_route(logits, w["bias"], L.SCORE_SIGMOID, 1.0, 1, 1.0, h,
                                        *w["routed"], yr, idx[li], wts[li], DIM, INTER, E, TOPK,
@@ -548,9 +561,13 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
                                L.SCORE_SIGMOID, 1.0, True, 1.0, stream=st)
                     L.moe_prefill(h, idx[li], wts[li], *w["routed"], yr, M, DIM, INTER, E, TOPK,
                                   pws, stream=st)
-                L.shared_expert_fp8_w13(h, *w["shared"], ys, M, DIM, SI, sws, stream=st)
-                L.acc_f32(ys, yr, M * DIM, stream=st)
-                L.acc_f32(yr, h, M * DIM, stream=st)
+                # h = h + (yr + shared(h)): the shared expert and the two
+                # acc_f32 adds (M == 1: the down GEMV only, its gate/up ran
+                # with the gate; same bits)
+                if M == 1:
+                    L.shared_expert_down_acc(hsf, *w["shared"][2:], yr, h, M, DIM, SI, stream=st)
+                else:
+                    L.shared_expert_fp8_w13_acc(h, *w["shared"], yr, h, M, DIM, SI, sws, stream=st)
 
         step(0, torch.cuda.current_stream())
         torch.cuda.synchronize()

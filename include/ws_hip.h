@@ -238,6 +238,46 @@ int ws_shared_expert_fp8_w13(const float *x, const uint8_t *w13, const uint8_t *
                              int64_t dim, int64_t inter, float swiglu_limit, void *workspace,
                              size_t workspace_bytes, ws_stream_t stream);
 
+/* Fused block steps. No single reference counterpart: each replaces a
+ * sequence of the reference's launches with one or two, same bits.
+ *
+ * ws_fp8_gemv_acc: h[m, n] += emit8(x) . w^T, i.e. launch.rs emit8 +
+ * gemm_q8 (fp8_gemm, engine.rs:4000-4018 for wo_b) + acc_f32
+ * (launch.rs:1175) in one launch: x [m, k] f32 is quantised per 1x32 inside
+ * the kernel. w e4m3 [n, k] with UE8M0 [n/32, k/32]. m <= 16, k <= 8192,
+ * k % 128 == 0, n % 16 == 0; x and h 16-byte aligned and not overlapping. */
+int ws_fp8_gemv_acc(const float *x, const uint8_t *w, const uint8_t *sw, float *h, int64_t m,
+                    int64_t n, int64_t k, ws_stream_t stream);
+/* ws_shared_expert_fp8_w13_acc: h = h + (yr + shared(x)), i.e.
+ * ws_shared_expert_fp8_w13 into y, then acc_f32(y, yr) (engine.rs:4532:
+ * y_moe += expert_y) and the residual add of y_moe into h, without writing
+ * yr. For m <= 16 (dim, inter <= 8192) two launches: the gate/up GEMV with
+ * the SwiGLU in its epilogue (h_s kept in f32 in the workspace), then the
+ * down GEMV that quantises h_s per 1x32 and adds into h. Larger m: the
+ * unfused sequence and one add kernel. Workspace as ws_shared_expert_fp8.
+ * x may be h itself (it is read before h is written). */
+int ws_shared_expert_fp8_w13_acc(const float *x, const uint8_t *w13, const uint8_t *s13,
+                                 const uint8_t *w2, const uint8_t *s2, const float *yr, float *h,
+                                 int64_t m, int64_t dim, int64_t inter, float swiglu_limit,
+                                 void *workspace, size_t workspace_bytes, ws_stream_t stream);
+/* The same split at the routed experts, for a decode step (m <= 8):
+ * ws_moe_gate_shared_w13 computes, in one launch, the f32 gate logits
+ * [m, n_experts] of h (ws_moe_gate_logits with f32 gate_w [n_experts, dim],
+ * dim % 256 == 0, dim <= 8192: the same bits) and the shared expert's
+ * hs [m, inter] = silu(min(g, L)) * clamp(u, -L, L) of g/u = emit8(h) . w13^T
+ * (f32, not quantised); the two read h only. After the routed experts have
+ * written yr, ws_shared_expert_down_acc quantises hs per 1x32 and does
+ * h = h + (yr + emit8(hs) . w2^T). Together: the bits of
+ * ws_moe_gate_logits + ws_shared_expert_fp8_w13_acc. hs is the caller's
+ * f32 [m, inter] buffer (16-byte aligned). */
+int ws_moe_gate_shared_w13(const float *h, const float *gate_w, float *logits,
+                           const uint8_t *w13, const uint8_t *s13, float *hs, int64_t m,
+                           int64_t dim, int64_t n_experts, int64_t inter, float swiglu_limit,
+                           ws_stream_t stream);
+int ws_shared_expert_down_acc(const float *hs, const uint8_t *w2, const uint8_t *s2,
+                              const float *yr, float *h, int64_t m, int64_t dim, int64_t inter,
+                              ws_stream_t stream);
+
 /* ---------------------------------------------------------------------
  * Packed FP4 expert weights. The routed-expert entry points below read FP4
  * weight slabs in a fragment-major layout: 16-row bands, each 128-K step of a

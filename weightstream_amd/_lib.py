@@ -85,6 +85,11 @@ SIGNATURES = {
                                   C.c_size_t, _p]),
     "ws_shared_expert_fp8_w13": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p,
                                       C.c_size_t, _p]),
+    "ws_fp8_gemv_acc": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_moe_gate_shared_w13": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f, _p]),
+    "ws_shared_expert_down_acc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_shared_expert_fp8_w13_acc": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p,
+                                          C.c_size_t, _p]),
     "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_x": (_i, [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),
     "ws_expert_glu_quant_route": (_i, [_p, _p, _i, _f, _i, _f] + [_p] * 9 + [_i64, _i64, _i64, _i64, _f, _p]),

@@ -24,6 +24,7 @@
 //  - the weight operand is streamed with non-temporal loads: each weight byte
 //    is used by exactly one workgroup.
 #include "ws_internal.hpp"
+#include "ws_gate.hpp"
 
 #include <stdlib.h>
 
@@ -32,7 +33,12 @@
 namespace ws {
 
 enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
-enum OutMode { kOutF32 = 0, kOutBf16 = 1 };
+// kOutAcc: C += sum; kOutAcc2: C = C + (aux + sum); kOutSwiglu: fragment 0
+// is a gate column, fragment 1 the up column jstride rows further, and C gets
+// silu(min(g, L)) * clamp(u, -L, L) (the three used by the fused GEMV paths,
+// one K split only)
+enum OutMode { kOutF32 = 0, kOutBf16 = 1, kOutAcc = 2, kOutAcc2 = 3, kOutSwiglu = 4 };
+static_assert(kOutAcc == kGemvAcc && kOutAcc2 == kGemvAcc2 && kOutSwiglu == kGemvSwiglu, "");
 
 // Operand registers of U consecutive 128-K steps of one wave.
 template <int WM, int WN, int U>
@@ -269,33 +275,42 @@ struct KpStage {
 
 constexpr int kKpMaxSaWords = 16;  // activation scale words staged per thread
 
-template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT>
-__global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A, const void *SA,
-                                                                const uint8_t *__restrict__ B,
-                                                                const void *__restrict__ SB,
-                                                                void *__restrict__ C, int M,
-                                                                int N, int K, int S,
-                                                                float *__restrict__ part_out,
-                                                                int sb_div) {
+//
+// AF32: A is f32 (M <= 16 rows); the workgroup quantises it per 1x32 block
+// (the act_quant rule, quant_fp8_block32: the bytes ws_emit8 writes) into
+// LDS, rows K + 16 bytes apart, while its first weight stages are in flight,
+// and the waves read their A fragments and scale words from there.
+template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT,
+          bool AF32 = false>
+__device__ __forceinline__ void kp_body(int bx, int by, int bz, const uint8_t *A, const void *SA,
+                                        const uint8_t *__restrict__ B, const void *__restrict__ SB,
+                                        void *__restrict__ C, int M, int N, int K, int S,
+                                        float *__restrict__ part_out, int sb_div, const float *aux,
+                                        float limit, int jstride) {
     constexpr int kRows = 16 * MF * GMH;
     constexpr int kCols = 16 * NF;
+    static_assert(!AF32 || (MF == 1 && GMH == 1 && SMODE == kUe8m0 && !BFP4), "AF32: a GEMV");
+    static_assert(OMODE != kOutSwiglu || NF == 2, "SwiGLU pairs two fragments");
     // UE8M0 activation scales: staged in LDS for blocks of rows; a single
     // 16-row fragment (GEMV) loads its word per step instead (no prologue)
-    constexpr bool kStageSa = SMODE == kF32s || kRows > 16;
+    constexpr bool kStageSa = !AF32 && (SMODE == kF32s || kRows > 16);
     constexpr int kThreads = 64 * GMH * GK;
     extern __shared__ __align__(16) float kp_lds[];
     float *part = kp_lds;                         // [GK][kRows][kCols]
     float *sa_l = kp_lds + GK * kRows * kCols;    // [ksteps][kRows] (f32-scale mode)
+    uint8_t *a_l = (uint8_t *)sa_l;               // AF32: [M][K + 16] e4m3
+    const int a_pitch = K + 16;
+    uint8_t *as_l = a_l + (size_t)M * a_pitch;    // AF32: [M][K / 32] UE8M0
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int wk = w % GK, wm = w / GK;
     const int r = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * kCols;
-    const int mb = blockIdx.y * kRows;           // workgroup's first row
+    const int n0 = bx * (OMODE == kOutSwiglu ? 16 : kCols);
+    const int mb = by * kRows;                   // workgroup's first row
     const int ml = wm * 16 * MF;                 // wave's first row within the workgroup
     const int ksteps = K / 128;
-    // K split S ways over blockIdx.z (S > 1: f32 partial planes, added in
+    // K split S ways over bz (S > 1: f32 partial planes, added in
     // split order by split_reduce_kernel), then over the GK waves
-    const int kz0 = blockIdx.z * ksteps / S, kzn = (blockIdx.z + 1) * ksteps / S - kz0;
+    const int kz0 = bz * ksteps / S, kzn = (bz + 1) * ksteps / S - kz0;
     const int k0 = kz0 + wk * kzn / GK, k1 = kz0 + (wk + 1) * kzn / GK;
     const int kbn = K / 32, kb128 = K / 128;
 
@@ -347,7 +362,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     const uint8_t *sbrow[NF];
 #pragma unroll
     for (int j = 0; j < NF; j++) {
-        const int col = n0 + 16 * j + r;
+        const int col = n0 + (OMODE == kOutSwiglu ? j * jstride : 16 * j) + r;
         brow[j] = BFP4 ? B + (size_t)col * (K / 2) + g * 16
                        : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
         // FP8 weight scales: one row per 32-row block, or per row (sb_div 1)
@@ -361,6 +376,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
             const int ks = max(min(ks0 + u, k1 - 1), 0);
 #pragma unroll
             for (int i = 0; i < MF; i++) {
+                if (AF32) break;  // A is read from LDS at use
                 const uint8_t *p = arow[i] + (size_t)ks * 128;
                 st.a[u][i][0] = ldg16(p);
                 st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
@@ -403,10 +419,22 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
 #pragma unroll
                 for (int i = 0; i < MF; i++) {
                     v8bf aq[4];
-                    const uint32_t saw = !kStageSa ? st.sa[u][i]
-                                         : ((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g);
+                    uint4 a0, a1;
+                    uint32_t saw;
+                    if (AF32) {
+                        const int rl = min(r, M - 1);
+                        const uint8_t *ap = a_l + rl * a_pitch + ks * 128 + g * 32;
+                        a0 = *(const uint4 *)ap;
+                        a1 = *(const uint4 *)(ap + 16);
+                        saw = *(const uint32_t *)(as_l + rl * (K / 32) + ks * 4) >> (8 * g);
+                    } else {
+                        a0 = st.a[u][i][0];
+                        a1 = st.a[u][i][1];
+                        saw = !kStageSa ? st.sa[u][i]
+                                        : ((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g);
+                    }
                     const float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(saw & 0xFF) : 1.0f;
-                    cvt_fp8x32(st.a[u][i][0], st.a[u][i][1], sav_f, aq);
+                    cvt_fp8x32(a0, a1, sav_f, aq);
 #pragma unroll
                     for (int j = 0; j < NF; j++) {
                         if (SMODE == kUe8m0) {
@@ -428,11 +456,19 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                     b[j] = BFP4 ? frag_from4(st.b[u][j][0]) : frag_from(st.b[u][j][0], st.b[u][j][1]);
 #pragma unroll
                 for (int i = 0; i < MF; i++) {
-                    const v8i a = frag_from(st.a[u][i][0], st.a[u][i][1]);
-                    const int sai =
-                        SMODE != kUe8m0 ? 0
-                        : !kStageSa     ? (int)(st.sa[u][i] & 0xFF)
-                                        : (int)((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF);
+                    v8i a;
+                    int sai;
+                    if (AF32) {
+                        const int rl = min(r, M - 1);
+                        const uint8_t *ap = a_l + rl * a_pitch + ks * 128 + g * 16;
+                        a = frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64));
+                        sai = (int)((*(const uint32_t *)(as_l + rl * (K / 32) + ks * 4) >> (8 * g)) & 0xFF);
+                    } else {
+                        a = frag_from(st.a[u][i][0], st.a[u][i][1]);
+                        sai = SMODE != kUe8m0 ? 0
+                              : !kStageSa     ? (int)(st.sa[u][i] & 0xFF)
+                                              : (int)((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF);
+                    }
 #pragma unroll
                     for (int j = 0; j < NF; j++) {
                         if (SMODE == kUe8m0) {
@@ -460,6 +496,26 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
     mem_order();
     load(s1, k0 + U);
     mem_order();
+    if (AF32) {
+        // four values per lane, a 1x32 block per 8 lanes; every lane of a
+        // block takes part in its maximum (dead blocks quantise zeros and
+        // store nothing; M K % 32 == 0)
+        const float4 *X = (const float4 *)A;
+        const int n4 = M * K / 4;
+        for (int i0 = 0; i0 < n4; i0 += kThreads) {
+            const int i = i0 + t;
+            const bool live = i < n4;
+            uint32_t sbyte;
+            const uint32_t q = quant_fp8_block32_x4(live ? X[i] : float4{0.f, 0.f, 0.f, 0.f},
+                                                    &sbyte);
+            if (live) {
+                const int row = (4 * i) / K, col = 4 * i - row * K;
+                *(uint32_t *)(a_l + row * a_pitch + col) = q;
+                if ((t & 7) == 0) as_l[row * (K / 32) + col / 32] = (uint8_t)sbyte;
+            }
+        }
+        lds_barrier();
+    }
     if (kStageSa) {
         uint32_t *sa_w = (uint32_t *)sa_l;
 #pragma unroll
@@ -501,17 +557,54 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
             for (int v = 0; v < 4; v++)
                 part[(wk * kRows + ml + 16 * f + 4 * g + v) * kCols + 16 * j + r] = acc[f][j][v];
     __syncthreads();
+    auto wave_sum = [&](int rl, int c) {
+        float sum = part[rl * kCols + c];
+#pragma unroll
+        for (int q = 1; q < GK; q++) sum = sum + part[(q * kRows + rl) * kCols + c];
+        return sum;
+    };
+    if (OMODE == kOutSwiglu) {
+        // C [M][N]: N = the intermediate width (jstride)
+        for (int o = t; o < kRows * 16; o += kThreads) {
+            const int rl = o / 16, c = o % 16;
+            const int row = mb + rl;
+            if (row >= M) continue;
+            float gv = wave_sum(rl, c), uv = wave_sum(rl, c + 16);
+            if (limit > 0.0f) {
+                uv = rclamp(uv, -limit, limit);
+                gv = fminf(gv, limit);
+            }
+            ((float *)C)[(size_t)row * N + n0 + c] = ws_silu(gv) * uv;
+        }
+        return;
+    }
     for (int o = t; o < kRows * kCols; o += kThreads) {
         const int rl = o / kCols, c = o % kCols;
         const int row = mb + rl;
         if (row >= M) continue;
-        float sum = part[rl * kCols + c];
-#pragma unroll
-        for (int q = 1; q < GK; q++) sum = sum + part[(q * kRows + rl) * kCols + c];
-        if (S > 1) part_out[((size_t)blockIdx.z * M + row) * N + n0 + c] = sum;
-        else if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + n0 + c] = sum;
-        else ((uint16_t *)C)[(size_t)row * N + n0 + c] = f32_to_bf16(sum);
+        const float sum = wave_sum(rl, c);
+        const size_t at = (size_t)row * N + n0 + c;
+        if (S > 1) part_out[((size_t)bz * M + row) * N + n0 + c] = sum;
+        else if (OMODE == kOutF32) ((float *)C)[at] = sum;
+        else if (OMODE == kOutBf16) ((uint16_t *)C)[at] = f32_to_bf16(sum);
+        else if (OMODE == kOutAcc) ((float *)C)[at] = ((float *)C)[at] + sum;
+        else ((float *)C)[at] = ((float *)C)[at] + (aux[at] + sum);
     }
+}
+
+template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT,
+          bool AF32 = false>
+__global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A, const void *SA,
+                                                                const uint8_t *__restrict__ B,
+                                                                const void *__restrict__ SB,
+                                                                void *__restrict__ C, int M,
+                                                                int N, int K, int S,
+                                                                float *__restrict__ part_out,
+                                                                int sb_div, const float *aux,
+                                                                float limit, int jstride) {
+    kp_body<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, EXACT, AF32>(
+        blockIdx.x, blockIdx.y, blockIdx.z, A, SA, B, SB, C, M, N, K, S, part_out, sb_div, aux,
+        limit, jstride);
 }
 
 // out = the S partial planes [S][M][N] summed in plane order (deterministic)
@@ -554,16 +647,98 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     if (math_mode() == WS_MATH_NATIVE)
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false>), grid,
                            dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
-                           sb_div);
+                           sb_div, nullptr, 0.0f, 16);
     else
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true>), grid,
                            dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
-                           sb_div);
+                           sb_div, nullptr, 0.0f, 16);
     int rc = launch_status();
     if (rc || S == 1) return rc;
     const int64_t mn = (int64_t)m * n;
     hipLaunchKernelGGL((split_reduce_kernel<OMODE>), dim3((unsigned)((mn / 4 + 255) / 256)),
                        dim3(256), 0, stream, part, out, mn, S);
+    return launch_status();
+}
+
+// The fused GEMVs (M <= 16, FP8 weights with 32 x 32 UE8M0 scales, f32
+// activations quantised in the kernel): the 16-column-strip kernel with
+// 8 K waves and no K split, so every output is the same sum, bit for bit,
+// as ws_emit8 followed by ws_fp8_gemm (whose kernel this is for M <= 16 and
+// K <= 8192). OMODE kOutAcc / kOutAcc2 write n columns; kOutSwiglu writes
+// h [m][n] from the gate rows [0, n) and up rows [n, 2n) of the weights.
+int kp_gemv_fused(int omode, const float *x, const uint8_t *w, const uint8_t *sw, float *out,
+                  const float *aux, float limit, int64_t m, int64_t n, int64_t k,
+                  hipStream_t stream) {
+    if (!x || !w || !sw || !out || (omode == kOutAcc2 && !aux)) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || m > 16 || n <= 0 || k <= 0) return WS_ERR_INVALID_ARG;
+    if (k % 128 || n % 16 || k > 8192 || n > (1 << 24)) return WS_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)out | (uintptr_t)aux) & 15 ||
+        (uintptr_t)sw & 3)
+        return WS_ERR_INVALID_ARG;
+    const int nf = omode == kOutSwiglu ? 2 : 1;
+    const size_t lds = (size_t)8 * 16 * 16 * nf * 4 + (size_t)m * (k + 16) + (size_t)m * (k / 32);
+    if (lds > 160 * 1024) return WS_ERR_SHAPE;
+    const dim3 grid((unsigned)(n / 16)), block(512);
+    const bool ex = math_mode() == WS_MATH_EXACT;
+    const int M = (int)m, N = (int)n, K = (int)k;
+#define WS_KPF(OM, NFV, E)                                                                     \
+    hipLaunchKernelGGL((gemm_kp_kernel<1, NFV, 1, 8, false, kUe8m0, OM, 2, E, true>), grid, block, \
+                       lds, stream, (const uint8_t *)x, (const void *)nullptr, w, (const void *)sw, \
+                       (void *)out, M, N, K, 1, (float *)nullptr, 32, aux, limit, N)
+    switch (omode) {
+        case kOutAcc: if (ex) WS_KPF(kOutAcc, 1, true); else WS_KPF(kOutAcc, 1, false); break;
+        case kOutAcc2: if (ex) WS_KPF(kOutAcc2, 1, true); else WS_KPF(kOutAcc2, 1, false); break;
+        case kOutSwiglu: if (ex) WS_KPF(kOutSwiglu, 2, true); else WS_KPF(kOutSwiglu, 2, false); break;
+        default: return WS_ERR_INVALID_ARG;
+    }
+#undef WS_KPF
+    return launch_status();
+}
+
+// The gate logits and the shared expert's gate/up GEMV + SwiGLU in one
+// launch: both read h and neither reads the other's output. The logits are a
+// latency-bound sequential chain per expert (two waves on each of the first
+// ceil(E / 4) x m workgroups); the GEMV is a weight stream over the next
+// inter / 16 workgroups. Each part is the same code, and gives the same bits,
+// as its own kernel (gate_logits_pc_kernel<4, 1, f32>; the kOutSwiglu GEMV).
+template <bool EXACT>
+__global__ __launch_bounds__(512) void gate_w13_kernel(const float *h, const float *gw,
+                                                       float *logits, int m, int dim,
+                                                       int n_experts, const uint8_t *w13,
+                                                       const uint8_t *s13, float *hs, int inter,
+                                                       float limit) {
+    const int gx = (n_experts + 3) / 4, n_gate = gx * m;
+    const int b = blockIdx.x;
+    if (b < n_gate) {
+        gate_pc_body<4, 1, false>(b % gx, b / gx, h, gw, logits, m, dim, n_experts);
+        return;
+    }
+    kp_body<1, 2, 1, 8, false, kUe8m0, kOutSwiglu, 2, EXACT, true>(
+        b - n_gate, 0, 0, (const uint8_t *)h, nullptr, w13, s13, hs, m, inter, dim, 1, nullptr, 32,
+        nullptr, limit, inter);
+}
+
+int gate_w13_launch(const float *h, const float *gw, float *logits, const uint8_t *w13,
+                    const uint8_t *s13, float *hs, int64_t m, int64_t dim, int64_t n_experts,
+                    int64_t inter, float limit, hipStream_t stream) {
+    if (!h || !gw || !logits || !w13 || !s13 || !hs) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || m > 8 || dim <= 0 || n_experts <= 0 || inter <= 0) return WS_ERR_INVALID_ARG;
+    if (dim % kGC || dim > 8192 || inter % 16 || inter > (1 << 20) || n_experts > (1 << 16))
+        return WS_ERR_SHAPE;
+    if (((uintptr_t)h | (uintptr_t)w13 | (uintptr_t)hs) & 15 || (uintptr_t)s13 & 3)
+        return WS_ERR_INVALID_ARG;
+    using G = GateGeom<4, 1, false>;
+    const size_t gate_lds = (size_t)kGS * G::kStage + (size_t)2 * 4 * kPcPitch * 4;
+    const size_t kp_lds = (size_t)8 * 16 * 32 * 4 + (size_t)m * (dim + 16) + (size_t)m * (dim / 32);
+    const size_t lds = gate_lds > kp_lds ? gate_lds : kp_lds;
+    const unsigned grid = (unsigned)((n_experts + 3) / 4 * m + inter / 16);
+    if (math_mode() == WS_MATH_EXACT)
+        hipLaunchKernelGGL(gate_w13_kernel<true>, dim3(grid), dim3(512), lds, stream, h, gw, logits,
+                           (int)m, (int)dim, (int)n_experts, w13, s13, hs, (int)inter, limit);
+    else
+        hipLaunchKernelGGL(gate_w13_kernel<false>, dim3(grid), dim3(512), lds, stream, h, gw,
+                           logits, (int)m, (int)dim, (int)n_experts, w13, s13, hs, (int)inter,
+                           limit);
     return launch_status();
 }
 

@@ -58,8 +58,17 @@ __global__ __launch_bounds__(256) void acc_f32_kernel(const float *__restrict__ 
     }
 }
 
+// h = h + (yr + ys), the two acc_f32 adds of the block in their order
+// (yr += ys, then h += yr) without writing yr
+__global__ __launch_bounds__(256) void acc2_f32_kernel(const float *__restrict__ ys,
+                                                       const float *__restrict__ yr,
+                                                       float *__restrict__ h, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] = h[i] + (yr[i] + ys[i]);
+}
+
 struct SharedLayout {
-    size_t xq, xs, g, u, hq, hs, total;
+    size_t xq, xs, g, u, hq, hs, y, total;
 };
 
 static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
@@ -73,6 +82,7 @@ static SharedLayout shared_layout(int64_t m, int64_t dim, int64_t inter) {
     l.u = o; o += al256((size_t)m * inter * 4);
     l.hq = o; o += al256((size_t)m * inter);
     l.hs = o; o += al256((size_t)m * (inter / 32));
+    l.y = o; o += al256((size_t)m * dim * 4);
     l.total = o;
     return l;
 }
@@ -146,6 +156,55 @@ int ws_shared_expert_fp8_w13(const float *x, const uint8_t *w13, const uint8_t *
     rc = launch_status();
     if (rc) return rc;
     return ws_fp8_gemm(hq, hs, w2, s2, y, m, dim, inter, stream);
+}
+
+// emit8 + fp8_gemm + acc_f32 in one launch (m <= 16)
+int ws_fp8_gemv_acc(const float *x, const uint8_t *w, const uint8_t *sw, float *h, int64_t m,
+                    int64_t n, int64_t k, ws_stream_t stream) {
+    return kp_gemv_fused(kGemvAcc, x, w, sw, h, nullptr, 0.0f, m, n, k, stream);
+}
+
+int ws_shared_expert_fp8_w13_acc(const float *x, const uint8_t *w13, const uint8_t *s13,
+                                 const uint8_t *w2, const uint8_t *s2, const float *yr, float *h,
+                                 int64_t m, int64_t dim, int64_t inter, float swiglu_limit,
+                                 void *workspace, size_t workspace_bytes, ws_stream_t stream) {
+    if (!x || !w13 || !s13 || !w2 || !s2 || !yr || !h || !workspace) return WS_ERR_INVALID_ARG;
+    if (m <= 0 || dim <= 0 || inter <= 0 || dim % 128 || inter % 128) return WS_ERR_SHAPE;
+    const SharedLayout l = shared_layout(m, dim, inter);
+    if (workspace_bytes < l.total || ((uintptr_t)workspace & 255)) return WS_ERR_INVALID_ARG;
+    uint8_t *ws = (uint8_t *)workspace;
+    if (m <= 16 && dim <= 8192 && inter <= 8192) {
+        // gate/up GEMV + SwiGLU -> h_s (f32), then the down GEMV that
+        // quantises h_s and adds into h
+        float *hf = (float *)(ws + l.g);
+        int rc = kp_gemv_fused(kGemvSwiglu, x, w13, s13, hf, nullptr, swiglu_limit, m, inter, dim,
+                               stream);
+        if (rc) return rc;
+        return kp_gemv_fused(kGemvAcc2, hf, w2, s2, h, yr, 0.0f, m, dim, inter, stream);
+    }
+    float *ys = (float *)(ws + l.y);
+    int rc = ws_shared_expert_fp8_w13(x, w13, s13, w2, s2, ys, m, dim, inter, swiglu_limit,
+                                      workspace, workspace_bytes, stream);
+    if (rc) return rc;
+    const int64_t n = m * dim;
+    hipLaunchKernelGGL(acc2_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       ys, yr, h, n);
+    return launch_status();
+}
+
+int ws_moe_gate_shared_w13(const float *h, const float *gate_w, float *logits,
+                           const uint8_t *w13, const uint8_t *s13, float *hs, int64_t m,
+                           int64_t dim, int64_t n_experts, int64_t inter, float swiglu_limit,
+                           ws_stream_t stream) {
+    return gate_w13_launch(h, gate_w, logits, w13, s13, hs, m, dim, n_experts, inter, swiglu_limit,
+                           stream);
+}
+
+int ws_shared_expert_down_acc(const float *hs, const uint8_t *w2, const uint8_t *s2,
+                              const float *yr, float *h, int64_t m, int64_t dim, int64_t inter,
+                              ws_stream_t stream) {
+    if (!yr) return WS_ERR_INVALID_ARG;
+    return kp_gemv_fused(kGemvAcc2, hs, w2, s2, h, yr, 0.0f, m, dim, inter, stream);
 }
 
 }  // extern "C"

@@ -211,6 +211,27 @@ __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_b
     return f32_to_e4m3(rclamp(x / s, -448.0f, 448.0f));
 }
 
+// The same block quantisation with four consecutive values per lane, a block
+// being 8 lanes (a lane-group of 8 aligned lanes): the bytes of
+// quant_fp8_block32, packed low value first. The block maximum is
+// order-free; x / 2^e is computed as x * 2^-e, the same real number rounded
+// the same way (2^-e is exact for the e this scale rule yields, e in
+// [-22, 120]), which costs a multiply instead of a division.
+__device__ __forceinline__ uint32_t quant_fp8_block32_x4(float4 v, uint32_t *scale_byte) {
+    float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
+                       fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
+#pragma unroll
+    for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    if (amax < 1e-4f) amax = 1e-4f;
+    const int e = log2_ceil(amax / 448.0f);
+    *scale_byte = (uint32_t)(e + 127) & 0xFF;
+    const float inv = __builtin_ldexpf(1.0f, -e);
+    return f32_to_e4m3(rclamp(v.x * inv, -448.0f, 448.0f)) |
+           (f32_to_e4m3(rclamp(v.y * inv, -448.0f, 448.0f)) << 8) |
+           (f32_to_e4m3(rclamp(v.z * inv, -448.0f, 448.0f)) << 16) |
+           (f32_to_e4m3(rclamp(v.w * inv, -448.0f, 448.0f)) << 24);
+}
+
 // Scaled MFMA, 16x16 output, K = 128: D += (A * 2^sa) (B * 2^sb).
 // Operand layout (measured on gfx950): lane l supplies row (A) / column (B)
 // l % 16. With g = l / 16, an FP8 operand lane holds K [16g, 16g+16) in its

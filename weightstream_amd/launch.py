@@ -285,6 +285,35 @@ def shared_expert_fp8_w13(x, w13, s13, w2, s2, y, m, dim, inter, workspace, swig
           workspace.numel() * workspace.element_size(), _s(stream))
 
 
+def fp8_gemv_acc(x, w, sw, h, m, n, k, stream=None):
+    """h[m, n] += emit8(x) . w^T in one launch (emit8 + fp8_gemm + acc_f32,
+    launch.rs:1175; m <= 16)."""
+    _call("ws_fp8_gemv_acc", _ptr(x), _ptr(w), _ptr(sw), _ptr(h), m, n, k, _s(stream))
+
+
+def shared_expert_fp8_w13_acc(x, w13, s13, w2, s2, yr, h, m, dim, inter, workspace,
+                              swiglu_limit=10.0, stream=None):
+    """h = h + (yr + shared(x)): the shared expert, engine.rs:4532's
+    y_moe += expert_y and the residual add, fused (two launches for m <= 16)."""
+    _call("ws_shared_expert_fp8_w13_acc", _ptr(x), _ptr(w13), _ptr(s13), _ptr(w2), _ptr(s2),
+          _ptr(yr), _ptr(h), m, dim, inter, swiglu_limit, _ptr(workspace),
+          workspace.numel() * workspace.element_size(), _s(stream))
+
+
+def moe_gate_shared_w13(h, gate_w, logits, w13, s13, hs, m, dim, n_experts, inter,
+                        swiglu_limit=10.0, stream=None):
+    """Gate logits (f32 gate) and the shared expert's SwiGLU hidden state hs
+    (f32) in one launch (m <= 8)."""
+    _call("ws_moe_gate_shared_w13", _ptr(h), _ptr(gate_w), _ptr(logits), _ptr(w13), _ptr(s13),
+          _ptr(hs), m, dim, n_experts, inter, swiglu_limit, _s(stream))
+
+
+def shared_expert_down_acc(hs, w2, s2, yr, h, m, dim, inter, stream=None):
+    """h = h + (yr + emit8(hs) . w2^T) in one launch (m <= 16)."""
+    _call("ws_shared_expert_down_acc", _ptr(hs), _ptr(w2), _ptr(s2), _ptr(yr), _ptr(h), m, dim,
+          inter, _s(stream))
+
+
 def shared_expert_fp8(x, w1, s1, w3, s3, w2, s2, y, m, dim, inter, workspace,
                       swiglu_limit=10.0, stream=None):
     """moe.rs:210-250 shared_expert_hidden for m tokens (engine.rs:4063
