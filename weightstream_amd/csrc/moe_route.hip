@@ -14,8 +14,9 @@
 //    (moe.rs:50 `total_cmp(..).then(a.cmp(&b))`);
 //  - the weight normaliser is the sequential sum in top-k order plus 1e-20
 //    (moe.rs:61-66), then * route_scale.
-// sqrtsoftplus uses the device logf and sqrtf; sqrtf is correctly rounded,
-// logf is within 1 ulp of glibc's (not bit-exact).
+// sqrtsoftplus uses ws_logf and sqrtf: ws_logf equals glibc logf on every
+// input (ws_logf.h), sqrtf is correctly rounded, so the scores are the CPU's
+// bits.
 #include "ws_internal.hpp"
 #include "ws_route.hpp"
 #include "ws_gate.hpp"
