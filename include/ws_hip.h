@@ -245,16 +245,20 @@ int ws_shared_expert_fp8_w13(const float *x, const uint8_t *w13, const uint8_t *
  * gemm_q8 (fp8_gemm, engine.rs:4000-4018 for wo_b) + acc_f32
  * (launch.rs:1175) in one launch: x [m, k] f32 is quantised per 1x32 inside
  * the kernel. w e4m3 [n, k] with UE8M0 [n/32, k/32]. m <= 16, k <= 8192,
- * k % 128 == 0, n % 16 == 0; x and h 16-byte aligned and not overlapping. */
+ * k % 128 == 0, n % 16 == 0; x and h 16-byte aligned and not overlapping.
+ * Every workgroup quantises all of x, so it pays for one or two rows (the
+ * config-5 block at m = 8 is faster with the three separate launches). */
 int ws_fp8_gemv_acc(const float *x, const uint8_t *w, const uint8_t *sw, float *h, int64_t m,
                     int64_t n, int64_t k, ws_stream_t stream);
 /* ws_shared_expert_fp8_w13_acc: h = h + (yr + shared(x)), i.e.
  * ws_shared_expert_fp8_w13 into y, then acc_f32(y, yr) (engine.rs:4532:
  * y_moe += expert_y) and the residual add of y_moe into h, without writing
- * yr. For m <= 16 (dim, inter <= 8192) two launches: the gate/up GEMV with
+ * yr. For m <= 2 (dim, inter <= 8192) two launches: the gate/up GEMV with
  * the SwiGLU in its epilogue (h_s kept in f32 in the workspace), then the
  * down GEMV that quantises h_s per 1x32 and adds into h. Larger m: the
- * unfused sequence and one add kernel. Workspace as ws_shared_expert_fp8.
+ * unfused sequence and one add kernel (each workgroup of the fused GEMVs
+ * quantises the whole activation, which stops paying beyond a few rows).
+ * Workspace as ws_shared_expert_fp8.
  * x may be h itself (it is read before h is written). */
 int ws_shared_expert_fp8_w13_acc(const float *x, const uint8_t *w13, const uint8_t *s13,
                                  const uint8_t *w2, const uint8_t *s2, const float *yr, float *h,

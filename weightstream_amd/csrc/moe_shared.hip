@@ -173,9 +173,11 @@ int ws_shared_expert_fp8_w13_acc(const float *x, const uint8_t *w13, const uint8
     const SharedLayout l = shared_layout(m, dim, inter);
     if (workspace_bytes < l.total || ((uintptr_t)workspace & 255)) return WS_ERR_INVALID_ARG;
     uint8_t *ws = (uint8_t *)workspace;
-    if (m <= 16 && dim <= 8192 && inter <= 8192) {
+    if (m <= 2 && dim <= 8192 && inter <= 8192) {
         // gate/up GEMV + SwiGLU -> h_s (f32), then the down GEMV that
-        // quantises h_s and adds into h
+        // quantises h_s and adds into h. Every workgroup quantises the whole
+        // activation itself, so this pays for few rows only (block at m = 8:
+        // 184.7 us/layer this way against 167 unfused)
         float *hf = (float *)(ws + l.g);
         int rc = kp_gemv_fused(kGemvSwiglu, x, w13, s13, hf, nullptr, swiglu_limit, m, inter, dim,
                                stream);
