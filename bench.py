@@ -491,10 +491,11 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     fused into one w13 matrix as the engine loads them, engine.rs:1520, one
     gate/up GEMM as at :4067) and the two acc_f32 adds. For M <= 16 the
     out-projection with its token quantisation and residual add is one launch
-    (ws_fp8_gemv_acc) and the shared gate/up GEMV + SwiGLU runs in
-    the gate logits' launch (ws_moe_gate_shared_w13) and its down GEMV with
-    the adds after the routed experts (ws_shared_expert_down_acc); all give
-    the unfused chain's bits. Routed layers 2..4 are device copies of layer 1's packed
+    (ws_fp8_gemv_acc), the shared gate/up GEMV + SwiGLU runs in the gate
+    logits' launch (ws_moe_gate_shared_w13) and its down GEMV in the routed
+    gate/up launch, the adds at the end of the routed down kernel
+    (ws_moe_decode_route_shared): five launches per layer, the unfused
+    chain's bits. Routed layers 2..4 are device copies of layer 1's packed
     experts (distinct memory, so no layer reads another's weights from
     cache). Reported per layer; bytes = weights touched once."""
     import numpy as np
@@ -530,6 +531,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
         wts = torch.empty((layers, M, TOPK), dtype=torch.float32, device=dev)
         yr = torch.empty((M, DIM), dtype=torch.float32, device=dev)
         hsf = torch.empty((M, SI), dtype=torch.float32, device=dev)
+        ysb = torch.empty((M, DIM), dtype=torch.float32, device=dev)
         ys = torch.empty((M, DIM), dtype=torch.float32, device=dev)
         sws = torch.empty(L.shared_expert_workspace_size(M, DIM, SI), dtype=torch.uint8,
                           device=dev)
@@ -553,20 +555,21 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
                 else:
                     L.moe_gate_logits(h, w["gate"], logits, M, DIM, E, stream=st)
                 if M == 1:
-                    L.moe_decode_route(logits, w["bias"], L.SCORE_SIGMOID, 1.0, 1, 1.0, h,
-                                       *w["routed"], yr, idx[li], wts[li], DIM, INTER, E, TOPK,
-                                       dws, stream=st)
+                    # the routed experts, the shared down GEMV on extra
+                    # workgroups of their gate/up launch, and h = h + (yr + ys)
+                    # at the end of their down kernel (same bits as
+                    # moe_decode_route + shared_expert_down_acc)
+                    L.moe_decode_route_shared(logits, w["bias"], L.SCORE_SIGMOID, 1.0, 1, 1.0, h,
+                                              *w["routed"], yr, idx[li], wts[li], DIM, INTER, E,
+                                              TOPK, hsf, *w["shared"][2:], SI, ysb, h, dws,
+                                              stream=st)
                 else:
                     L.moe_topk(logits, w["bias"], None, idx[li], wts[li], M, E, TOPK,
                                L.SCORE_SIGMOID, 1.0, True, 1.0, stream=st)
                     L.moe_prefill(h, idx[li], wts[li], *w["routed"], yr, M, DIM, INTER, E, TOPK,
                                   pws, stream=st)
-                # h = h + (yr + shared(h)): the shared expert and the two
-                # acc_f32 adds (M == 1: the down GEMV only, its gate/up ran
-                # with the gate; same bits)
-                if M == 1:
-                    L.shared_expert_down_acc(hsf, *w["shared"][2:], yr, h, M, DIM, SI, stream=st)
-                else:
+                    # h = h + (yr + shared(h)): the shared expert and the
+                    # two acc_f32 adds
                     L.shared_expert_fp8_w13_acc(h, *w["shared"], yr, h, M, DIM, SI, sws, stream=st)
 
         step(0, torch.cuda.current_stream())

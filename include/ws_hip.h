@@ -407,6 +407,27 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
                         int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
                         float swiglu_limit, void *workspace, size_t workspace_bytes,
                         ws_stream_t stream);
+/* ws_moe_decode_route with the block's shared down projection and residual
+ * add folded in (no single reference counterpart; it replaces
+ * ws_moe_decode_route + ws_shared_expert_down_acc, the same bits): the
+ * shared expert's down GEMV ys [dim] = emit8(hs_shared) . w2_shared^T runs on
+ * extra workgroups of the routed gate/up launch (its weight stream joins the
+ * routed one), and the routed down kernel ends with h = h + (y + ys). y is
+ * written as by ws_moe_decode_route; hs_shared [shared_inter] is the f32
+ * SwiGLU state ws_moe_gate_shared_w13 wrote; w2_shared e4m3 [dim,
+ * shared_inter] with UE8M0 [dim/32, shared_inter/32]; ys [dim] f32 scratch
+ * (16-byte aligned) of the caller. shared_inter % 128 == 0, <= 8192. Softmax
+ * scores or dim > 8192 take the two separate calls. */
+int ws_moe_decode_route_shared(const float *logits, const float *bias, int score_func,
+                               float gate_temp, int norm_topk_prob, float route_scale,
+                               const float *x, const uint8_t *w1, const uint8_t *s1,
+                               const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                               const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                               int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                               float swiglu_limit, const float *hs_shared, const uint8_t *w2_shared,
+                               const uint8_t *s2_shared, int64_t shared_inter, float *ys,
+                               float *h, void *workspace, size_t workspace_bytes,
+                               ws_stream_t stream);
 
 /* ws_moe_decode_route with no workspace argument and no allocation. No
  * counterpart in the reference: for callers that cannot call hipMalloc or

@@ -6,6 +6,7 @@ replace, bit for bit (both are the same FP8 GEMV sums, in the same order):
                                   -> acc_f32(yr, h)   (engine.rs:4532)
   ws_moe_gate_shared_w13 + ws_shared_expert_down_acc
                                == ws_moe_gate_logits + the line above
+  ws_moe_decode_route_shared   == ws_moe_decode_route + ws_shared_expert_down_acc
 
 The unfused chains are themselves checked against the oracle
 (test_gpu_kernels.py, test_gpu_block.py). Both math modes."""
@@ -117,6 +118,52 @@ def test_gate_shared_split_bit_exact(mode, m, limit):
     torch.cuda.synchronize()
     assert torch.equal(lg.view(torch.int32), lg_want.view(torch.int32))
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+def _slabs(gen, E, dim, inter):
+    """Packed FP4 expert slabs (w1, s1, w3, s3, w2, s2) of E experts."""
+    def enc(rows, cols):
+        w = torch.empty((rows, cols), device=DEV).normal_(0.0, 0.02, generator=gen)
+        q = torch.empty((rows, cols // 2), dtype=torch.uint8, device=DEV)
+        sc = torch.empty((rows, cols // 32), dtype=torch.uint8, device=DEV)
+        L.weight_quant_fp4(w, q, sc, rows, cols)
+        return L.prepack_fp4_new(q, sc, rows, cols)
+    return enc(E * inter, dim) + enc(E * inter, dim) + enc(E * dim, inter)
+
+
+@pytest.mark.parametrize("E,score,limit", [(64, L.SCORE_SIGMOID, 10.0),
+                                           (96, L.SCORE_SQRTSOFTPLUS, 0.0)])
+def test_decode_route_shared_bit_exact(mode, E, score, limit):
+    dim, inter, k, si = 4096, 2048, 8, 2048
+    announce("moe_decode_route_shared mode=%d E=%d score=%d" % (mode, E, score))
+    gen = torch.Generator(device=DEV).manual_seed(300 + E)
+    routed = _slabs(gen, E, dim, inter)
+    w2s, s2s = _fp8(gen, dim, si)
+    logits = torch.randn(E, device=DEV, generator=gen)
+    bias = torch.randn(E, device=DEV, generator=gen) * 0.1
+    x = torch.randn(dim, device=DEV, generator=gen)
+    hsf = torch.randn(si, device=DEV, generator=gen) * 0.1
+    h0 = torch.randn(dim, device=DEV, generator=gen)
+    ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
+    outs = []
+    for fused in (False, True):
+        y = torch.full((dim,), float("nan"), device=DEV)
+        idx = torch.full((k,), -5, dtype=torch.int32, device=DEV)
+        w = torch.full((k,), float("nan"), device=DEV)
+        h = h0.clone()
+        if fused:
+            ys = torch.full((dim,), float("nan"), device=DEV)
+            L.moe_decode_route_shared(logits, bias, score, 1.0, 1, 2.5, x, *routed, y, idx, w, dim,
+                                      inter, E, k, hsf, w2s, s2s, si, ys, h, ws,
+                                      swiglu_limit=limit)
+        else:
+            L.moe_decode_route(logits, bias, score, 1.0, 1, 2.5, x, *routed, y, idx, w, dim,
+                               inter, E, k, ws, swiglu_limit=limit)
+            L.shared_expert_down_acc(hsf, w2s, s2s, y, h, 1, dim, si)
+        torch.cuda.synchronize()
+        outs.append((y, idx, w, h))
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32))
 
 
 def test_fused_rejects_bad_shapes():

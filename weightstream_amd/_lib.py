@@ -88,6 +88,9 @@ SIGNATURES = {
     "ws_fp8_gemv_acc": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_moe_gate_shared_w13": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _f, _p]),
     "ws_shared_expert_down_acc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_moe_decode_route_shared": (_i, [_p, _p, _i, _f, _i, _f, _p, _p, _p, _p, _p, _p, _p, _p,
+                                        _p, _p, _i64, _i64, _i64, _i64, _f, _p, _p, _p, _i64,
+                                        _p, _p, _p, C.c_size_t, _p]),
     "ws_shared_expert_fp8_w13_acc": (_i, [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p,
                                           C.c_size_t, _p]),
     "ws_expert_glu_quant": (_i, [_p] * 10 + [_i64, _i64, _i64, _i64, _f, _p]),

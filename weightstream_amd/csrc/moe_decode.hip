@@ -30,6 +30,7 @@
 #include <mutex>
 
 #include "ws_internal.hpp"
+#include "ws_kp.hpp"
 #include "ws_pack.hpp"
 #include "ws_route.hpp"
 
@@ -361,9 +362,9 @@ struct PickSrc {
 // CPL == 0: picks from `ps`. HF32: write h in f32 to hf [slot, inter]
 // (expert_glu) instead of its FP8 1x32 quantisation to hq / hs.
 template <bool EXACT, bool XF32, int CPL, bool HF32 = false>
-__global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
-    const uint8_t *xq, const uint8_t *xs, const float *xf, PickSrc ps, RouteArgs ra,
-    const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
+__device__ __forceinline__ void glu_body(
+    int bx, int by, const uint8_t *xq, const uint8_t *xs, const float *xf, const PickSrc &ps,
+    const RouteArgs &ra, const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
     const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
     uint8_t *__restrict__ hs, float *__restrict__ hf, int dim, int inter, int n_experts,
     int top_k, float limit, int tpw) {
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     uint8_t *xq_l = lds;
     uint8_t *xs_l = lds + dim;
     __shared__ float gu[kGluKParts][2][32];
-    int slot = blockIdx.y;
+    int slot = by;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int ksteps = dim / 128;
 
@@ -446,7 +447,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     // whole workgroup: a pick another rank owns (or a row outside the slab)
     if (e < 0 || e >= n_experts) return;
 
-    const int tile = blockIdx.x * tpw + (tpw == 2 ? sub : 0);
+    const int tile = bx * tpw + (tpw == 2 ? sub : 0);
     int k0, k1;
     k_part(ksteps, tpw == 2 ? 0 : sub, kparts, k0, k1);
     const size_t wmat = (size_t)inter * (dim / 2);
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
             if (lane < top_k) {
                 pk_l[lane] = pk;
                 pw_l[lane] = pw;
-                if (blockIdx.x == 0 && slot == 0) {
+                if (bx == 0 && slot == 0) {
                     ra.idx_out[lane] = pk;
                     ra.w_out[lane] = pw;
                 }
@@ -491,10 +492,10 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     }
     __syncthreads();
     if (w >= tpw) return;
-    // wave w finishes tile blockIdx.x * tpw + w; lanes 0-31 own its 32 values,
+    // wave w finishes tile bx * tpw + w; lanes 0-31 own its 32 values,
     // lanes 32-63 mirror them so the half-wave reduction stays uniform, and do
     // not store. K halves (tpw == 1) are added in fixed order.
-    const int otile = blockIdx.x * tpw + w;
+    const int otile = bx * tpw + w;
     const int n = lane & 31;
     float g = gu[w][0][n], u = gu[w][1][n];
     for (int q = 1; q < kparts; q++) {
@@ -518,6 +519,48 @@ __global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
     }
 }
 
+template <bool EXACT, bool XF32, int CPL, bool HF32 = false>
+__global__ __launch_bounds__(kDecThreads) void expert_glu_quant_kernel(
+    const uint8_t *xq, const uint8_t *xs, const float *xf, PickSrc ps, RouteArgs ra,
+    const uint8_t *__restrict__ w1, const uint8_t *__restrict__ s1,
+    const uint8_t *__restrict__ w3, const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq,
+    uint8_t *__restrict__ hs, float *__restrict__ hf, int dim, int inter, int n_experts,
+    int top_k, float limit, int tpw) {
+    glu_body<EXACT, XF32, CPL, HF32>(blockIdx.x, blockIdx.y, xq, xs, xf, ps, ra, w1, s1, w3, s3,
+                                     hq, hs, hf, dim, inter, n_experts, top_k, limit, tpw);
+}
+
+// The routed gate/up kernel with the shared expert's down GEMV on extra
+// workgroups (rows top_k.. of the grid): ys [sdim] = emit8(hsf) . w2s^T, the
+// 16-column-strip GEMV with the f32 activation quantised in the kernel (the
+// same sums as ws_fp8_gemm of ws_emit8's bytes). Its weight stream joins the
+// routed one; neither part reads the other's output.
+struct SharedDown {
+    const float *hsf;
+    const uint8_t *w2, *s2;
+    float *ys;
+    int dim, inter;
+};
+
+template <bool EXACT, int CPL>
+__global__ __launch_bounds__(kDecThreads) void glu_shared_down_kernel(
+    const float *xf, RouteArgs ra, const uint8_t *__restrict__ w1,
+    const uint8_t *__restrict__ s1, const uint8_t *__restrict__ w3,
+    const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq, uint8_t *__restrict__ hs, int dim,
+    int inter, int n_experts, int top_k, float limit, int tpw, SharedDown sd) {
+    if ((int)blockIdx.y < top_k) {
+        glu_body<EXACT, true, CPL, false>(blockIdx.x, blockIdx.y, nullptr, nullptr, xf, PickSrc{},
+                                          ra, w1, s1, w3, s3, hq, hs, nullptr, dim, inter,
+                                          n_experts, top_k, limit, tpw);
+        return;
+    }
+    const int b = (blockIdx.y - top_k) * gridDim.x + blockIdx.x;
+    if (b >= sd.dim / 16) return;  // whole workgroup
+    kp_body<1, 1, 1, 8, false, kUe8m0, kOutF32, 2, EXACT, true>(
+        b, 0, 0, (const uint8_t *)sd.hsf, nullptr, sd.w2, sd.s2, sd.ys, 1, sd.dim, sd.inter, 1,
+        nullptr, 32, nullptr, 0.0f, 16);
+}
+
 // Picks of the down kernel: the top-k output (local == nullptr; picks outside
 // [0, E) skipped) or moe_local_slots' lists with the global ids in idx.
 struct ReducePicks {
@@ -530,7 +573,7 @@ template <bool EXACT>
 __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const uint8_t *hq, const uint8_t *hs, ReducePicks pk,
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ y, int dim,
-    int inter, int n_experts, int top_k) {
+    int inter, int n_experts, int top_k, float *hres, const float *ys) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float part[kMaxTopkDec][kRedWaves][16];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -615,6 +658,8 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
             acc = acc + pe;
         }
         y[row0 + t] = acc;
+        // with hres: the block's residual add h = h + (y + ys) (acc_f32 twice)
+        if (hres) hres[row0 + t] = hres[row0 + t] + (acc + ys[row0 + t]);
     }
 }
 
@@ -677,17 +722,20 @@ static int glu_launch(const uint8_t *xq, const uint8_t *xs, const float *xf, con
 
 static int reduce_launch(const uint8_t *hq, const uint8_t *hs, const ReducePicks &pk,
                          const uint8_t *w2, const uint8_t *s2, float *y, int64_t dim,
-                         int64_t inter, int64_t n_experts, int64_t top_k, hipStream_t stream) {
+                         int64_t inter, int64_t n_experts, int64_t top_k, hipStream_t stream,
+                         float *hres = nullptr, const float *ys = nullptr) {
     const bool exact = math_mode() == WS_MATH_EXACT;
     size_t lds = exact ? (size_t)top_k * inter * 2
                        : (size_t)top_k * inter + (size_t)top_k * (inter / 32);
     dim3 grid((unsigned)(dim / 16));
     if (exact)
         hipLaunchKernelGGL(expert_reduce_kernel<true>, grid, dim3(kRedThreads), lds, stream, hq,
-                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k);
+                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k,
+                           hres, ys);
     else
         hipLaunchKernelGGL(expert_reduce_kernel<false>, grid, dim3(kRedThreads), lds, stream, hq,
-                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k);
+                           hs, pk, w2, s2, y, (int)dim, (int)inter, (int)n_experts, (int)top_k,
+                           hres, ys);
     return launch_status();
 }
 
@@ -1008,6 +1056,84 @@ int ws_moe_decode_route(const float *logits, const float *bias, int score_func, 
     if (rc) return rc;
     return reduce_launch(hq, hs, ReducePicks{topk_idx, nullptr, nullptr, 0}, w2, s2, y, dim, inter,
                          n_experts, top_k, stream);
+}
+
+int ws_moe_decode_route_shared(const float *logits, const float *bias, int score_func,
+                               float gate_temp, int norm_topk_prob, float route_scale,
+                               const float *x, const uint8_t *w1, const uint8_t *s1,
+                               const uint8_t *w3, const uint8_t *s3, const uint8_t *w2,
+                               const uint8_t *s2, float *y, int32_t *topk_idx, float *topk_w,
+                               int64_t dim, int64_t inter, int64_t n_experts, int64_t top_k,
+                               float swiglu_limit, const float *hs_shared, const uint8_t *w2_shared,
+                               const uint8_t *s2_shared, int64_t shared_inter, float *ys,
+                               float *h, void *workspace, size_t workspace_bytes,
+                               ws_stream_t stream) {
+    if (!hs_shared || !w2_shared || !s2_shared || !ys || !h) return WS_ERR_INVALID_ARG;
+    if (shared_inter <= 0 || shared_inter % 128) return WS_ERR_SHAPE;
+    if (((uintptr_t)hs_shared | (uintptr_t)w2_shared | (uintptr_t)ys | (uintptr_t)h) & 15 ||
+        ((uintptr_t)s2_shared & 3))
+        return WS_ERR_INVALID_ARG;
+    const bool fused_path = logits && bias && score_func != WS_SCORE_SOFTMAX &&
+                            score_func >= WS_SCORE_SOFTMAX && score_func <= WS_SCORE_SQRTSOFTPLUS &&
+                            dim <= kMaxDimF32 && shared_inter <= 8192 && n_experts <= kMaxExperts &&
+                            top_k <= kMaxTopk && top_k <= n_experts;
+    if (!fused_path) {
+        // the same results through the separate launches
+        int rc = ws_moe_decode_route(logits, bias, score_func, gate_temp, norm_topk_prob,
+                                     route_scale, x, w1, s1, w3, s3, w2, s2, y, topk_idx, topk_w,
+                                     dim, inter, n_experts, top_k, swiglu_limit, workspace,
+                                     workspace_bytes, stream);
+        if (rc) return rc;
+        return ws_shared_expert_down_acc(hs_shared, w2_shared, s2_shared, y, h, 1, dim,
+                                         shared_inter, stream);
+    }
+    if (!x || !workspace || !topk_idx || !topk_w) return WS_ERR_INVALID_ARG;
+    int rc = check_decode_shapes(dim, inter, n_experts, top_k);
+    if (rc) return rc;
+    if (dim % 16) return WS_ERR_SHAPE;
+    if (workspace_bytes < ws_moe_decode_workspace_size(dim, inter, top_k) || !aligned16(workspace))
+        return WS_ERR_INVALID_ARG;
+    if (((uintptr_t)x & 15) || !aligned16(w1) || !aligned16(w3) || !aligned16(w2) ||
+        ((uintptr_t)s1 & 7) || ((uintptr_t)s3 & 7) || ((uintptr_t)s2 & 7) || !w1 || !s1 || !w3 ||
+        !s3 || !w2 || !s2 || !y)
+        return WS_ERR_INVALID_ARG;
+    uint8_t *hq = (uint8_t *)workspace;
+    uint8_t *hs = hq + align256(top_k * inter);
+    const RouteArgs ra{logits, bias, score_func, gate_temp, norm_topk_prob, route_scale,
+                       topk_idx, topk_w};
+    const SharedDown sd{hs_shared, w2_shared, s2_shared, ys, (int)dim, (int)shared_inter};
+    // the routed grid of glu_launch, plus rows of workgroups for the shared
+    // down GEMV (one per 16 output columns)
+    const int tpw = (inter / 32) * top_k >= 512 ? 2 : 1;
+    const int gx = (int)(inter / 32 / tpw);
+    const int kp_rows = (int)((dim / 16 + gx - 1) / gx);
+    dim3 grid((unsigned)gx, (unsigned)(top_k + kp_rows));
+    const bool exact = math_mode() == WS_MATH_EXACT;
+    const size_t glu_lds = exact ? (size_t)dim * 2 : (size_t)dim + dim / 32;
+    const size_t kp_lds = (size_t)8 * 16 * 16 * 4 + (size_t)(shared_inter + 16) +
+                          (size_t)(shared_inter / 32);
+    const size_t lds = glu_lds > kp_lds ? glu_lds : kp_lds;
+    const int cpl = n_experts <= 128 ? 2 : n_experts <= 256 ? 4 : n_experts <= 384 ? 6
+                  : n_experts <= 512 ? 8 : 16;
+#define WS_GSD(EX, CPL)                                                                         \
+    hipLaunchKernelGGL((glu_shared_down_kernel<EX, CPL>), grid, dim3(kDecThreads), lds, stream, x, \
+                       ra, w1, s1, w3, s3, hq, hs, (int)dim, (int)inter, (int)n_experts,          \
+                       (int)top_k, swiglu_limit, tpw, sd)
+#define WS_GSD_R(EX)                          \
+    switch (cpl) {                            \
+        case 2: WS_GSD(EX, 2); break;         \
+        case 4: WS_GSD(EX, 4); break;         \
+        case 6: WS_GSD(EX, 6); break;         \
+        case 8: WS_GSD(EX, 8); break;         \
+        default: WS_GSD(EX, 16); break;       \
+    }
+    if (exact) { WS_GSD_R(true) } else { WS_GSD_R(false) }
+#undef WS_GSD_R
+#undef WS_GSD
+    rc = launch_status();
+    if (rc) return rc;
+    return reduce_launch(hq, hs, ReducePicks{topk_idx, nullptr, nullptr, 0}, w2, s2, y, dim, inter,
+                         n_experts, top_k, stream, h, ys);
 }
 
 }  // extern "C"

@@ -1,0 +1,355 @@
+// The 16-column-strip GEMM/GEMV body (gemm.hip's gemm_kp_kernel) as a
+// device function, so that other launches (the fused decode steps) can run
+// it on some of their workgroups.
+#pragma once
+
+#include "ws_internal.hpp"
+
+namespace ws {
+
+enum ScaleMode { kUe8m0 = 0, kF32s = 1 };
+// kOutAcc: C += sum; kOutAcc2: C = C + (aux + sum); kOutSwiglu: fragment 0
+// is a gate column, fragment 1 the up column jstride rows further, and C gets
+// silu(min(g, L)) * clamp(u, -L, L) (the three used by the fused GEMV paths,
+// one K split only)
+enum OutMode { kOutF32 = 0, kOutBf16 = 1, kOutAcc = 2, kOutAcc2 = 3, kOutSwiglu = 4 };
+static_assert(kOutAcc == kGemvAcc && kOutAcc2 == kGemvAcc2 && kOutSwiglu == kGemvSwiglu, "");
+
+// ---- K-parallel GEMM: one workgroup per 16 output columns -----------------
+// HBM-bound shapes (M <= a few hundred, e.g. M=128, K=4096): the weight matrix
+// must cross HBM exactly once, so a workgroup owns a 16*NF-column strip of B
+// for all K and up to 16*MF*GMH rows of A. Its GMH x GK waves split the rows in
+// GMH halves and K in GK parts; a wave streams its K part in double-buffered
+// register stages of U 128-K steps (clamped, unconditional loads: one wait per
+// stage). The GK partial sums meet in LDS and are added in wave order
+// (deterministic). The activation scales of the workgroup's rows (f32, or a
+// step's four UE8M0 bytes) are staged in LDS once, transposed to [step][row].
+template <int MF, int NF, int U>
+struct KpStage {
+    uint4 a[U][MF][2];
+    uint32_t sa[U][MF];
+    uint4 b[U][NF][2];
+    uint32_t sb[U][NF];
+    float sbf[U];
+};
+
+constexpr int kKpMaxSaWords = 16;  // activation scale words staged per thread
+
+//
+// AF32: A is f32 (M <= 16 rows); the workgroup quantises it per 1x32 block
+// (the act_quant rule, quant_fp8_block32: the bytes ws_emit8 writes) into
+// LDS, rows K + 16 bytes apart, while its first weight stages are in flight,
+// and the waves read their A fragments and scale words from there.
+template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT,
+          bool AF32 = false>
+__device__ __forceinline__ void kp_body(int bx, int by, int bz, const uint8_t *A, const void *SA,
+                                        const uint8_t *__restrict__ B, const void *__restrict__ SB,
+                                        void *__restrict__ C, int M, int N, int K, int S,
+                                        float *__restrict__ part_out, int sb_div, const float *aux,
+                                        float limit, int jstride) {
+    constexpr int kRows = 16 * MF * GMH;
+    constexpr int kCols = 16 * NF;
+    static_assert(!AF32 || (MF == 1 && GMH == 1 && SMODE == kUe8m0 && !BFP4), "AF32: a GEMV");
+    static_assert(OMODE != kOutSwiglu || NF == 2, "SwiGLU pairs two fragments");
+    // UE8M0 activation scales: staged in LDS for blocks of rows; a single
+    // 16-row fragment (GEMV) loads its word per step instead (no prologue)
+    constexpr bool kStageSa = !AF32 && (SMODE == kF32s || kRows > 16);
+    constexpr int kThreads = 64 * GMH * GK;
+    extern __shared__ __align__(16) float kp_lds[];
+    float *part = kp_lds;                         // [GK][kRows][kCols]
+    float *sa_l = kp_lds + GK * kRows * kCols;    // [ksteps][kRows] (f32-scale mode)
+    uint8_t *a_l = (uint8_t *)sa_l;               // AF32: [M][K + 16] e4m3
+    const int a_pitch = K + 16;
+    uint8_t *as_l = a_l + (size_t)M * a_pitch;    // AF32: [M][K / 32] UE8M0
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int wk = w % GK, wm = w / GK;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = bx * (OMODE == kOutSwiglu ? 16 : kCols);
+    const int mb = by * kRows;                   // workgroup's first row
+    const int ml = wm * 16 * MF;                 // wave's first row within the workgroup
+    const int ksteps = K / 128;
+    // K split S ways over bz (S > 1: f32 partial planes, added in
+    // split order by split_reduce_kernel), then over the GK waves
+    const int kz0 = bz * ksteps / S, kzn = (bz + 1) * ksteps / S - kz0;
+    const int k0 = kz0 + wk * kzn / GK, k1 = kz0 + (wk + 1) * kzn / GK;
+    const int kbn = K / 32, kb128 = K / 128;
+
+    // activation scales of the workgroup's rows, one 32-bit word per (row,
+    // step): the f32 scale, or the step's four UE8M0 bytes. Loaded first
+    // and staged in LDS as [step][row].
+    // four steps per 16-byte load when the rows allow it, else word by word
+    uint32_t sav[kKpMaxSaWords];
+    const int nsa = kRows * ksteps;  // <= kThreads * kKpMaxSaWords (checked on the host)
+    const bool quad = (ksteps % 4) == 0 && (((uintptr_t)SA & 15) == 0);
+    if (kStageSa) {
+        if (quad) {
+#pragma unroll
+            for (int j = 0; j < kKpMaxSaWords / 4; j++) {
+                // words e..e+3 = row_local * ksteps + ks .. +3
+                const int e = min((j * kThreads + t) * 4, nsa - 4);
+                const int rl = e / ksteps, ks = e % ksteps;
+                const int row = min(mb + rl, M - 1);
+                const uint4 v = SMODE == kF32s
+                                    ? *(const uint4 *)((const uint32_t *)SA + (size_t)row * kb128 + ks)
+                                    : *(const uint4 *)((const uint8_t *)SA + (size_t)row * kbn + ks * 4);
+                sav[4 * j] = v.x;
+                sav[4 * j + 1] = v.y;
+                sav[4 * j + 2] = v.z;
+                sav[4 * j + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < kKpMaxSaWords; j++) {
+                const int e = min(j * kThreads + t, nsa - 1);
+                const int rl = e / ksteps, ks = e % ksteps;
+                const int row = min(mb + rl, M - 1);
+                sav[j] = SMODE == kF32s ? *((const uint32_t *)SA + (size_t)row * kb128 + ks)
+                                        : *(const uint32_t *)((const uint8_t *)SA + (size_t)row * kbn + ks * 4);
+            }
+        }
+        mem_order();
+    }
+
+    const uint8_t *arow[MF];
+    const uint8_t *sarow[MF];
+#pragma unroll
+    for (int i = 0; i < MF; i++) {
+        const int row = min(mb + ml + 16 * i + r, M - 1);
+        arow[i] = A + (size_t)row * K + (EXACT ? g * 32 : g * 16);
+        sarow[i] = (const uint8_t *)SA + (size_t)row * kbn;
+    }
+    const uint8_t *brow[NF];
+    const uint8_t *sbrow[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        const int col = n0 + (OMODE == kOutSwiglu ? j * jstride : 16 * j) + r;
+        brow[j] = BFP4 ? B + (size_t)col * (K / 2) + g * 16
+                       : B + (size_t)col * K + (EXACT ? g * 32 : g * 16);
+        // FP8 weight scales: one row per 32-row block, or per row (sb_div 1)
+        sbrow[j] = (const uint8_t *)SB + (size_t)(BFP4 ? col : col / sb_div) * kbn;
+    }
+    const float *sbf_row = (const float *)SB + (size_t)(n0 / 128) * kb128;
+
+    auto load = [&](KpStage<MF, NF, U> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int ks = max(min(ks0 + u, k1 - 1), 0);
+#pragma unroll
+            for (int i = 0; i < MF; i++) {
+                if (AF32) break;  // A is read from LDS at use
+                const uint8_t *p = arow[i] + (size_t)ks * 128;
+                st.a[u][i][0] = ldg16(p);
+                st.a[u][i][1] = ldg16(p + (EXACT ? 16 : 64));
+                if (!kStageSa) st.sa[u][i] = *(const uint32_t *)(sarow[i] + ks * 4) >> (8 * g);
+            }
+#pragma unroll
+            for (int j = 0; j < NF; j++) {
+                if (BFP4) {
+                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                } else {
+                    const uint8_t *p = brow[j] + (size_t)ks * 128;
+                    st.b[u][j][0] = ldg16_stream(p);
+                    st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+                }
+                if (SMODE == kUe8m0) st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
+            }
+            if (SMODE == kF32s) st.sbf[u] = sbf_row[ks];
+        }
+    };
+
+    v4f acc[MF][NF];
+#pragma unroll
+    for (int i = 0; i < MF; i++)
+#pragma unroll
+        for (int j = 0; j < NF; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const KpStage<MF, NF, U> &st, int ks0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int ks = ks0 + u;
+            if (ks >= k1) continue;  // uniform
+            if (EXACT) {
+                v8bf bq[NF][4];
+#pragma unroll
+                for (int j = 0; j < NF; j++) {
+                    const float sbv = SMODE == kUe8m0 ? e8m0_to_f32(st.sb[u][j] & 0xFF) : 1.0f;
+                    if (BFP4) cvt_fp4x32(st.b[u][j][0], sbv, bq[j]);
+                    else cvt_fp8x32(st.b[u][j][0], st.b[u][j][1], sbv, bq[j]);
+                }
+#pragma unroll
+                for (int i = 0; i < MF; i++) {
+                    v8bf aq[4];
+                    uint4 a0, a1;
+                    uint32_t saw;
+                    if (AF32) {
+                        const int rl = min(r, M - 1);
+                        const uint8_t *ap = a_l + rl * a_pitch + ks * 128 + g * 32;
+                        a0 = *(const uint4 *)ap;
+                        a1 = *(const uint4 *)(ap + 16);
+                        saw = *(const uint32_t *)(as_l + rl * (K / 32) + ks * 4) >> (8 * g);
+                    } else {
+                        a0 = st.a[u][i][0];
+                        a1 = st.a[u][i][1];
+                        saw = !kStageSa ? st.sa[u][i]
+                                        : ((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g);
+                    }
+                    const float sav_f = SMODE == kUe8m0 ? e8m0_to_f32(saw & 0xFF) : 1.0f;
+                    cvt_fp8x32(a0, a1, sav_f, aq);
+#pragma unroll
+                    for (int j = 0; j < NF; j++) {
+                        if (SMODE == kUe8m0) {
+                            acc[i][j] = mfma_bf16_k128(aq, bq[j], acc[i][j]);
+                        } else {
+                            const v4f p = mfma_bf16_k128(aq, bq[j], v4f{0.f, 0.f, 0.f, 0.f});
+                            const float4 sa4 = *(const float4 *)(sa_l + ks * kRows + ml + 16 * i + 4 * g);
+                            const float sa_v[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                acc[i][j][v] = acc[i][j][v] + p[v] * (sa_v[v] * st.sbf[u]);
+                        }
+                    }
+                }
+            } else {
+                v8i b[NF];
+#pragma unroll
+                for (int j = 0; j < NF; j++)
+                    b[j] = BFP4 ? frag_from4(st.b[u][j][0]) : frag_from(st.b[u][j][0], st.b[u][j][1]);
+#pragma unroll
+                for (int i = 0; i < MF; i++) {
+                    v8i a;
+                    int sai;
+                    if (AF32) {
+                        const int rl = min(r, M - 1);
+                        const uint8_t *ap = a_l + rl * a_pitch + ks * 128 + g * 16;
+                        a = frag_from(*(const uint4 *)ap, *(const uint4 *)(ap + 64));
+                        sai = (int)((*(const uint32_t *)(as_l + rl * (K / 32) + ks * 4) >> (8 * g)) & 0xFF);
+                    } else {
+                        a = frag_from(st.a[u][i][0], st.a[u][i][1]);
+                        sai = SMODE != kUe8m0 ? 0
+                              : !kStageSa     ? (int)(st.sa[u][i] & 0xFF)
+                                              : (int)((((const uint32_t *)sa_l)[ks * kRows + ml + 16 * i + r] >> (8 * g)) & 0xFF);
+                    }
+#pragma unroll
+                    for (int j = 0; j < NF; j++) {
+                        if (SMODE == kUe8m0) {
+                            acc[i][j] = BFP4 ? mfma_scaled<kFmtFp8, kFmtFp4>(a, b[j], acc[i][j], sai,
+                                                                             (int)(st.sb[u][j] & 0xFF))
+                                             : mfma_scaled<kFmtFp8, kFmtFp8>(a, b[j], acc[i][j], sai,
+                                                                             (int)(st.sb[u][j] & 0xFF));
+                        } else {
+                            const v4f p = mfma_scaled<kFmtFp8, kFmtFp8>(a, b[j], v4f{0.f, 0.f, 0.f, 0.f},
+                                                                        kScaleOne, kScaleOne);
+                            const float4 sa4 = *(const float4 *)(sa_l + ks * kRows + ml + 16 * i + 4 * g);
+                            const float sa_v[4] = {sa4.x, sa4.y, sa4.z, sa4.w};
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                acc[i][j][v] = acc[i][j][v] + p[v] * (sa_v[v] * st.sbf[u]);
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    KpStage<MF, NF, U> s0, s1;
+    load(s0, k0);
+    mem_order();
+    load(s1, k0 + U);
+    mem_order();
+    if (AF32) {
+        // four values per lane, a 1x32 block per 8 lanes; every lane of a
+        // block takes part in its maximum (dead blocks quantise zeros and
+        // store nothing; M K % 32 == 0)
+        const float4 *X = (const float4 *)A;
+        const int n4 = M * K / 4;
+        for (int i0 = 0; i0 < n4; i0 += kThreads) {
+            const int i = i0 + t;
+            const bool live = i < n4;
+            uint32_t sbyte;
+            const uint32_t q = quant_fp8_block32_x4(live ? X[i] : float4{0.f, 0.f, 0.f, 0.f},
+                                                    &sbyte);
+            if (live) {
+                const int row = (4 * i) / K, col = 4 * i - row * K;
+                *(uint32_t *)(a_l + row * a_pitch + col) = q;
+                if ((t & 7) == 0) as_l[row * (K / 32) + col / 32] = (uint8_t)sbyte;
+            }
+        }
+        lds_barrier();
+    }
+    if (kStageSa) {
+        uint32_t *sa_w = (uint32_t *)sa_l;
+#pragma unroll
+        for (int j = 0; j < kKpMaxSaWords; j++) {
+            const int e = quad ? ((j / 4) * kThreads + t) * 4 + j % 4 : j * kThreads + t;
+            if (e >= nsa) continue;
+            const int rl = e / ksteps, ks = e % ksteps;
+            sa_w[ks * kRows + rl] = sav[j];
+        }
+        lds_barrier();
+    }
+
+    // steady state: both stages reloaded unconditionally (straight-line body)
+    const int nst = (k1 - k0 + U - 1) / U;
+    int i = 0, ks0 = k0;
+    for (; i + 3 < nst; i += 2, ks0 += 2 * U) {
+        compute(s0, ks0);
+        load(s0, ks0 + 2 * U);
+        compute(s1, ks0 + U);
+        load(s1, ks0 + 3 * U);
+    }
+    const int rest = nst - i;
+    if (rest == 3) {
+        compute(s0, ks0);
+        load(s0, ks0 + 2 * U);
+        compute(s1, ks0 + U);
+        compute(s0, ks0 + 2 * U);
+    } else {
+        if (rest >= 1) compute(s0, ks0);
+        if (rest == 2) compute(s1, ks0 + U);
+    }
+
+    // D[m][n]: lane -> row 4g+v of fragment i, column 16j + r
+#pragma unroll
+    for (int f = 0; f < MF; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                part[(wk * kRows + ml + 16 * f + 4 * g + v) * kCols + 16 * j + r] = acc[f][j][v];
+    __syncthreads();
+    auto wave_sum = [&](int rl, int c) {
+        float sum = part[rl * kCols + c];
+#pragma unroll
+        for (int q = 1; q < GK; q++) sum = sum + part[(q * kRows + rl) * kCols + c];
+        return sum;
+    };
+    if (OMODE == kOutSwiglu) {
+        // C [M][N]: N = the intermediate width (jstride)
+        for (int o = t; o < kRows * 16; o += kThreads) {
+            const int rl = o / 16, c = o % 16;
+            const int row = mb + rl;
+            if (row >= M) continue;
+            float gv = wave_sum(rl, c), uv = wave_sum(rl, c + 16);
+            if (limit > 0.0f) {
+                uv = rclamp(uv, -limit, limit);
+                gv = fminf(gv, limit);
+            }
+            ((float *)C)[(size_t)row * N + n0 + c] = ws_silu(gv) * uv;
+        }
+        return;
+    }
+    for (int o = t; o < kRows * kCols; o += kThreads) {
+        const int rl = o / kCols, c = o % kCols;
+        const int row = mb + rl;
+        if (row >= M) continue;
+        const float sum = wave_sum(rl, c);
+        const size_t at = (size_t)row * N + n0 + c;
+        if (S > 1) part_out[((size_t)bz * M + row) * N + n0 + c] = sum;
+        else if (OMODE == kOutF32) ((float *)C)[at] = sum;
+        else if (OMODE == kOutBf16) ((uint16_t *)C)[at] = f32_to_bf16(sum);
+        else if (OMODE == kOutAcc) ((float *)C)[at] = ((float *)C)[at] + sum;
+        else ((float *)C)[at] = ((float *)C)[at] + (aux[at] + sum);
+    }
+}
+
+}  // namespace ws

@@ -413,6 +413,20 @@ def moe_decode_route(logits, bias, score_func, gate_temp, norm_topk_prob, route_
           workspace.numel() * workspace.element_size(), _s(stream))
 
 
+def moe_decode_route_shared(logits, bias, score_func, gate_temp, norm_topk_prob, route_scale, x,
+                            w1, s1, w3, s3, w2, s2, y, topk_idx, topk_w, dim, inter, n_experts,
+                            top_k, hs_shared, w2_shared, s2_shared, shared_inter, ys, h,
+                            workspace, swiglu_limit=10.0, stream=None):
+    """moe_decode_route with the shared down GEMV on extra workgroups of the
+    gate/up launch and h = h + (y + ys) at the end of the down kernel."""
+    _call("ws_moe_decode_route_shared", _ptr(logits), _ptr(bias), int(score_func),
+          float(gate_temp), int(norm_topk_prob), float(route_scale), _ptr(x), _ptr(w1), _ptr(s1),
+          _ptr(w3), _ptr(s3), _ptr(w2), _ptr(s2), _ptr(y), _ptr(topk_idx), _ptr(topk_w), dim,
+          inter, n_experts, top_k, swiglu_limit, _ptr(hs_shared), _ptr(w2_shared),
+          _ptr(s2_shared), shared_inter, _ptr(ys), _ptr(h), _ptr(workspace),
+          workspace.numel() * workspace.element_size(), _s(stream))
+
+
 def moe_decode_route_noalloc(logits, bias, score_func, gate_temp, norm_topk_prob, route_scale, x,
                              w1, s1, w3, s3, w2, s2, y, topk_idx, topk_w, dim, inter, n_experts,
                              top_k, swiglu_limit=10.0, stream=None):
