@@ -148,6 +148,27 @@ def test_fp8_gemm_matches_oracle(m, n, k, gemm_path):
     assert same >= 0.999, same
 
 
+@pytest.mark.parametrize("m", [1, 8, 64])
+def test_fp8_gemm_out_projection_shape_matches_oracle(m, gemm_path):
+    """The config-5 attention out-projection shape, N=4096, K=8192, at the
+    block's M in {1, 8, 64}: f32 and bf16 outputs against the oracle's
+    dequantise-then-f32 GEMM (or_gemm_q) on sampled rows."""
+    n, k = 4096, 8192
+    rng = np.random.default_rng(1500 + m)
+    aq, as_, wq, ws = _quantised_case(rng, m, n, k, False)
+    rows = sorted({0, m // 2, m - 1})
+    want = O.gemm_q(np.ascontiguousarray(aq[rows]), np.ascontiguousarray(as_[rows]), len(rows),
+                    wq, ws, n, k, False)
+    announce("fp8_gemm out-projection %s m=%d" % (gemm_path, m))
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    L.fp8_gemm(dev(aq), dev(as_), dev(wq), dev(ws), out, m, n, k)
+    assert_close(host(out)[rows], want, GEMM_TOL, "fp8_gemm %dx%dx%d" % (m, n, k))
+    ob = torch.empty((m, n), dtype=torch.int16, device=DEV)
+    L.fp8_gemm_bf16(dev(aq), dev(as_), dev(wq), dev(ws), ob, m, n, k)
+    got = (host(ob).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    assert_close(got[rows], want, 2.0 ** -8 + GEMM_TOL, "fp8_gemm_bf16 %dx%dx%d" % (m, n, k))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 4096), (8, 512, 1024), (128, 256, 2048),
                                    (33, 80, 512), (200, 192, 1024), (130, 8192, 256)])
 def test_fp4_gemm_matches_oracle(m, n, k, gemm_path):
