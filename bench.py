@@ -494,7 +494,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     (ws_fp8_gemv_acc), the shared gate/up GEMV + SwiGLU runs in the gate
     logits' launch (ws_moe_gate_shared_w13) and its down GEMV in the routed
     gate/up launch, the adds at the end of the routed down kernel
-    (ws_moe_decode_route_shared): five launches per layer, the unfused
+    (ws_moe_decode_route_shared): four launches per layer, the unfused
     chain's bits. Routed layers 2..4 are device copies of layer 1's packed
     experts (distinct memory, so no layer reads another's weights from
     cache). Reported per layer; bytes = weights touched once."""
