@@ -489,7 +489,7 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     the 384 routed FP4 experts (M=1: ws_moe_decode_route; M>1: ws_moe_topk +
     the grouped ws_moe_prefill), the shared FP8 expert (inter 2048; w1 and w3
     fused into one w13 matrix as the engine loads them, engine.rs:1520, one
-    gate/up GEMM as at :4067) and the two acc_f32 adds. For M <= 16 the
+    gate/up GEMM as at :4067) and the two acc_f32 adds. For M = 1 the
     out-projection with its token quantisation and residual add is one launch
     (ws_fp8_gemv_acc), the shared gate/up GEMV + SwiGLU runs in the gate
     logits' launch (ws_moe_gate_shared_w13) and its down GEMV in the routed
