@@ -112,11 +112,11 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 #pragma unroll
             for (int j = 0; j < WN; j++) {
                 if (BFP4) {
-                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                    st.b[u][j][0] = ldg16(brow[j] + (size_t)ks * 64);
                 } else {
                     const uint8_t *p = brow[j] + (size_t)ks * 128;
-                    st.b[u][j][0] = ldg16_stream(p);
-                    st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+                    st.b[u][j][0] = ldg16(p);
+                    st.b[u][j][1] = ldg16(p + (EXACT ? 16 : 64));
                 }
                 if (SMODE == kUe8m0)
                     st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * kb);
@@ -507,8 +507,8 @@ __global__ __launch_bounds__(64 * kAlWaves) void gemm_al_kernel(const uint8_t *A
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             const uint8_t *p = brow[j] + (size_t)ks * 128;
-            st.b[j][0] = ldg16_stream(p);
-            st.b[j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+            st.b[j][0] = ldg16(p);
+            st.b[j][1] = ldg16(p + (EXACT ? 16 : 64));
             if (SMODE == kUe8m0) st.sb[j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
         }
         if (SMODE == kF32s) st.sbf = sbf_row[ks];

@@ -145,11 +145,11 @@ __device__ __forceinline__ void kp_body(int bx, int by, int bz, const uint8_t *A
 #pragma unroll
             for (int j = 0; j < NF; j++) {
                 if (BFP4) {
-                    st.b[u][j][0] = ldg16_stream(brow[j] + (size_t)ks * 64);
+                    st.b[u][j][0] = ldg16(brow[j] + (size_t)ks * 64);
                 } else {
                     const uint8_t *p = brow[j] + (size_t)ks * 128;
-                    st.b[u][j][0] = ldg16_stream(p);
-                    st.b[u][j][1] = ldg16_stream(p + (EXACT ? 16 : 64));
+                    st.b[u][j][0] = ldg16(p);
+                    st.b[u][j][1] = ldg16(p + (EXACT ? 16 : 64));
                 }
                 if (SMODE == kUe8m0) st.sb[u][j] = *(const uint32_t *)(sbrow[j] + ks * 4) >> (8 * g);
             }
