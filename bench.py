@@ -606,6 +606,9 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device-to-device 5 times (calibrates the HBM "
                          "traffic counters against a known byte count) and exit")
+    ap.add_argument("--gemm-probe", type=int, default=0, metavar="N",
+                    help="only run the config-2 GEMM (M=128, K=4096, UE8M0, bf16 out) at this N "
+                         "60 times on rotated cold weights (for counter runs) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the hot path is built and measured on a single "
@@ -626,6 +629,24 @@ def main():
     from weightstream_amd import launch as L
     L.Hip.global_()
     dev = "cuda:0"
+    if args.gemm_probe:
+        m, n, k = 128, args.gemm_probe, 4096
+        x = torch.randn((m, k), device=dev)
+        aq = torch.empty((m, k), dtype=torch.uint8, device=dev)
+        asc = torch.empty((m, k // 32), dtype=torch.uint8, device=dev)
+        L.emit8(x, aq, asc, m * k)
+        copies = max(2, -(-400_000_000 // (n * k)))
+        w = torch.randn((n, k), device=dev) * 0.02
+        wq = torch.empty((copies, n, k), dtype=torch.uint8, device=dev)
+        wsc = torch.empty((copies, n // 32, k // 32), dtype=torch.uint8, device=dev)
+        for c in range(copies):
+            L.weight_quant_fp8(w, wq[c], wsc[c], n, k)
+        y = torch.empty((m, n), dtype=torch.int16, device=dev)
+        for i in range(60):
+            L.fp8_gemm_bf16(aq, asc, wq[i % copies], wsc[i % copies], y, m, n, k)
+        torch.cuda.synchronize()
+        print(json.dumps({"gemm_probe_n": n, "calls": 60}), flush=True)
+        return
     log("device:", torch.cuda.get_device_name(0))
 
     gen = torch.Generator(device=dev)
