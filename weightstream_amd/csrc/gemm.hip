@@ -249,7 +249,7 @@ __global__ __launch_bounds__(64 * GM * GK) void gemm_kernel(const uint8_t *__res
 }
 
 template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U, bool EXACT,
-          bool AF32 = false>
+          bool AF32 = false, bool ALDS = false>
 __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A, const void *SA,
                                                                 const uint8_t *__restrict__ B,
                                                                 const void *__restrict__ SB,
@@ -258,7 +258,7 @@ __global__ __launch_bounds__(64 * GMH * GK) void gemm_kp_kernel(const uint8_t *A
                                                                 float *__restrict__ part_out,
                                                                 int sb_div, const float *aux,
                                                                 float limit, int jstride) {
-    kp_body<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, EXACT, AF32>(
+    kp_body<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, EXACT, AF32, ALDS>(
         blockIdx.x, blockIdx.y, blockIdx.z, A, SA, B, SB, C, M, N, K, S, part_out, sb_div, aux,
         limit, jstride);
 }
@@ -297,16 +297,19 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     constexpr bool stage = SMODE == kF32s || rows > 16;
     if (stage && rows * ksteps > threads * kKpMaxSaWords)
         return -1;  // caller falls back to the general kernel
-    size_t lds = (size_t)GK * rows * 16 * NF * 4 + (size_t)ksteps * rows * 4;
+    // blocks of 32 or 64 rows read A through LDS (kp_body's ALDS)
+    constexpr bool alds = MF >= 2 && GMH == 1 && U == 1;
+    const size_t lds = kp_head_bytes<MF, NF, GMH, GK, alds>() + (size_t)ksteps * rows * 4;
+    if (lds > 160 * 1024) return -1;
     if (S < 1 || (S > 1 && !part)) return -1;
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows), (unsigned)S);
     if (math_mode() == WS_MATH_NATIVE)
-        hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
+        hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false, false, alds>),
+                           grid, dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
                            sb_div, nullptr, 0.0f, 16);
     else
-        hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true>), grid,
-                           dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
+        hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true, false, alds>),
+                           grid, dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
                            sb_div, nullptr, 0.0f, 16);
     int rc = launch_status();
     if (rc || S == 1) return rc;
