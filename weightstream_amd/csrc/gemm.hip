@@ -341,7 +341,7 @@ int kp_gemv_fused(int omode, const float *x, const uint8_t *w, const uint8_t *sw
     const bool ex = math_mode() == WS_MATH_EXACT;
     const int M = (int)m, N = (int)n, K = (int)k;
 #define WS_KPF(OM, NFV, E)                                                                     \
-    hipLaunchKernelGGL((gemm_kp_kernel<1, NFV, 1, 8, false, kUe8m0, OM, 2, E, true>), grid, block, \
+    hipLaunchKernelGGL((gemm_kp_kernel<1, NFV, 1, 8, false, kUe8m0, OM, 1, E, true>), grid, block, \
                        lds, stream, (const uint8_t *)x, (const void *)nullptr, w, (const void *)sw, \
                        (void *)out, M, N, K, 1, (float *)nullptr, 32, aux, limit, N)
     switch (omode) {
@@ -372,7 +372,7 @@ __global__ __launch_bounds__(512) void gate_w13_kernel(const float *h, const flo
         gate_pc_body<4, 1, false>(b % gx, b / gx, h, gw, logits, m, dim, n_experts);
         return;
     }
-    kp_body<1, 2, 1, 8, false, kUe8m0, kOutSwiglu, 2, EXACT, true>(
+    kp_body<1, 2, 1, 8, false, kUe8m0, kOutSwiglu, 1, EXACT, true>(
         b - n_gate, 0, 0, (const uint8_t *)h, nullptr, w13, s13, hs, m, inter, dim, 1, nullptr, 32,
         nullptr, limit, inter);
 }
@@ -1152,7 +1152,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         int rc;
         if (M <= 16) {
             const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
-            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream, S,
+            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, S,
                                                                (float *)wsp.ptr, sb_div);
         } else if (M <= 32) {
             rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
@@ -1201,7 +1201,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         // do not stage)
         if (M <= 16) {
             const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
-            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 2>(a, sa, b, sb, out, M, N, K, stream, S,
+            rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, S,
                                                                (float *)wsp.ptr);
         }
         else if (M <= 32) rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);

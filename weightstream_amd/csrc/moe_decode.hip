@@ -556,7 +556,7 @@ __global__ __launch_bounds__(kDecThreads) void glu_shared_down_kernel(
     }
     const int b = (blockIdx.y - top_k) * gridDim.x + blockIdx.x;
     if (b >= sd.dim / 16) return;  // whole workgroup
-    kp_body<1, 1, 1, 8, false, kUe8m0, kOutF32, 2, EXACT, true>(
+    kp_body<1, 1, 1, 8, false, kUe8m0, kOutF32, 1, EXACT, true>(
         b, 0, 0, (const uint8_t *)sd.hsf, nullptr, sd.w2, sd.s2, sd.ys, 1, sd.dim, sd.inter, 1,
         nullptr, 32, nullptr, 0.0f, 16);
 }
