@@ -130,12 +130,12 @@ __device__ __forceinline__ RankedPicks ranked_from_local(const int32_t *local,
 // LDS: EXACT -> bf16 values (x_lds); native -> e4m3 bytes + UE8M0 scales
 // (xq_lds, xs_lds). Returns the updated 16x16 accumulator (row i of the band
 // in D[i][*]).
-template <bool EXACT>
-__device__ __forceinline__ v4f fp4_compute(const Fp4Stage &st, v4f acc, const uint8_t *xq_lds,
+template <bool EXACT, int U>
+__device__ __forceinline__ v4f fp4_compute(const Fp4StageU<U> &st, v4f acc, const uint8_t *xq_lds,
                                            const uint8_t *xs_lds, const __bf16 *x_lds, int kb,
                                            int ks0, int kend) {
 #pragma unroll
-    for (int u = 0; u < kU; u++) {
+    for (int u = 0; u < U; u++) {
         const int ks = ks0 + u;
         if (ks >= kend) continue;  // uniform
         const uint32_t sw = stage_scale(st, u);
@@ -156,42 +156,46 @@ __device__ __forceinline__ v4f fp4_compute(const Fp4Stage &st, v4f acc, const ui
     return acc;
 }
 
-// Stream band steps [k0, k1) (k0 % 8 == 0) given the first two stages already
-// in flight (s0 = k0.., s1 = k0+kU..): one stage is multiplied while the
+// Stream band steps [k0, k1) (k0 % U == 0) given the first two stages already
+// in flight (s0 = k0.., s1 = k0+U..): one stage is multiplied while the
 // other's loads are outstanding. The steady-state loop reloads both stages
 // unconditionally, so its body is straight-line and each wait covers only the
 // stage about to be used; the last two or three stages are the tail.
-template <bool EXACT>
-__device__ __forceinline__ v4f fp4_stream(const Fp4Band &b, Fp4Stage &s0, Fp4Stage &s1,
+template <bool EXACT, int U>
+__device__ __forceinline__ v4f fp4_stream(const Fp4Band &b, Fp4StageU<U> &s0, Fp4StageU<U> &s1,
                                           const uint8_t *xq_lds, const uint8_t *xs_lds,
                                           const __bf16 *x_lds, int kb, int k0, int k1) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
-    const int nst = (k1 - k0 + kU - 1) / kU;
+    const int nst = (k1 - k0 + U - 1) / U;
     int i = 0, ks0 = k0;
-    for (; i + 3 < nst; i += 2, ks0 += 2 * kU) {
-        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
-        fp4_load(s0, b, ks0 + 2 * kU, k1);
-        acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
-        fp4_load(s1, b, ks0 + 3 * kU, k1);
+    for (; i + 3 < nst; i += 2, ks0 += 2 * U) {
+        acc = fp4_compute<EXACT, U>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        fp4_load(s0, b, ks0 + 2 * U, k1);
+        acc = fp4_compute<EXACT, U>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + U, k1);
+        fp4_load(s1, b, ks0 + 3 * U, k1);
     }
     const int rest = nst - i;
     if (rest == 3) {
-        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
-        fp4_load(s0, b, ks0 + 2 * kU, k1);
-        acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
-        acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0 + 2 * kU, k1);
+        acc = fp4_compute<EXACT, U>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        fp4_load(s0, b, ks0 + 2 * U, k1);
+        acc = fp4_compute<EXACT, U>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + U, k1);
+        acc = fp4_compute<EXACT, U>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0 + 2 * U, k1);
     } else {
-        if (rest >= 1) acc = fp4_compute<EXACT>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
-        if (rest == 2) acc = fp4_compute<EXACT>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + kU, k1);
+        if (rest >= 1) acc = fp4_compute<EXACT, U>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
+        if (rest == 2) acc = fp4_compute<EXACT, U>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + U, k1);
     }
     return acc;
 }
 
-// K range [k0, k1) of part `part` of `parts`, in whole 8-step stages
+// 128-K steps per register stage of the decode streams (two stages in
+// flight per wave)
+constexpr int kUD = 4;
+
+// K range [k0, k1) of part `part` of `parts`, in whole decode stages
 __device__ __forceinline__ void k_part(int ksteps, int part, int parts, int &k0, int &k1) {
-    const int stages = (ksteps + kU - 1) / kU;
-    k0 = min(ksteps, part * stages / parts * kU);
-    k1 = min(ksteps, (part + 1) * stages / parts * kU);
+    const int stages = (ksteps + kUD - 1) / kUD;
+    k0 = min(ksteps, part * stages / parts * kUD);
+    k1 = min(ksteps, (part + 1) * stages / parts * kUD);
 }
 
 // ---- operand preparation in LDS ------------------------------------------
@@ -454,10 +458,10 @@ __device__ __forceinline__ void glu_body(
     const size_t smat = (size_t)packed_fp4_scale_bytes(inter, dim);
     const Fp4Band band = fp4_band((mat ? w3 : w1) + (size_t)e * wmat,
                                   (mat ? s3 : s1) + (size_t)e * smat, tile * 2 + half, dim, lane);
-    Fp4Stage st0, st1;
+    Fp4StageU<kUD> st0, st1;
     fp4_load(st0, band, k0, k1);
     mem_order();
-    fp4_load(st1, band, k0 + kU, k1);
+    fp4_load(st1, band, k0 + kUD, k1);
     mem_order();
 
     // the routing weight and the picks' ranks
@@ -598,7 +602,7 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int ksteps = inter / 128;
     int ksplit = kRedWaves / (nv > 0 ? nv : 1);
     ksplit = ksplit < 1 ? 1 : ksplit;
-    const int stages = (ksteps + kU - 1) / kU;
+    const int stages = (ksteps + kUD - 1) / kUD;
     if (ksplit > stages) ksplit = stages;
     const int nunits = nv * ksplit;
     const size_t wmat = (size_t)dim * (inter / 2);
@@ -609,10 +613,10 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     const int e0 = __builtin_amdgcn_readlane(rp.e, p);
     Fp4Band band = fp4_band(w2 + (size_t)e0 * wmat, s2 + (size_t)e0 * smat, blockIdx.x, inter,
                             lane);
-    Fp4Stage s0, s1;
+    Fp4StageU<kUD> s0, s1;
     fp4_load(s0, band, k0, k1);
     mem_order();
-    fp4_load(s1, band, k0 + kU, k1);
+    fp4_load(s1, band, k0 + kUD, k1);
     mem_order();
 
     // EXACT: picks as bf16 (2 * top_k * inter bytes); native: e4m3 + scales
@@ -639,7 +643,7 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
         const int e = __builtin_amdgcn_readlane(rp.e, p);
         band = fp4_band(w2 + (size_t)e * wmat, s2 + (size_t)e * smat, blockIdx.x, inter, lane);
         fp4_load(s0, band, k0, k1);
-        fp4_load(s1, band, k0 + kU, k1);
+        fp4_load(s1, band, k0 + kUD, k1);
         v4f acc = fp4_stream<EXACT>(band, s0, s1, hq_l + (size_t)p * inter,
                                     hs_l + (size_t)p * (inter / 32), h_l + (size_t)p * inter,
                                     lane >> 4, k0, k1);

@@ -39,23 +39,31 @@ __device__ __forceinline__ Fp4Band fp4_band(const uint8_t *w, const uint8_t *s, 
                    ks};
 }
 
-struct Fp4Stage {
-    uint4 w[kU];
-    uint2 s;  // scale bytes of the kU steps
+// U steps of a band in registers (U = 8: a whole scale group; U = 4: half
+// of one, its four scale bytes in s.x)
+template <int U>
+struct Fp4StageU {
+    static_assert(U == 8 || U == 4, "stages of 8 or 4 steps");
+    uint4 w[U];
+    uint2 s;  // scale bytes of the U steps
 };
+using Fp4Stage = Fp4StageU<kU>;
 
-// Steps [ks0, ks0 + kU) of the band; steps at or past `kend` re-load step
+// Steps [ks0, ks0 + U) of the band; steps at or past `kend` re-load step
 // max(kend - 1, 0) (never used), keeping the loads unconditional so that one
 // counter wait covers a whole stage. An empty range (kend == 0, or a stage past
-// the end) thus still reads inside the band. ks0 % 8 == 0, kend <= ks_total.
-__device__ __forceinline__ void fp4_load(Fp4Stage &st, const Fp4Band &b, int ks0, int kend) {
+// the end) thus still reads inside the band. ks0 % U == 0, kend <= ks_total.
+template <int U>
+__device__ __forceinline__ void fp4_load(Fp4StageU<U> &st, const Fp4Band &b, int ks0, int kend) {
     const int last = kend > 0 ? kend - 1 : 0;
 #pragma unroll
-    for (int u = 0; u < kU; u++) {
+    for (int u = 0; u < U; u++) {
         int ks = min(ks0 + u, last);
         st.w[u] = ldg16_stream(b.w + (size_t)ks * 1024);
     }
-    st.s = *(const uint2 *)(b.s + (size_t)(min(ks0, last) / 8) * 512);
+    const int sk = min(ks0, last);
+    if (U == 8) st.s = *(const uint2 *)(b.s + (size_t)(sk / 8) * 512);
+    else st.s.x = *(const uint32_t *)(b.s + (size_t)(sk / 8) * 512 + (sk & 4));
 }
 
 // K range [k0, k1) of part `part` of `parts` over `ksteps` 128-K steps, in
@@ -66,7 +74,8 @@ __device__ __forceinline__ void k_part8(int ksteps, int part, int parts, int &k0
     k1 = min(ksteps, (part + 1) * stages / parts * kU);
 }
 
-__device__ __forceinline__ uint32_t stage_scale(const Fp4Stage &st, int u) {
+template <int U>
+__device__ __forceinline__ uint32_t stage_scale(const Fp4StageU<U> &st, int u) {
     return ((u < 4 ? st.s.x : st.s.y) >> (8 * (u & 3))) & 0xFF;
 }
 
