@@ -54,22 +54,26 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
 // rounding up to 2^-6 returns 0x38, as the reference does (quant.rs:120-122);
 // inputs reaching that branch are in [15/1024, 2^-6).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
-    uint32_t bits = __float_as_uint(v);
-    uint32_t sign = (bits >> 24) & 0x80;
-    if (v != v) return sign | 0x7F;
-    float a = __builtin_fabsf(v);
-    if (a >= 448.0f) return sign | 0x7E;
-    if (a < 0.015625f) {
-        int m = (int)__builtin_rintf(a * 512.0f);
-        if (m == 8) return sign | 0x38;
-        return sign | (uint32_t)m;
-    }
-    int e = (int)((bits >> 23) & 0xFF) - 127;
-    float q = a * __builtin_ldexpf(1.0f, 3 - e);
-    int m8 = (int)__builtin_rintf(q);
-    int ef = (m8 == 16) ? e + 8 : e + 7;
-    int mant = (m8 == 16) ? 0 : m8 - 8;
-    return sign | (uint32_t)(ef << 3) | (uint32_t)mant;
+    // branch-free: both the normal-range and the subnormal encoding are
+    // computed and selected (the exponent arithmetic of the unused one may
+    // be garbage); checked on the host against the branching form of this
+    // rule for every float in [-448, 448] and NaN
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t sign = (bits >> 24) & 0x80;
+    const float a = __builtin_fabsf(v);
+    const int e = (int)((bits >> 23) & 0xFF) - 127;
+    // normal range: 3 mantissa bits, rounded to nearest even
+    const float q = fminf(a * __builtin_ldexpf(1.0f, min(3 - e, 126)), 32.0f);
+    const int m8 = (int)__builtin_rintf(q);
+    const bool up = m8 == 16;
+    const uint32_t cn = ((uint32_t)(up ? e + 8 : e + 7) << 3) | (uint32_t)(up ? 0 : m8 - 8);
+    // below 2^-6: multiples of 2^-9 (a result of 2^-6 encodes as 0x38)
+    const int m = (int)__builtin_rintf(fminf(a, 1.0f) * 512.0f);
+    const uint32_t cs = m == 8 ? 0x38u : (uint32_t)m;
+    uint32_t c = a < 0.015625f ? cs : cn;
+    c = a >= 448.0f ? 0x7Eu : c;
+    c = (v != v) ? 0x7Fu : c;
+    return sign | c;
 }
 
 // Rust f32::clamp (NaN passes through).
@@ -197,6 +201,28 @@ __device__ __forceinline__ float half_wave_max(float v) {
     return v;
 }
 
+// log2_ceil(amax / 448) from the bits of amax (amax >= 1e-4, or inf/NaN):
+// with amax = M 2^E, M in [1, 2), the correctly rounded quotient is exactly
+// 2^(E-8) when M == 1.75, just above it when M > 1.75 and in
+// [2^(E-9), 2^(E-8)) when M < 1.75, so the ceiling is E - 8 + (M > 1.75);
+// inf / 448 = inf (128) and NaN / 448 = NaN (129). Checked on the host
+// against the division for every float >= 1e-4.
+__device__ __forceinline__ int log2_ceil_div448(float amax) {
+    const uint32_t b = __float_as_uint(amax);
+    const int ef = (int)((b >> 23) & 0xFF);
+    const uint32_t mant = b & 0x7FFFFF;
+    return ef == 255 ? (mant ? 129 : 128) : ef - 135 + (mant > 0x600000u ? 1 : 0);
+}
+
+// Max over each aligned group of 8 lanes by DPP moves (half-row mirror,
+// then quad swaps 2 and 1): every lane ends with the maximum of its group.
+__device__ __forceinline__ float max8_lanes(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));
+    return v;
+}
+
 // FP8 activation quantisation of one 1x32 block held one value per lane in a
 // 32-lane group (weightstream-ref actquant.rs:21-45 / act_quant_fp8_emit,
 // actquant.cu:47): amax floored at 1e-4, scale 2^log2_ceil(amax/448),
@@ -205,7 +231,7 @@ __device__ __forceinline__ float half_wave_max(float v) {
 __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_byte) {
     float amax = half_wave_max(__builtin_fabsf(x));
     if (amax < 1e-4f) amax = 1e-4f;
-    int e = log2_ceil(amax / 448.0f);
+    int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
     float s = __builtin_ldexpf(1.0f, e);
     return f32_to_e4m3(rclamp(x / s, -448.0f, 448.0f));
@@ -220,10 +246,9 @@ __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_b
 __device__ __forceinline__ uint32_t quant_fp8_block32_x4(float4 v, uint32_t *scale_byte) {
     float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                        fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
-#pragma unroll
-    for (int off = 4; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    amax = max8_lanes(amax);
     if (amax < 1e-4f) amax = 1e-4f;
-    const int e = log2_ceil(amax / 448.0f);
+    const int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
     const float inv = __builtin_ldexpf(1.0f, -e);
     return f32_to_e4m3(rclamp(v.x * inv, -448.0f, 448.0f)) |

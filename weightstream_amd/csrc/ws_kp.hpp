@@ -339,6 +339,23 @@ __device__ __forceinline__ void kp_body(int bx, int by, int bz, const uint8_t *A
         }
     };
 
+    // AF32: the activation is read in rounds of kXR float4 per thread, the
+    // first round before the weight stages: loads return in issue order, so
+    // a wait for activation values issued after the weights would wait for
+    // the weights too (measured at M=1, K=8192: 12.9 against 8.2 us for the
+    // GEMV of pre-quantised bytes; 11.0 us this way)
+    constexpr int kXR = 4;
+    const float4 *X = (const float4 *)A;
+    const int n4 = AF32 ? M * K / 4 : 0;
+    float4 xr[AF32 ? kXR : 1];
+    if (AF32) {
+#pragma unroll
+        for (int j = 0; j < kXR; j++) {
+            const int i = j * kThreads + t;
+            xr[j] = i < n4 ? X[i] : float4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    mem_order();
     KpStage<MF, NF, U> s0, s1;
     load(s0, k0, 0);
     mem_order();
@@ -348,18 +365,24 @@ __device__ __forceinline__ void kp_body(int bx, int by, int bz, const uint8_t *A
         // four values per lane, a 1x32 block per 8 lanes; every lane of a
         // block takes part in its maximum (dead blocks quantise zeros and
         // store nothing; M K % 32 == 0)
-        const float4 *X = (const float4 *)A;
-        const int n4 = M * K / 4;
-        for (int i0 = 0; i0 < n4; i0 += kThreads) {
-            const int i = i0 + t;
-            const bool live = i < n4;
-            uint32_t sbyte;
-            const uint32_t q = quant_fp8_block32_x4(live ? X[i] : float4{0.f, 0.f, 0.f, 0.f},
-                                                    &sbyte);
-            if (live) {
-                const int row = (4 * i) / K, col = 4 * i - row * K;
-                *(uint32_t *)(a_l + row * a_pitch + col) = q;
-                if ((t & 7) == 0) as_l[row * (K / 32) + col / 32] = (uint8_t)sbyte;
+        for (int base = 0; base < n4; base += kXR * kThreads) {
+            if (base > 0) {
+#pragma unroll
+                for (int j = 0; j < kXR; j++) {
+                    const int i = base + j * kThreads + t;
+                    xr[j] = i < n4 ? X[i] : float4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kXR; j++) {
+                const int i = base + j * kThreads + t;
+                uint32_t sbyte;
+                const uint32_t q = quant_fp8_block32_x4(xr[j], &sbyte);
+                if (i < n4) {
+                    const int row = (4 * i) / K, col = 4 * i - row * K;
+                    *(uint32_t *)(a_l + row * a_pitch + col) = q;
+                    if ((t & 7) == 0) as_l[row * (K / 32) + col / 32] = (uint8_t)sbyte;
+                }
             }
         }
         lds_barrier();
