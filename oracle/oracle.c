@@ -660,3 +660,34 @@ void or_dispatch(const int32_t *topk_idx, const float *topk_w, size_t routes, si
     }
     free(fill);
 }
+
+/* Test infrastructure: the reference's byte for the 32-bit pattern u, for
+ * the exhaustive device checks of ws_math_probe: fn 2 the e4m3 encoding of
+ * x (quant.rs:103-137), fn 3 the UE8M0 scale byte of a block whose largest
+ * magnitude is |x| (or_fp8_act_emit's rule: the `a > amax` scan from 0, so
+ * NaN counts as 0; floor 1e-4; log2_ceil(amax / 448) + 127). */
+static uint32_t or_probe_byte(int fn, uint32_t u) {
+    const float x = u2f(u);
+    if (fn == 2) return or_f32_to_e4m3(x);
+    float a = fabsf(x), amax = 0.0f;
+    if (a > amax) amax = a;
+    if (amax < 1e-4f) amax = 1e-4f;
+    return (uint32_t)(uint8_t)(or_log2_ceil(amax / 448.0f) + 127);
+}
+
+/* sum over u in [lo, hi) of (byte(u) ^ (u * 0x9E3779B1)) * (2u + 1) mod 2^64
+ * (the digest the GPU test computes with wrapping int64 arithmetic) */
+uint64_t or_probe_digest(int fn, uint64_t lo, uint64_t hi) {
+    uint64_t acc = 0;
+#pragma omp parallel for reduction(+ : acc) schedule(static, 1 << 16)
+    for (long long u = (long long)lo; u < (long long)hi; u++)
+        acc += (uint64_t)(or_probe_byte(fn, (uint32_t)u) ^ (uint32_t)((uint32_t)u * 0x9E3779B1u)) *
+               (2 * (uint64_t)u + 1);
+    return acc;
+}
+
+/* the bytes for the patterns [lo, lo + n) */
+void or_probe_bytes(int fn, uint32_t lo, uint32_t n, uint32_t *out) {
+#pragma omp parallel for schedule(static, 1 << 16)
+    for (long long i = 0; i < (long long)n; i++) out[i] = or_probe_byte(fn, lo + (uint32_t)i);
+}

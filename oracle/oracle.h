@@ -49,6 +49,9 @@ void or_fp8_act_emit(const float *x, size_t n, uint8_t *q, uint8_t *s);
 /* y[rows] = W[rows,cols](e4m3, 32x32 UE8M0) . x (f32, quantised inside) */
 /* threads for the GEMV row loops (default 1; results are the same for any count) */
 void or_set_threads(int n);
+/* exhaustive device checks (ws_math_probe fn 2, 3): reference bytes and their digest */
+uint64_t or_probe_digest(int fn, uint64_t lo, uint64_t hi);
+void or_probe_bytes(int fn, uint32_t lo, uint32_t n, uint32_t *out);
 void or_fp8_gemv(const uint8_t *w, const uint8_t *s, size_t rows, size_t cols, const float *x, float *y);
 /* y[rows] = W[rows,cols/2](packed e2m1, 1x32 UE8M0) . x */
 void or_fp4_gemv(const uint8_t *w, const uint8_t *s, size_t rows, size_t cols, const float *x, float *y);

@@ -73,6 +73,8 @@ _sigs = {
     "or_dispatch": (None, [_i32p, _f32p, _sz, _sz, _sz, _i32p, _f32p, _i32p, _i32p, _i32p,
                            _i32p, _i32p, _i32p]),
     "or_set_threads": (None, [C.c_int]),
+    "or_probe_digest": (C.c_uint64, [C.c_int, C.c_uint64, C.c_uint64]),
+    "or_probe_bytes": (None, [C.c_int, C.c_uint32, C.c_uint32, C.c_void_p]),
 }
 for _n, (_r, _a) in _sigs.items():
     _f = getattr(lib, _n)

@@ -252,7 +252,7 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
         float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                            fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
         amax = max8_lanes(amax);
-        if (amax < 1e-4f) amax = 1e-4f;
+        if (!(amax >= 1e-4f)) amax = 1e-4f;
         const int e = log2_ceil_div448(amax);
         // x / 2^e == x * 2^-e exactly (2^-e is a normal f32 here)
         const float inv = __builtin_ldexpf(1.0f, -e), sc = __builtin_ldexpf(1.0f, e);

@@ -329,9 +329,11 @@ __global__ __launch_bounds__(256) void score_kernel(float *__restrict__ v, int64
 }
 
 // Device math over the 32-bit patterns lo .. lo+n-1 (exhaustive host/device
-// agreement checks): fn 0 logf, fn 1 the sqrtsoftplus score of score_fn.
-// Each also evaluates the wave-lane variant the top-k kernels use
-// (wave_scores_of) and reports a difference as 0x7fbadbad.
+// agreement checks): fn 0 logf, fn 1 the sqrtsoftplus score of score_fn
+// (each also evaluates the wave-lane variant the top-k kernels use,
+// wave_scores_of, and reports a difference as 0x7fbadbad); fn 2 the e4m3
+// byte of x (f32_to_e4m3), fn 3 the UE8M0 scale byte of the activation
+// quantisation for a block whose largest magnitude is |x|.
 __global__ __launch_bounds__(256) void math_probe_kernel(int fn, uint32_t lo, uint32_t n,
                                                          uint32_t *out) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
@@ -339,6 +341,12 @@ __global__ __launch_bounds__(256) void math_probe_kernel(int fn, uint32_t lo, ui
     uint32_t a, b;
     if (fn == 0) {
         a = b = __float_as_uint(ws_logf(x));
+    } else if (fn == 2) {
+        a = b = f32_to_e4m3(x);
+    } else if (fn == 3) {
+        float amax = __builtin_fabsf(x);
+        if (!(amax >= 1e-4f)) amax = 1e-4f;
+        a = b = (uint32_t)(log2_ceil_div448(amax) + 127) & 0xFF;
     } else {
         a = __float_as_uint(score_fn(x, WS_SCORE_SQRTSOFTPLUS, 1.0f));
         float v[1] = {x}, o[1];
@@ -401,7 +409,7 @@ using namespace ws;
 extern "C" {
 
 int ws_math_probe(int fn, uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream) {
-    if (!out || n == 0 || fn < 0 || fn > 1) return WS_ERR_INVALID_ARG;
+    if (!out || n == 0 || fn < 0 || fn > 3) return WS_ERR_INVALID_ARG;
     hipLaunchKernelGGL(math_probe_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, fn, lo, n,
                        out);
     return launch_status();

@@ -230,7 +230,7 @@ __device__ __forceinline__ float max8_lanes(float v) {
 // UE8M0 byte. fmaxf drops NaN like the reference's `a > amax` scan.
 __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_byte) {
     float amax = half_wave_max(__builtin_fabsf(x));
-    if (amax < 1e-4f) amax = 1e-4f;
+    if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's scan
     int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
     float s = __builtin_ldexpf(1.0f, e);
@@ -247,7 +247,7 @@ __device__ __forceinline__ uint32_t quant_fp8_block32_x4(float4 v, uint32_t *sca
     float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                        fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
     amax = max8_lanes(amax);
-    if (amax < 1e-4f) amax = 1e-4f;
+    if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's scan
     const int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
     const float inv = __builtin_ldexpf(1.0f, -e);
