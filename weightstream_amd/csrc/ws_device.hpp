@@ -298,7 +298,7 @@ __device__ __forceinline__ v8i frag_from4(uint4 lo) {
 
 // ---- exact math: dequantise to bf16, accumulate with bf16 MFMA -----------
 // The FP8/FP4 scaled MFMAs of gfx950 sum their products at reduced internal
-// precision (measured: up to 2^-12 of sum|p| per instruction, against 2^-24
+// precision (measured: about 2^-11 of sum|p| per instruction, against 2^-24
 // for an f32 sum), while v_mfma_f32_16x16x32_bf16 accumulates in f32
 // (measured: 2e-7 of sum|p|). Every e4m3 / e2m1 value times a UE8M0 scale is
 // exactly representable in bf16 (4 and 2 significant bits, f32 exponent
