@@ -56,8 +56,8 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
 __device__ __forceinline__ uint32_t f32_to_e4m3(float v) {
     // branch-free: both the normal-range and the subnormal encoding are
     // computed and selected (the exponent arithmetic of the unused one may
-    // be garbage); checked on the host against the branching form of this
-    // rule for every float in [-448, 448] and NaN
+    // be garbage); equal to the reference rule on all 2^32 inputs (device
+    // digest against the oracle, tests/test_gpu_route.py)
     const uint32_t bits = __float_as_uint(v);
     const uint32_t sign = (bits >> 24) & 0x80;
     const float a = __builtin_fabsf(v);
@@ -205,8 +205,9 @@ __device__ __forceinline__ float half_wave_max(float v) {
 // with amax = M 2^E, M in [1, 2), the correctly rounded quotient is exactly
 // 2^(E-8) when M == 1.75, just above it when M > 1.75 and in
 // [2^(E-9), 2^(E-8)) when M < 1.75, so the ceiling is E - 8 + (M > 1.75);
-// inf / 448 = inf (128) and NaN / 448 = NaN (129). Checked on the host
-// against the division for every float >= 1e-4.
+// inf / 448 = inf (128) and NaN / 448 = NaN (129). Equal to the division
+// form for every input (device digest against the oracle,
+// tests/test_gpu_route.py).
 __device__ __forceinline__ int log2_ceil_div448(float amax) {
     const uint32_t b = __float_as_uint(amax);
     const int ef = (int)((b >> 23) & 0xFF);
