@@ -161,18 +161,27 @@ __device__ __forceinline__ v4f fp4_compute(const Fp4StageU<U> &st, v4f acc, cons
 // other's loads are outstanding. The steady-state loop reloads both stages
 // unconditionally, so its body is straight-line and each wait covers only the
 // stage about to be used; the last two or three stages are the tail.
-template <bool EXACT, int U>
+// `between` runs after each reload (the wave waits on memory there): the
+// decode kernel's routing wave finishes its top-k rounds in those gaps.
+struct NoHook {
+    __device__ __forceinline__ void operator()() const {}
+};
+
+template <bool EXACT, int U, class Hook = NoHook>
 __device__ __forceinline__ v4f fp4_stream(const Fp4Band &b, Fp4StageU<U> &s0, Fp4StageU<U> &s1,
                                           const uint8_t *xq_lds, const uint8_t *xs_lds,
-                                          const __bf16 *x_lds, int kb, int k0, int k1) {
+                                          const __bf16 *x_lds, int kb, int k0, int k1,
+                                          Hook between = Hook{}) {
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     const int nst = (k1 - k0 + U - 1) / U;
     int i = 0, ks0 = k0;
     for (; i + 3 < nst; i += 2, ks0 += 2 * U) {
         acc = fp4_compute<EXACT, U>(s0, acc, xq_lds, xs_lds, x_lds, kb, ks0, k1);
         fp4_load(s0, b, ks0 + 2 * U, k1);
+        between();
         acc = fp4_compute<EXACT, U>(s1, acc, xq_lds, xs_lds, x_lds, kb, ks0 + U, k1);
         fp4_load(s1, b, ks0 + 3 * U, k1);
+        between();
     }
     const int rest = nst - i;
     if (rest == 3) {
@@ -463,30 +472,40 @@ __device__ __forceinline__ void glu_body(
     fp4_load(st1, band, k0 + kUD, k1);
     mem_order();
 
-    // the routing weight and the picks' ranks
-    if constexpr (CPL > 0) {
-        if (w == 0) {
-            for (int k = slot + 1; k < top_k; k++) tk.round(k, lane);
-            const int pk = tk.pick;
-            const float pw = tk.weight(top_k, ra.norm, ra.route_scale);
-            if (lane < top_k) {
-                pk_l[lane] = pk;
-                pw_l[lane] = pw;
-                if (bx == 0 && slot == 0) {
-                    ra.idx_out[lane] = pk;
-                    ra.w_out[lane] = pw;
-                }
-            }
-        }
-    }
-
     if (XF32) tok_quant_f32<EXACT>(tr, tb0, tb1, lane, x_l, xq_l, xs_l);
     else share_store_fp8<EXACT>(tr.b, tc0, tc1, lane, x_l, xq_l, xs_l);
     lds_barrier();
-    if constexpr (CPL > 0) rw = pw_l[slot];
 
     {
-        v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1);
+        // the routing weight needs every pick: wave 0 runs the rounds after
+        // this slot's in the gaps of its weight stream (the other waves do
+        // not wait for them) and the rest after it; the weight is used in the
+        // epilogue only
+        int kn = slot + 1;
+        auto rounds = [&]() {
+            if constexpr (CPL > 0) {
+                if (w == 0 && kn < top_k) {  // uniform
+                    tk.round(kn, lane);
+                    kn++;
+                }
+            }
+        };
+        v4f acc = fp4_stream<EXACT>(band, st0, st1, xq_l, xs_l, x_l, lane >> 4, k0, k1, rounds);
+        if constexpr (CPL > 0) {
+            if (w == 0) {
+                for (; kn < top_k; kn++) tk.round(kn, lane);
+                const int pk = tk.pick;
+                const float pw = tk.weight(top_k, ra.norm, ra.route_scale);
+                if (lane < top_k) {
+                    pk_l[lane] = pk;
+                    pw_l[lane] = pw;
+                    if (bx == 0 && slot == 0) {
+                        ra.idx_out[lane] = pk;
+                        ra.w_out[lane] = pw;
+                    }
+                }
+            }
+        }
         // D[i][j]: i = weight row 4*(lane/16)+v, j = lane%16 (all columns equal)
         if ((lane & 15) == 0) {
 #pragma unroll
@@ -494,6 +513,7 @@ __device__ __forceinline__ void glu_body(
         }
     }
     __syncthreads();
+    if constexpr (CPL > 0) rw = pw_l[slot];
     if (w >= tpw) return;
     // wave w finishes tile bx * tpw + w; lanes 0-31 own its 32 values,
     // lanes 32-63 mirror them so the half-wave reduction stays uniform, and do
