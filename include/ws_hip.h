@@ -70,7 +70,8 @@ int ws_expf_probe(uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);
  * bits(ws_logf(x)), fn 1 bits of the sqrtsoftplus score sqrt(softplus(x))
  * (num.rs:82-88, moe.rs:38-42), fn 2 the e4m3 byte of x (quant.rs:103-137),
  * fn 3 the UE8M0 scale byte of the FP8 activation quantisation of a block
- * whose largest magnitude is |x| (actquant.rs:21-45). Test hook for the
+ * whose largest magnitude is |x| (actquant.rs:21-45), fn 4 the f32 bits of
+ * the value of x's e4m3 byte. Test hook for the
  * exhaustive host/device agreement checks; 0x7fbadbad marks an input where
  * the routing kernels' wave variant disagrees. */
 int ws_math_probe(int fn, uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream);

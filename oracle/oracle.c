@@ -665,10 +665,15 @@ void or_dispatch(const int32_t *topk_idx, const float *topk_w, size_t routes, si
  * the exhaustive device checks of ws_math_probe: fn 2 the e4m3 encoding of
  * x (quant.rs:103-137), fn 3 the UE8M0 scale byte of a block whose largest
  * magnitude is |x| (or_fp8_act_emit's rule: the `a > amax` scan from 0, so
- * NaN counts as 0; floor 1e-4; log2_ceil(amax / 448) + 127). */
+ * NaN counts as 0; floor 1e-4; log2_ceil(amax / 448) + 127), fn 4 the f32
+ * bits of the value of x's e4m3 byte (NaN canonical). */
 static uint32_t or_probe_byte(int fn, uint32_t u) {
     const float x = u2f(u);
     if (fn == 2) return or_f32_to_e4m3(x);
+    if (fn == 4) {  /* the value of the e4m3 byte of x (NaN canonical) */
+        const float d = or_e4m3_to_f32(or_f32_to_e4m3(x));
+        return isnan(d) ? 0x7FC00000u : f2u(d);
+    }
     float a = fabsf(x), amax = 0.0f;
     if (a > amax) amax = a;
     if (amax < 1e-4f) amax = 1e-4f;

@@ -251,28 +251,34 @@ def test_swiglu_bit_exact():
 
 def test_device_e4m3_and_activation_scale_equal_oracle_on_every_input():
     """All 2^32 inputs: the digests of the device e4m3 encoder (f32_to_e4m3,
-    branch-free) and of the activation quantisation's scale byte for a block
-    maximum |x| (the exponent taken from the bits of amax, no division) equal
-    the oracle's (quant.rs:103-137, actquant.rs:21-45); 2^24 inputs around
-    the subnormal / normal boundary are also compared value by value."""
+    branch-free), of the activation quantisation's scale byte for a block
+    maximum |x| (the exponent taken from the bits of amax, no division) and of
+    the e4m3 rounding without the byte (e4m3_round_value) equal the oracle's
+    (quant.rs:103-137, actquant.rs:21-45); 2^24 inputs around the subnormal /
+    normal boundary are also compared value by value."""
     lib = L._lib.load()
     chunk = 1 << 28
     out = torch.empty(chunk, dtype=torch.int32, device=DEV)
     stream = torch.cuda.current_stream().cuda_stream
-    for fn in (2, 3):
+    for fn in (2, 3, 4):
         total = 0
         for c in range(16):
             lo = c * chunk
             announce("quant probe fn %d chunk %d" % (fn, c))
             L._lib.check("ws_math_probe", lib.ws_math_probe(fn, lo, chunk, out.data_ptr(), stream))
             r = out.to(torch.int64) & 0xFFFFFFFF
+            if fn == 4:  # canonical NaN, as the oracle's bytes
+                nan = ((r & 0x7F800000) == 0x7F800000) & ((r & 0x7FFFFF) != 0)
+                r = torch.where(nan, torch.full_like(r, 0x7FC00000), r)
             u = torch.arange(lo, lo + chunk, dtype=torch.int64, device=DEV)
             mixed = (r ^ ((u * 0x9E3779B1) & 0xFFFFFFFF)) * (2 * u + 1)
             total = (total + int(mixed.sum().item())) & ((1 << 64) - 1)
         assert total == O.lib.or_probe_digest(fn, 0, 1 << 32), fn
         lo, n = 0x3C000000, 1 << 24
         L._lib.check("ws_math_probe", lib.ws_math_probe(fn, lo, n, out.data_ptr(), stream))
-        got = host(out[:n]).view(np.uint32)
+        got = host(out[:n]).view(np.uint32).copy()
+        if fn == 4:
+            got[((got & 0x7F800000) == 0x7F800000) & ((got & 0x7FFFFF) != 0)] = 0x7FC00000
         ref = np.empty(n, np.uint32)
         O.lib.or_probe_bytes(fn, lo, n, ref.ctypes.data)
         assert np.array_equal(got, ref), fn

@@ -266,19 +266,22 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
         // x / 2^e == x * 2^-e exactly (2^-e is a normal f32 here)
         const float inv = __builtin_ldexpf(1.0f, -e), sc = __builtin_ldexpf(1.0f, e);
         const float f[4] = {v.x, v.y, v.z, v.w};
-        uint32_t q[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] * inv, -448.0f, 448.0f));
-        if (blk >= b1) continue;
         const int i = blk * 32 + (lane & 7) * 4;
         if (EXACT) {
-            // exact: every value has at most 4 significant bits
-            const float d[4] = {e4m3_to_f32(q[0]) * sc, e4m3_to_f32(q[1]) * sc,
-                                e4m3_to_f32(q[2]) * sc, e4m3_to_f32(q[3]) * sc};
+            // the dequantised values (e4m3 value x 2^e), each with at most 4
+            // significant bits, so exact in bf16
+            float d[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) d[c] = e4m3_round_value(rclamp(f[c] * inv, -448.0f, 448.0f)) * sc;
+            if (blk >= b1) continue;
             *(uint2 *)(x_l + i) =
                 uint2{(__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xFFFF0000u),
                       (__float_as_uint(d[2]) >> 16) | (__float_as_uint(d[3]) & 0xFFFF0000u)};
         } else {
+            uint32_t q[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] * inv, -448.0f, 448.0f));
+            if (blk >= b1) continue;
             *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
             if ((lane & 7) == 0) xs_l[blk] = (uint8_t)(e + 127);
         }

@@ -333,7 +333,8 @@ __global__ __launch_bounds__(256) void score_kernel(float *__restrict__ v, int64
 // (each also evaluates the wave-lane variant the top-k kernels use,
 // wave_scores_of, and reports a difference as 0x7fbadbad); fn 2 the e4m3
 // byte of x (f32_to_e4m3), fn 3 the UE8M0 scale byte of the activation
-// quantisation for a block whose largest magnitude is |x|.
+// quantisation for a block whose largest magnitude is |x|, fn 4 x rounded
+// to the e4m3 grid (e4m3_round_value: the value of the e4m3 byte of x).
 __global__ __launch_bounds__(256) void math_probe_kernel(int fn, uint32_t lo, uint32_t n,
                                                          uint32_t *out) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
@@ -343,6 +344,8 @@ __global__ __launch_bounds__(256) void math_probe_kernel(int fn, uint32_t lo, ui
         a = b = __float_as_uint(ws_logf(x));
     } else if (fn == 2) {
         a = b = f32_to_e4m3(x);
+    } else if (fn == 4) {
+        a = b = __float_as_uint(e4m3_round_value(x));
     } else if (fn == 3) {
         float amax = __builtin_fabsf(x);
         if (!(amax >= 1e-4f)) amax = 1e-4f;
@@ -409,7 +412,7 @@ using namespace ws;
 extern "C" {
 
 int ws_math_probe(int fn, uint32_t lo, uint32_t n, uint32_t *out, ws_stream_t stream) {
-    if (!out || n == 0 || fn < 0 || fn > 3) return WS_ERR_INVALID_ARG;
+    if (!out || n == 0 || fn < 0 || fn > 4) return WS_ERR_INVALID_ARG;
     hipLaunchKernelGGL(math_probe_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, fn, lo, n,
                        out);
     return launch_status();

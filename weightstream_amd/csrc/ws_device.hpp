@@ -201,6 +201,26 @@ __device__ __forceinline__ float half_wave_max(float v) {
     return v;
 }
 
+// e4m3_to_f32(f32_to_e4m3(v)) without the byte: v rounded to the e4m3 grid
+// (3 mantissa bits, RNE; multiples of 2^-9 below 2^-6, where a value rounding
+// up to 2^-6 gives 1.0 as the encoder's 0x38 decodes; 448 at and above 448;
+// NaN -> the decoder's NaN). Equal to the composition on all 2^32 inputs
+// (device digest against the oracle, tests/test_gpu_route.py).
+__device__ __forceinline__ float e4m3_round_value(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t sign = bits & 0x80000000u;
+    const float a = __builtin_fabsf(v);
+    const int e = (int)((bits >> 23) & 0xFF) - 127;
+    const float m8 = __builtin_rintf(fminf(a * __builtin_ldexpf(1.0f, min(3 - e, 126)), 32.0f));
+    const float vn = __builtin_ldexpf(m8, max(e - 3, -126));  // m8 2^(e-3), exact
+    const float ms = __builtin_rintf(fminf(a, 1.0f) * 512.0f);
+    const float vs = ms == 8.0f ? 1.0f : ms * 0.001953125f;  // m 2^-9, exact
+    float r = a < 0.015625f ? vs : vn;
+    r = a >= 448.0f ? 448.0f : r;
+    const float sr = __uint_as_float(__float_as_uint(r) | sign);
+    return (v != v) ? __builtin_nanf("") : sr;
+}
+
 // log2_ceil(amax / 448) from the bits of amax (amax >= 1e-4, or inf/NaN):
 // with amax = M 2^E, M in [1, 2), the correctly rounded quotient is exactly
 // 2^(E-8) when M == 1.75, just above it when M > 1.75 and in
