@@ -119,9 +119,10 @@ __device__ __forceinline__ void wave_scores(const float *lg, int n_experts, int 
 // normalised by the top-k-order sum + 1e-20 (norm 1: moe.rs:61, only when
 // top_k > 1; norm 2: moe_select's unconditional normalisation, moe.cu:84-88),
 // times route_scale. Each lane keeps CPL 64-bit keys (score+bias key, then
-// the complemented index); a round is a lane-local max, a 32-bit DPP wave max
-// of the score halves and a ballot; only an exact score tie across lanes
-// takes the 64-bit wave max.
+// the complemented index), sorted once in descending order, so a lane's
+// largest remaining key is its first; a round is a 32-bit DPP wave max of
+// the lanes' first score halves and a ballot (only an exact score tie across
+// lanes takes the 64-bit wave max), and the winning lane shifts its keys.
 // bv[c]: the bias of expert lane + 64 c.
 template <int CPL>
 struct WaveTopk {
@@ -140,27 +141,29 @@ struct WaveTopk {
                           : 0ull;
             sc[c] = s[c];
         }
+        // odd-even transposition sort, descending (keys are distinct)
+#pragma unroll
+        for (int p = 0; p < CPL; p++)
+#pragma unroll
+            for (int c = p & 1; c + 1 < CPL; c += 2) {
+                const bool sw = cand[c + 1] > cand[c];
+                const uint64_t a = cand[c], b = cand[c + 1];
+                const float x = sc[c], y = sc[c + 1];
+                cand[c] = sw ? b : a;
+                cand[c + 1] = sw ? a : b;
+                sc[c] = sw ? y : x;
+                sc[c + 1] = sw ? x : y;
+            }
         pick = 0;
         ws = 0.0f;
     }
 
     // round k: the largest remaining key; returns its expert id (uniform)
     __device__ __forceinline__ int round(int k, int lane) {
-        // the lane's largest key and its score (keys are distinct: the low
-        // half is the complemented expert id), no indexing by position
-        // (the asm keeps each score a register value: a select between
-        // array elements would otherwise become an indexed load of a
-        // private-memory copy of the array)
-        uint64_t best = cand[0];
-        float sb = sc[0];
-#pragma unroll
-        for (int c = 1; c < CPL; c++) {
-            float v = sc[c];
-            __asm__("" : "+v"(v));
-            const bool gt = cand[c] > best;
-            best = gt ? cand[c] : best;
-            sb = gt ? v : sb;
-        }
+        // the lane's largest remaining key is its first (keys are distinct:
+        // the low half is the complemented expert id)
+        const uint64_t best = cand[0];
+        const float sb = sc[0];
         const uint32_t hk = (uint32_t)(best >> 32);
         const uint32_t wk = wave_max_u32(hk);
         uint64_t bal = __ballot(hk == wk);
@@ -176,8 +179,16 @@ struct WaveTopk {
             pick = e;
             ws = w;
         }
+        // the winning lane drops its first key (constant indices only: a
+        // select between array elements by a run-time index would become an
+        // indexed load of a private-memory copy of the array)
+        const bool drop = lane == win;
 #pragma unroll
-        for (int c = 0; c < CPL; c++) cand[c] = (lane == win && cand[c] == best) ? 0ull : cand[c];
+        for (int c = 0; c + 1 < CPL; c++) {
+            cand[c] = drop ? cand[c + 1] : cand[c];
+            sc[c] = drop ? sc[c + 1] : sc[c];
+        }
+        cand[CPL - 1] = drop ? 0ull : cand[CPL - 1];
         return e;
     }
 
