@@ -85,19 +85,6 @@ struct RankedPicks {
     int nv;
 };
 
-// from the top-k output: rank by (expert id, slot) among picks in [0, E)
-__device__ __forceinline__ RankedPicks ranked_from_topk(const int32_t *idx, int top_k,
-                                                        int n_experts, int lane) {
-    const WavePicks wp = wave_picks(idx, top_k, n_experts, lane);
-    RankedPicks rp{0, 0, wp.nv};
-    for (int i = 0; i < top_k; i++) {
-        if (__builtin_amdgcn_readlane(wp.rank, i) == lane) {
-            rp.slot = i;
-            rp.e = __builtin_amdgcn_readlane(wp.e, i);
-        }
-    }
-    return rp;
-}
 
 // from moe_local_slots' lists (moe_grouped.cu:23-58: slots already in
 // ascending expert id): slot local[r], slab row gate_idx[slot] - e_start.
@@ -318,14 +305,27 @@ __device__ __forceinline__ void share_load_ranked(Fp8Share<R> &tr, const uint8_t
     }
 }
 
-// ... into LDS: exact bf16 values (EXACT) or the bytes and scales as they are
+// ... into LDS: exact bf16 values (EXACT) or the bytes and scales as they are.
+// With slot_rank (lane s: the rank of row s, -1 to drop it) the source is the
+// rows in slot order, each stored at its rank's row.
 template <bool EXACT, int R>
 __device__ __forceinline__ void share_store_fp8(const Fp8Share<R> &tr, int c0, int c1, int lane,
-                                                __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l) {
+                                                __bf16 *x_l, uint8_t *xq_l, uint8_t *xs_l,
+                                                int inter = 0, int slot_rank = 0,
+                                                bool remap = false) {
 #pragma unroll
     for (int j = 0; j < R; j++) {
-        const int i = c0 + j * 1024 + lane * 16;
-        if (i >= c1) continue;
+        const int src = c0 + j * 1024 + lane * 16;
+        int i = src;
+        bool keep = src < c1;
+        if (remap) {
+            // every lane takes part in the shuffle
+            const int sr = min(src, c1 - 1) / inter;
+            const int rk = __shfl(slot_rank, min(sr, 63), 64);
+            keep = keep && rk >= 0;
+            i = rk * inter + (src - sr * inter);
+        }
+        if (!keep) continue;
         if (EXACT) {
             const float f = e8m0_to_f32(tr.s[j]);
             const uint32_t wd[4] = {tr.q[j].x, tr.q[j].y, tr.q[j].z, tr.q[j].w};
@@ -604,17 +604,37 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     __shared__ float part[kMaxTopkDec][kRedWaves][16];
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int row0 = blockIdx.x * 16;
+    // the picks' hidden states: every wave converts 1/8 of them into LDS, in
+    // rank order (ascending expert id). From the top-k output the rows are
+    // loaded in slot order before the picks are ranked (no dependence on the
+    // ranking) and stored at their ranks' rows; from local-slot lists, in
+    // rank order after it.
+    const bool by_slot = pk.local == nullptr;
+    Fp8Share<kRedShareRounds> hr;
+    const int tot_s = top_k * inter;
+    const int c0s = w * (tot_s / kRedWaves), c1s = c0s + tot_s / kRedWaves;
+    if (by_slot) share_load_fp8(hr, hq, hs, c0s, c1s, lane);
+    mem_order();
     // every wave ranks the (<= 16) picks itself: no barrier before the loads
-    const RankedPicks rp = pk.local ? ranked_from_local(pk.local, pk.local_count, pk.idx,
-                                                        pk.e_start, n_experts, top_k, lane)
-                                    : ranked_from_topk(pk.idx, top_k, n_experts, lane);
+    WavePicks wp{};
+    RankedPicks rp;
+    if (by_slot) {
+        wp = wave_picks(pk.idx, top_k, n_experts, lane);
+        rp = RankedPicks{0, 0, wp.nv};
+        for (int i = 0; i < top_k; i++) {
+            if (__builtin_amdgcn_readlane(wp.rank, i) == lane) {
+                rp.slot = i;
+                rp.e = __builtin_amdgcn_readlane(wp.e, i);
+            }
+        }
+    } else {
+        rp = ranked_from_local(pk.local, pk.local_count, pk.idx, pk.e_start, n_experts, top_k,
+                               lane);
+    }
     const int nv = rp.nv;
-    // the picks' hidden states (nv rows of inter e4m3 bytes, ascending expert
-    // id): every wave converts 1/8 of them into LDS; their loads go first
     const int tot = nv * inter;
     const int c0 = w * (tot / kRedWaves), c1 = c0 + tot / kRedWaves;
-    Fp8Share<kRedShareRounds> hr;
-    share_load_ranked(hr, hq, hs, rp, inter, c0, c1, lane);
+    if (!by_slot) share_load_ranked(hr, hq, hs, rp, inter, c0, c1, lane);
     mem_order();
 
     // work units (pick, K part): a wave streams 16 rows of one expert's w2
@@ -645,7 +665,10 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     __bf16 *h_l = (__bf16 *)lds;
     uint8_t *hq_l = lds;
     uint8_t *hs_l = lds + (size_t)top_k * inter;
-    share_store_fp8<EXACT>(hr, c0, c1, lane, h_l, hq_l, hs_l);
+    if (by_slot)
+        share_store_fp8<EXACT>(hr, c0s, c1s, lane, h_l, hq_l, hs_l, inter, wp.rank, true);
+    else
+        share_store_fp8<EXACT>(hr, c0, c1, lane, h_l, hq_l, hs_l);
     lds_barrier();
 
     if (has) {
