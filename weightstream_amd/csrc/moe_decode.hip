@@ -71,11 +71,6 @@ __device__ __forceinline__ WavePicks wave_picks_of(int e_lane, int top_k, int n_
     return wp;
 }
 
-__device__ __forceinline__ WavePicks wave_picks(const int32_t *idx, int top_k, int n_experts,
-                                                int lane) {
-    return wave_picks_of(lane < top_k ? idx[lane] : -1, top_k, n_experts, lane);
-}
-
 // The valid picks in summation order (ascending expert id, then slot), as
 // the down kernel walks them: lane r < nv holds the gate-output slot of the
 // pick of rank r (its row of hq / hs) and its expert's row in the slab.
@@ -610,16 +605,23 @@ __global__ __launch_bounds__(kRedThreads) void expert_reduce_kernel(
     // ranking) and stored at their ranks' rows; from local-slot lists, in
     // rank order after it.
     const bool by_slot = pk.local == nullptr;
+    // the picks first: loads return in issue order, so the ranking then
+    // waits for them only. Both loads go out unconditionally (the idx
+    // clamped into its top_k entries, hq's top_k rows exist either way), so
+    // that the ranking's wait counts the younger hq loads out.
+    const int e_ld = pk.idx[min(lane, top_k - 1)];
+    mem_order();
     Fp8Share<kRedShareRounds> hr;
     const int tot_s = top_k * inter;
     const int c0s = w * (tot_s / kRedWaves), c1s = c0s + tot_s / kRedWaves;
-    if (by_slot) share_load_fp8(hr, hq, hs, c0s, c1s, lane);
+    share_load_fp8(hr, hq, hs, c0s, c1s, lane);
     mem_order();
+    const int e_lane = (by_slot && lane < top_k) ? e_ld : -1;
     // every wave ranks the (<= 16) picks itself: no barrier before the loads
     WavePicks wp{};
     RankedPicks rp;
     if (by_slot) {
-        wp = wave_picks(pk.idx, top_k, n_experts, lane);
+        wp = wave_picks_of(e_lane, top_k, n_experts, lane);
         rp = RankedPicks{0, 0, wp.nv};
         for (int i = 0; i < top_k; i++) {
             if (__builtin_amdgcn_readlane(wp.rank, i) == lane) {
