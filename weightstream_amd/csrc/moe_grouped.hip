@@ -579,11 +579,13 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
                     uv = rclamp(uv, -limit, limit);
                     gv = fminf(gv, limit);
                 }
-                // every lane evaluates silu (the lane-table exp permutes across the wave)
-                const float sg = ws_silu_lanes(gv, tab);
-                const float h = pad ? 0.0f : sg * uv * rw_l[srow];
-                uint32_t sbyte;
-                const uint32_t qb = quant_fp8_block32(h, &sbyte);
+                // a padding row (uniform over the half-wave) is a block of
+                // zeros: no silu, the zero block's bytes
+                uint32_t sbyte = zero_block_scale_byte(), qb = 0;
+                if (!pad) {
+                    const float h = ws_silu_lanes(gv, tab) * uv * rw_l[srow];
+                    qb = quant_fp8_block32(h, &sbyte);
+                }
                 hq[(size_t)slot * inter + nt * UC + cbk * 32 + col] = (uint8_t)qb;
                 if (col == 0) hs[(size_t)slot * (inter / 32) + nt * CB + cbk] = (uint8_t)sbyte;
             }

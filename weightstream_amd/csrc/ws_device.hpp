@@ -165,8 +165,8 @@ __device__ __forceinline__ void lds_barrier() {
 
 // ws_expf with the 32-entry table held in lane registers: lane l holds
 // ws_exp2f_tab[l % 32] (ws_lane_exp2f_tab) and the entry is fetched with a
-// lane permute instead of a memory load. Same arithmetic as ws_expf. Every
-// lane of the wave must take part.
+// lane permute instead of a memory load, from the lane's own half-wave. Same
+// arithmetic as ws_expf. Every lane of the half-wave must take part.
 __device__ __forceinline__ uint64_t ws_lane_exp2f_tab(int lane) { return ws_exp2f_tab[lane & 31]; }
 
 __device__ __forceinline__ float ws_expf_lanes(float x, uint64_t tab) {
@@ -174,7 +174,7 @@ __device__ __forceinline__ float ws_expf_lanes(float x, uint64_t tab) {
     double r = 0.0;
     float out = 0.0f;
     const int special = ws_expf_reduce(x, &ki, &r, &out);
-    const int j = (int)(ki & 31);
+    const int j = (int)(__lane_id() & 32) | (int)(ki & 31);
     const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)tab, j, 64);
     const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(tab >> 32), j, 64);
     const float v = ws_expf_finish(ki, r, ((uint64_t)hi << 32) | lo);
@@ -254,8 +254,13 @@ __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_b
     if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's scan
     int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
-    float s = __builtin_ldexpf(1.0f, e);
-    return f32_to_e4m3(rclamp(x / s, -448.0f, 448.0f));
+    // x / 2^e as x * 2^-e (exact scaling either way, as below)
+    return f32_to_e4m3(rclamp(x * __builtin_ldexpf(1.0f, -e), -448.0f, 448.0f));
+}
+
+// The scale byte quant_fp8_block32 gives a block of zeros (the 1e-4 floor)
+__device__ __forceinline__ uint32_t zero_block_scale_byte() {
+    return (uint32_t)(log2_ceil_div448(1e-4f) + 127) & 0xFF;
 }
 
 // The same block quantisation with four consecutive values per lane, a block
