@@ -91,6 +91,51 @@ def test_moe_decode_matches_oracle(E, dim, inter, k):
     assert_close(host(y), want, MOE_TOL, "moe_decode E=%d" % E)
 
 
+def _fp4_normal_slab(gen, E, rows, cols, chunk=64):
+    """E expert matrices [rows, cols] drawn N(0, 0.02) and encoded e2m1 +
+    UE8M0 per 1x32 on the device (the BASELINE weight recipe)."""
+    q = torch.empty((E * rows, cols // 2), dtype=torch.uint8, device=DEV)
+    s = torch.empty((E * rows, cols // 32), dtype=torch.uint8, device=DEV)
+    for e0 in range(0, E, chunk):
+        n = min(chunk, E - e0) * rows
+        w = torch.empty((n, cols), dtype=torch.float32, device=DEV).normal_(0.0, 0.02,
+                                                                           generator=gen)
+        L.weight_quant_fp4(w, q[e0 * rows:e0 * rows + n], s[e0 * rows:e0 * rows + n], n, cols)
+        del w
+    return q, s
+
+
+def test_config3_baseline_weights_route_matches_oracle():
+    """BASELINE config 3 as the bench runs it: 384 experts of N(0, 0.02)
+    weights in e2m1 + UE8M0, dim 4096, inter 2048, top-8 sigmoid routing of
+    N(0, 1) logits + N(0, 0.1) bias, one ws_moe_decode_route call per token,
+    against the oracle's routing and routed sum (several tokens)."""
+    E, dim, inter, k = 384, 4096, 2048, 8
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(3003)
+    rng = np.random.default_rng(3003)
+    announce("config 3: %d experts of N(0, 0.02) weights, route + decode" % E)
+    slabs = _fp4_normal_slab(gen, E, inter, dim) + _fp4_normal_slab(gen, E, inter, dim) + \
+        _fp4_normal_slab(gen, E, dim, inter)
+    packed = _packed(slabs, E, dim, inter)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    ws = torch.empty(L.moe_decode_workspace_size(dim, inter, k), dtype=torch.uint8, device=DEV)
+    for tok in range(4):
+        logits = rng.standard_normal(E).astype(np.float32)
+        x = rng.standard_normal(dim).astype(np.float32)
+        idx = torch.full((k,), -5, dtype=torch.int32, device=DEV)
+        w = torch.zeros(k, dtype=torch.float32, device=DEV)
+        y = torch.empty(dim, dtype=torch.float32, device=DEV)
+        L.moe_decode_route(dev(logits), dev(bias), O.SCORE_SIGMOID, 1.0, 1, 1.0, dev(x), *packed,
+                           y, idx, w, dim, inter, E, k, ws)
+        hi, hw = host(idx), host(w)
+        ri, rw = O.route(O.score(logits, O.SCORE_SIGMOID), bias, k)
+        assert np.array_equal(hi, ri) and np.array_equal(hw.view(np.uint32), rw.view(np.uint32))
+        H = _host_experts(slabs, hi, E, dim, inter)
+        want = O.moe_routed(*H, dim, inter, x, hi, hw)
+        assert_close(host(y), want, MOE_TOL, "config 3 token %d" % tok)
+
+
 def test_moe_decode_split_entry_points_and_order():
     """expert_glu_quant writes pick p's hidden state to row p (its gate
     slot); moe_local_slots orders the picks by ascending expert id and
