@@ -146,6 +146,58 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
         _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
 
 
+def _fp4_normal_slab(gen, E, rows, cols, chunk=64):
+    """E expert matrices [rows, cols] drawn N(0, 0.02) and encoded e2m1 +
+    UE8M0 per 1x32 on the device (the BASELINE weight recipe)."""
+    q = torch.empty((E * rows, cols // 2), dtype=torch.uint8, device=DEV)
+    s = torch.empty((E * rows, cols // 32), dtype=torch.uint8, device=DEV)
+    for e0 in range(0, E, chunk):
+        n = min(chunk, E - e0) * rows
+        wt = torch.empty((n, cols), dtype=torch.float32, device=DEV).normal_(0.0, 0.02,
+                                                                            generator=gen)
+        L.weight_quant_fp4(wt, q[e0 * rows:e0 * rows + n], s[e0 * rows:e0 * rows + n], n, cols)
+        del wt
+    return q, s
+
+
+@pytest.mark.parametrize("zipf", [1.1, 0.275])
+def test_config4_baseline_weights_prefill_matches_oracle(zipf):
+    """BASELINE config 4 as the bench runs it: M = 132 tokens, 384 experts of
+    N(0, 0.02) weights in e2m1 + UE8M0, dim 4096, inter 2048, top-8 sigmoid
+    routing of N(0, 1) logits skewed by Zipf(1.1) popularity (and the bench's
+    quarter-strength draw, 0.25 log Zipf(1.1) = log Zipf(0.275)), against the
+    oracle on sampled rows."""
+    m, E, dim, inter, k = 132, 384, 4096, 2048, 8
+    rng = np.random.default_rng(4004)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(4004)
+    announce("config 4: m=%d, %d experts of N(0, 0.02) weights, Zipf s=%.2f" % (m, E, zipf))
+    slabs = _fp4_normal_slab(gen, E, inter, dim) + _fp4_normal_slab(gen, E, inter, dim) + \
+        _fp4_normal_slab(gen, E, dim, inter)
+    logits, bias = zipf_routing(rng, m, E, k, s=zipf)
+    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), None, idx, w, m, E, k, O.SCORE_SIGMOID, 1.0, True, 1.0)
+    x = rng.standard_normal((m, dim)).astype(np.float32)
+    ws = torch.empty(L.moe_prefill_workspace_size(m, dim, inter, k, E), dtype=torch.uint8,
+                     device=DEV)
+    y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
+    P = _packed(slabs, E, dim, inter)
+    L.moe_prefill(dev(x), idx, w, *P, y, m, dim, inter, E, k, ws)
+    gi, gw, gy = host(idx), host(w), host(y)
+    rows = np.linspace(0, m - 1, 6).astype(int)
+    H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
+    staged = None
+    for r in rows:
+        want = O.moe_routed(*H, dim, inter, x[r], gi[r], gw[r])
+        if rel_err_stats(gy[r], want)[0] <= MOE_TOL:
+            assert_close(gy[r], want, MOE_TOL, "config 4 row %d" % r)
+            continue
+        if staged is None:
+            staged = _staged_hidden(x, idx, w, P, m, E, dim, inter, k)
+        _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
+
+
 def _staged_hidden(x, idx, w, P, m, E, dim, inter, k):
     """The GPU's re-quantised h per slot (emit8 + dispatch + grouped gate/up),
     decoded to f32, and route -> slot."""
