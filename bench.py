@@ -45,7 +45,7 @@ EXPERT_BYTES = 3 * (FP4_MAT + FP4_SC)
 # commands; counters cannot be read from inside this process).
 # The gate/up kernel as the decode step runs it (routing fused in:
 # expert_glu_quant_kernel<true, true, 6>).
-GLU_TRAFFIC_BYTES = 71792550
+GLU_TRAFFIC_BYTES = 71791526
 
 
 def log(*a):
