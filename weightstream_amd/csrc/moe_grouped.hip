@@ -741,6 +741,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
 }
 
 // ---- combine: y[row] = sum of its routes' outputs in ascending slot order --
+// V columns per thread (V = 4: 16-byte loads, dim % 4 == 0)
+template <int V>
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ down,
                                                       const int32_t *__restrict__ route_pos,
                                                       float *__restrict__ y, int dim, int top_k,
@@ -764,11 +766,23 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
         if (j == 0) ns = n;
     }
     __syncthreads();
-    const int d = blockIdx.x * 256 + threadIdx.x;
+    const int d = (blockIdx.x * 256 + threadIdx.x) * V;
     if (d >= dim) return;
-    float acc = 0.0f;
-    for (int i = 0; i < ns; i++) acc = acc + down[(size_t)slots[i] * dim + d];
-    y[(size_t)row * dim + d] = acc;
+    if constexpr (V == 4) {
+        float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int i = 0; i < ns; i++) {
+            const float4 v = *(const float4 *)(down + (size_t)slots[i] * dim + d);
+            acc.x = acc.x + v.x;
+            acc.y = acc.y + v.y;
+            acc.z = acc.z + v.z;
+            acc.w = acc.w + v.w;
+        }
+        *(float4 *)(y + (size_t)row * dim + d) = acc;
+    } else {
+        float acc = 0.0f;
+        for (int i = 0; i < ns; i++) acc = acc + down[(size_t)slots[i] * dim + d];
+        y[(size_t)row * dim + d] = acc;
+    }
 }
 
 // moe_swiglu_route (moe_grouped.cu:239-256): out = silu(min(g,10)) *
@@ -1003,9 +1017,14 @@ int ws_moe_combine_f32(const float *y, const int32_t *route_pos, float *out, int
     if (!y || !route_pos || !out) return WS_ERR_INVALID_ARG;
     if (rows <= 0 || dim <= 0 || top_k <= 0 || tiles <= 0) return WS_ERR_INVALID_ARG;
     if (top_k > 16 || rows > 65535) return WS_ERR_SHAPE;
-    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((dim + 255) / 256), (unsigned)rows),
-                       dim3(256), 0, stream, y, route_pos, out, (int)dim, (int)top_k,
-                       (int)(tiles * kTile));
+    if (dim % 4 == 0 && al16(y) && al16(out))
+        hipLaunchKernelGGL(combine_kernel<4>,
+                           dim3((unsigned)((dim / 4 + 255) / 256), (unsigned)rows), dim3(256), 0,
+                           stream, y, route_pos, out, (int)dim, (int)top_k, (int)(tiles * kTile));
+    else
+        hipLaunchKernelGGL(combine_kernel<1>, dim3((unsigned)((dim + 255) / 256), (unsigned)rows),
+                           dim3(256), 0, stream, y, route_pos, out, (int)dim, (int)top_k,
+                           (int)(tiles * kTile));
     return launch_status();
 }
 
