@@ -695,8 +695,12 @@ def main():
     prefill["native_math"] = {k: v for k, v in bench_prefill(L, torch, dev, packed, 10).items()
                               if k in ("avg_us", "GB/s", "TFLOP/s")}
     L.set_math_mode(L.MATH_EXACT)
+    prefill["draw"] = ("BASELINE config 4 as stated: logits + log Zipf(1.1) popularity, 'many "
+                       "0-3, a few >20' tokens per expert (count_hist_batch0)")
     log("prefill: %s" % prefill)
     prefill_mild = bench_prefill(L, torch, dev, packed, 4, zipf_scale=0.25)
+    prefill_mild["draw"] = ("logits + 0.25 log Zipf(1.1): most touched experts get 1-3 tokens, "
+                            "the 250-330 touched experts of real routing of 132 tokens")
     log("prefill (Zipf at 1/4 strength): %s" % prefill_mild)
     block = bench_block(L, torch, dev, packed, gen) if not args.no_block else None
     gemm = gemv = shapes = None
