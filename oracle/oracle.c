@@ -19,7 +19,12 @@
  *    f64 brute-force dot bounded by the f32 summation error bound.
  *  - f32-scale generalisation: f64 brute force of the dequantised product
  *    within the f32 summation bound; reduces to the UE8M0 path when all
- *    scales are powers of two (checked bit-exact).
+ *    scales are powers of two (checked bit-exact). The quantisers are
+ *    checked block by block against a numpy recomputation of the amax over
+ *    the block (ragged last row block included), the scale fl32(amax/448)
+ *    bit for bit and torch's e4m3 cast of the f32 quotient; a UE8M0-rounded
+ *    scale, a reciprocal multiply, a missing floor and a last-row amax are
+ *    each shown to fail that check (tests/test_oracle_f32s.py).
  *  - num: expf against the exhaustive glibc check of ws_expf, sigmoid /
  *    softplus closed forms at special points.
  *  - routing: a brute-force O(E^2) rank-count selection with the explicit
