@@ -713,6 +713,21 @@ def main():
         import multiprocessing
         cpu_gemm = cpu_baseline_gemm(L, torch, dev, max(1, min(16, multiprocessing.cpu_count())))
 
+    # the verbose per-kernel records go to stderr; the JSON line on stdout
+    # stays short so that every config's figure survives a tail capture
+    detail = {"kernels": res["kernels"],
+              "native_math": {"value": native["gbs"], "ms_per_step": native["ms_per_step"],
+                              "kernels": native["kernels"],
+                              "note": "FP4xFP8 scaled MFMA; ~13-bit internal accumulation"},
+              "fp8_gemv_m1": gemv, "fp8_gemm_m128": gemm, "cpu_baseline_gemm": cpu_gemm,
+              "fp8_gemm_model_shapes": shapes, "moe_prefill_m132": prefill,
+              "moe_prefill_m132_zipf_quarter": prefill_mild, "moe_block_4_layers": block}
+    log("detail: " + json.dumps(detail))
+    if cpu is not None:
+        cpu = {k: v for k, v in cpu.items() if k != "cpu_model"}
+        cpu["single_thread"] = {k: round(v, 3) if isinstance(v, float) else v
+                                for k, v in cpu["single_thread"].items() if k != "note"}
+
     line = {
         "metric": "MoE FP4 decode HBM GB/s (% of peak); FP8 block GEMM TFLOP/s at M=128",
         "value": res["gbs"],
@@ -728,25 +743,58 @@ def main():
         "data": "synthetic: N(0,0.02) weights encoded e2m1+UE8M0 1x32, N(0,1) tokens, "
                 "N(0,1) logits + N(0,0.1) bias, seed 0",
         "config": {"workload": "fp4_moe_decode_m1", "experts": E, "top_k": TOPK, "hidden": DIM,
-                   "inter": INTER, "score": "sigmoid", "swiglu_limit": 10.0,
-                   "bytes_per_step": res["step_bytes"], "frac_hbm_peak":
-                   res["gbs"] / PEAK_HBM_GBS, "tokens_per_s": 1e3 / res["ms_per_step"]},
-        "roofline": roof,
+                   "inter": INTER, "score": "sigmoid", "frac_hbm_peak":
+                   round(res["gbs"] / PEAK_HBM_GBS, 4), "tokens_per_s": round(1e3 / res["ms_per_step"])},
+        "roofline": {k: v for k, v in roof.items() if k != "traffic_source"},
         "cpu_baseline": cpu,
         "math": "exact (bf16 MFMA on exactly dequantised FP4/FP8)",
-        "kernels": res["kernels"],
-        "native_math": {"value": native["gbs"], "ms_per_step": native["ms_per_step"],
-                        "kernels": native["kernels"],
-                        "note": "FP4xFP8 scaled MFMA; ~13-bit internal accumulation"},
-        "fp8_gemv_m1": gemv,
-        "fp8_gemm_m128": gemm,
-        "cpu_baseline_gemm": cpu_gemm,
-        "fp8_gemm_model_shapes": shapes,
-        "moe_prefill_m132": prefill,
-        "moe_prefill_m132_zipf_quarter": prefill_mild,
-        "moe_block_4_layers": block,
+        "native_math_value": round(native["gbs"], 1),
+        "configs": compact_configs(res, gemv, gemm, prefill, prefill_mild, block),
     }
     print(json.dumps(line), flush=True)
+
+
+def _c(avg_us, gbs=None, tflops=None, peak_gbs=PEAK_HBM_GBS):
+    d = {"avg_us": round(avg_us, 2)}
+    if gbs is not None:
+        d["GB/s"] = round(gbs, 1)
+        d["frac"] = round(gbs / peak_gbs, 4)
+    if tflops is not None:
+        d["TFLOP/s"] = round(tflops, 1)
+    return d
+
+
+def compact_configs(res, gemv, gemm, prefill, prefill_mild, block):
+    """{avg_us, GB/s, frac of 8 TB/s[, TFLOP/s]} per BASELINE config: 1 (GEMV,
+    cold weights), 2 (M=128 at each N, both scale formats, cold), 3 (the
+    decode step and its two kernels), 4 (both routing draws) and 5 (per
+    layer at each M)."""
+    out = {}
+    if gemv:
+        g = gemv["4096"]
+        out["c1_fp8_gemv_m1"] = {f: _c(g[f]["avg_us"], g[f].get("GB/s")) for f in
+                                 ("ue8m0_32", "f32_128") if f in g}
+    if gemm:
+        out["c2_fp8_gemm_m128"] = {
+            n: {f: dict(_c(d[f]["avg_us"], d[f].get("GB/s"), d[f].get("TFLOP/s")),
+                        frac_fp8=round(d[f]["frac_fp8_peak"], 4))
+                for f in ("ue8m0_32", "f32_128") if f in d} for n, d in gemm.items()}
+    ks = res["kernels"]
+    short = {"expert_glu_quant_kernel": "glu_routed",
+             "expert_glu_quant_kernel (picks given, no routing)": "glu_picks_given",
+             "expert_reduce_kernel": "reduce"}
+    out["c3_fp4_moe_decode_m1"] = dict(
+        step=_c(res["ms_per_step"] * 1e3, res["gbs"]),
+        **{short.get(n, n): _c(k["avg_us"], k.get("GB/s")) for n, k in ks.items()
+           if "avg_us" in k})
+    out["c4_moe_prefill_m132"] = {
+        "zipf1.1": _c(prefill["avg_us"], prefill["GB/s"], prefill["TFLOP/s"]),
+        "zipf1.1_native": _c(prefill["native_math"]["avg_us"], prefill["native_math"]["GB/s"]),
+        "zipf0.25": _c(prefill_mild["avg_us"], prefill_mild["GB/s"], prefill_mild["TFLOP/s"])}
+    if block:
+        out["c5_moe_block_per_layer"] = {
+            "M%s" % m: _c(b["us_per_layer"], b["GB/s"]) for m, b in block.items()}
+    return out
 
 
 if __name__ == "__main__":

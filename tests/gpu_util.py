@@ -37,10 +37,26 @@ def rel_err_stats(got, want):
     return float(r.max()), float(np.median(r)), float(np.quantile(r, 0.99))
 
 
+def raw_rel_err_stats(got, want):
+    """|got - want| / |want| with no floor, over the outputs with want != 0:
+    the unfloored distribution (max, p50, p99, p99.9), reported beside the
+    floored one. Outputs that cancel to near zero dominate its maximum."""
+    got = np.asarray(got, np.float64).ravel()
+    want = np.asarray(want, np.float64).ravel()
+    nz = want != 0
+    if not nz.any():
+        return 0.0, 0.0, 0.0, 0.0
+    r = np.abs(got[nz] - want[nz]) / np.abs(want[nz])
+    return (float(r.max()), float(np.median(r)), float(np.quantile(r, 0.99)),
+            float(np.quantile(r, 0.999)))
+
+
 def assert_close(got, want, tol, what):
     mx, p50, p99 = rel_err_stats(got, want)
-    print("[%s] rel err max %.3g p50 %.3g p99 %.3g (tol %.1g)" % (what, mx, p50, p99, tol),
-          flush=True)
+    rmx, rp50, rp99, rp999 = raw_rel_err_stats(got, want)
+    print("[%s] rel err max %.3g p50 %.3g p99 %.3g (tol %.1g, floor 1%% of max|want|); "
+          "unfloored max %.3g p50 %.3g p99 %.3g p99.9 %.3g"
+          % (what, mx, p50, p99, tol, rmx, rp50, rp99, rp999), flush=True)
     assert mx <= tol, "%s: max rel err %.3g > %.1g" % (what, mx, tol)
 
 

@@ -243,3 +243,26 @@ def test_emit_decodes_to_snap():
     amax = np.maximum(np.abs(x).reshape(-1, 32).max(1), np.float32(1e-4))
     sc = np.ldexp(1.0, s.astype(np.int32) - 127)
     assert np.all(amax / sc <= 448.0 * (1 + 1e-7)) and np.all(amax / (sc / 2) > 448.0 * (1 - 1e-7))
+
+
+def test_act_emit_infinite_block_follows_ieee_division():
+    """A block holding an infinity: amax = inf, scale 2^128 = inf (UE8M0 byte
+    0xFF, quant.rs:41-48 decodes it as NaN). The reference divides by the
+    scale (actquant.rs:39-44), so each byte is the encoding of the host's
+    IEEE quotient: a finite x gives a zero of x's sign, an infinity the
+    invalid-operation NaN (on x86 its sign bit is set), a NaN stays NaN.
+    The quotients are formed by numpy on this host, not by the oracle."""
+    with np.errstate(invalid="ignore"):
+        x = np.array([1.5, -2.0, np.inf, -np.inf, np.nan, 0.0, -0.0, 3e38] + [0.25] * 24,
+                     np.float32)
+        qv = x / np.float32(np.inf)
+    q, s = O.fp8_act_emit(x)
+    assert s[0] == 0xFF
+    sign = (np.signbit(qv).astype(np.uint8) << 7)
+    want = np.where(np.isnan(qv), sign | 0x7F, sign)   # +-0 encode as sign | 0
+    assert np.array_equal(q, want.astype(np.uint8))
+    # a block at the largest finite amax keeps a finite scale (e = 120)
+    x2 = np.zeros(32, np.float32)
+    x2[0] = np.finfo(np.float32).max
+    q2, s2 = O.fp8_act_emit(x2)
+    assert s2[0] == 120 + 127 and q2[0] == 0x78    # 2^128 (1 - 2^-24) / 2^120 -> 256

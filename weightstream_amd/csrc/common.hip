@@ -55,8 +55,13 @@ __global__ __launch_bounds__(256) void act_quant_f32s_kernel(const float *x, uin
     for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
     if (amax < 1e-4f) amax = 1e-4f;
     float sc = amax / 448.0f;
-    q[b * 128 + l] = (uint8_t)f32_to_e4m3(rclamp(x0 / sc, -448.0f, 448.0f));
-    q[b * 128 + l + 64] = (uint8_t)f32_to_e4m3(rclamp(x1 / sc, -448.0f, 448.0f));
+    // inf / inf (a block holding an infinity) is the host's invalid-operation
+    // NaN, sign bit set on x86: byte 0xFF, as block_byte
+    const bool inf_blk = sc == __builtin_inff();
+    const uint32_t q0 = f32_to_e4m3(rclamp(x0 / sc, -448.0f, 448.0f));
+    const uint32_t q1 = f32_to_e4m3(rclamp(x1 / sc, -448.0f, 448.0f));
+    q[b * 128 + l] = (uint8_t)(inf_blk && __builtin_fabsf(x0) == sc ? 0xFFu : q0);
+    q[b * 128 + l + 64] = (uint8_t)(inf_blk && __builtin_fabsf(x1) == sc ? 0xFFu : q1);
     if (l == 0) s[b] = sc;
 }
 
@@ -114,7 +119,11 @@ __global__ __launch_bounds__(256) void weight_quant_fp8_kernel(const float *w, u
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         int r = rb * 32 + (t >> 5) + 8 * j;
-        if (r < rows) q[(size_t)r * cols + c] = (uint8_t)f32_to_e4m3(rclamp(v[j] / sc, -448.0f, 448.0f));
+        // an infinity over inf is the host's negative NaN (byte 0xFF), as block_byte
+        const uint32_t b = f32_to_e4m3(rclamp(v[j] / sc, -448.0f, 448.0f));
+        if (r < rows)
+            q[(size_t)r * cols + c] =
+                (uint8_t)(sc == __builtin_inff() && __builtin_fabsf(v[j]) == sc ? 0xFFu : b);
     }
     if (t == 0) s[(size_t)rb * (cols / 32) + cb] = (uint8_t)(e + 127);
 }

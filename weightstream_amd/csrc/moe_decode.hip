@@ -245,8 +245,7 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
         amax = max8_lanes(amax);
         if (!(amax >= 1e-4f)) amax = 1e-4f;
         const int e = log2_ceil_div448(amax);
-        // x / 2^e == x * 2^-e exactly (2^-e is a normal f32 here)
-        const float inv = __builtin_ldexpf(1.0f, -e), sc = __builtin_ldexpf(1.0f, e);
+        const float inv = block_inv_scale(e), sc = __builtin_ldexpf(1.0f, e);
         const float f[4] = {v.x, v.y, v.z, v.w};
         const int i = blk * 32 + (lane & 7) * 4;
         if (EXACT) {
@@ -255,6 +254,8 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
             float d[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) d[c] = e4m3_round_value(rclamp(f[c] * inv, -448.0f, 448.0f)) * sc;
+            // (an infinite block: sc = inf, so every value is NaN, as the
+            // reference's decoded scale byte 0xFF is)
             if (blk >= b1) continue;
             *(uint2 *)(x_l + i) =
                 uint2{(__float_as_uint(d[0]) >> 16) | (__float_as_uint(d[1]) & 0xFFFF0000u),
@@ -262,7 +263,7 @@ __device__ __forceinline__ void tok_quant_f32(const TokenRegs &tr, int b0, int b
         } else {
             uint32_t q[4];
 #pragma unroll
-            for (int c = 0; c < 4; c++) q[c] = f32_to_e4m3(rclamp(f[c] * inv, -448.0f, 448.0f));
+            for (int c = 0; c < 4; c++) q[c] = block_byte(f[c], inv);
             if (blk >= b1) continue;
             *(uint32_t *)(xq_l + i) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
             if ((lane & 7) == 0) xs_l[blk] = (uint8_t)(e + 127);

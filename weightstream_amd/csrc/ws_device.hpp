@@ -244,6 +244,21 @@ __device__ __forceinline__ float max8_lanes(float v) {
     return v;
 }
 
+// x / 2^e for a block scale exponent e, as x * 2^-e. For a finite block
+// maximum the rule yields e in [-22, 120], where 2^-e is an exact normal f32
+// and the product is the quotient, rounded the same way. A block holding an
+// infinity has e = 128: the reference divides by 2^128 = inf, which sends a
+// finite x to a signed zero (so does the factor 0 below) and an infinity to
+// the invalid-operation NaN, whose sign bit the host (x86) sets: its byte is
+// 0xFF, whatever the infinity's sign (block_byte). A NaN x stays that NaN.
+__device__ __forceinline__ float block_inv_scale(int e) {
+    return e >= 128 ? 0.0f : __builtin_ldexpf(1.0f, -e);
+}
+__device__ __forceinline__ uint32_t block_byte(float x, float inv) {
+    const uint32_t b = f32_to_e4m3(rclamp(x * inv, -448.0f, 448.0f));
+    return (inv == 0.0f && __builtin_fabsf(x) == __builtin_inff()) ? 0xFFu : b;
+}
+
 // FP8 activation quantisation of one 1x32 block held one value per lane in a
 // 32-lane group (weightstream-ref actquant.rs:21-45 / act_quant_fp8_emit,
 // actquant.cu:47): amax floored at 1e-4, scale 2^log2_ceil(amax/448),
@@ -254,8 +269,7 @@ __device__ __forceinline__ uint32_t quant_fp8_block32(float x, uint32_t *scale_b
     if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's scan
     int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
-    // x / 2^e as x * 2^-e (exact scaling either way, as below)
-    return f32_to_e4m3(rclamp(x * __builtin_ldexpf(1.0f, -e), -448.0f, 448.0f));
+    return block_byte(x, block_inv_scale(e));
 }
 
 // The scale byte quant_fp8_block32 gives a block of zeros (the 1e-4 floor)
@@ -266,9 +280,7 @@ __device__ __forceinline__ uint32_t zero_block_scale_byte() {
 // The same block quantisation with four consecutive values per lane, a block
 // being 8 lanes (a lane-group of 8 aligned lanes): the bytes of
 // quant_fp8_block32, packed low value first. The block maximum is
-// order-free; x / 2^e is computed as x * 2^-e, the same real number rounded
-// the same way (2^-e is exact for the e this scale rule yields, e in
-// [-22, 120]), which costs a multiply instead of a division.
+// order-free.
 __device__ __forceinline__ uint32_t quant_fp8_block32_x4(float4 v, uint32_t *scale_byte) {
     float amax = fmaxf(fmaxf(__builtin_fabsf(v.x), __builtin_fabsf(v.y)),
                        fmaxf(__builtin_fabsf(v.z), __builtin_fabsf(v.w)));
@@ -276,11 +288,9 @@ __device__ __forceinline__ uint32_t quant_fp8_block32_x4(float4 v, uint32_t *sca
     if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's scan
     const int e = log2_ceil_div448(amax);
     *scale_byte = (uint32_t)(e + 127) & 0xFF;
-    const float inv = __builtin_ldexpf(1.0f, -e);
-    return f32_to_e4m3(rclamp(v.x * inv, -448.0f, 448.0f)) |
-           (f32_to_e4m3(rclamp(v.y * inv, -448.0f, 448.0f)) << 8) |
-           (f32_to_e4m3(rclamp(v.z * inv, -448.0f, 448.0f)) << 16) |
-           (f32_to_e4m3(rclamp(v.w * inv, -448.0f, 448.0f)) << 24);
+    const float inv = block_inv_scale(e);
+    return block_byte(v.x, inv) | (block_byte(v.y, inv) << 8) | (block_byte(v.z, inv) << 16) |
+           (block_byte(v.w, inv) << 24);
 }
 
 // Scaled MFMA, 16x16 output, K = 128: D += (A * 2^sa) (B * 2^sb).
