@@ -196,10 +196,12 @@ inline void moe_dispatch_tl(const int64_t *topk_idx, const float *topk_weights, 
                              rows, top_k, tiles, n_experts, s));
 }
 enum class TlMoe : int { GateUp = WS_TL_MOE_GATE_UP, Down = WS_TL_MOE_DOWN };
+// launch.rs:542: the stream follows top_k as there; n, k and n_experts (the
+// slab's shape, which the reference reads from its tensor map) trail it
 inline void moe_grouped_tl_cached_on(TlMoe kind, U8 a, U8 sfa, U8 weights, U8 sfb,
                                      const int32_t *order, const int32_t *tile_expert, F32 out,
-                                     int64_t tiles, int64_t tokens, int64_t top_k, int64_t n,
-                                     int64_t k, int64_t n_experts, ws_stream_t s) {
+                                     int64_t tiles, int64_t tokens, int64_t top_k, ws_stream_t s,
+                                     int64_t n, int64_t k, int64_t n_experts) {
     check("moe_grouped_tl", ws_moe_grouped_tl((int)kind, a, sfa, weights, sfb, order, tile_expert,
                                               out, tiles, tokens, top_k, n, k, n_experts, s));
 }
@@ -208,7 +210,7 @@ inline void moe_grouped_tl_cached(TlMoe kind, U8 a, U8 sfa, U8 weights, U8 sfb,
                                   int64_t tiles, int64_t tokens, int64_t top_k, int64_t n,
                                   int64_t k, int64_t n_experts) {
     moe_grouped_tl_cached_on(kind, a, sfa, weights, sfb, order, tile_expert, out, tiles, tokens,
-                             top_k, n, k, n_experts, Hip::global().stream);
+                             top_k, Hip::global().stream, n, k, n_experts);
 }
 // launch.rs:478 moe_grouped_tl: the weights as a packed slab (no tensor map)
 inline void moe_grouped_tl(TlMoe kind, U8 a, U8 sfa, U8 weights, U8 sfb, const int32_t *order,

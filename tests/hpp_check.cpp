@@ -39,7 +39,7 @@ int main() {
     });
     bad += expect_code("moe_grouped_tl kind 5", WS_ERR_INVALID_ARG, [&] {
         wl::moe_grouped_tl_cached_on((wl::TlMoe)5, fake, fake, fake, fake, (const int32_t *)fake,
-                                     (const int32_t *)fake, out, 4, 4, 2, 128, 128, 4, nullptr);
+                                     (const int32_t *)fake, out, 4, 4, 2, nullptr, 128, 128, 4);
     });
     if (!weightstream_hip::built_with_hip()) bad++;
     std::printf(bad ? "FAIL\n" : "ok\n");

@@ -26,14 +26,15 @@ import pytest
 import torch
 
 import oracle_lib as O
-from gpu_util import DEV, announce, assert_close, host, rel_err_stats
+from gpu_util import DEV, announce, assert_close, dev, host, rel_err_stats
+from test_gpu_prefill import _staged_hidden, check_routed_by_stages
 from weightstream_amd import launch as L
 
 pytestmark = pytest.mark.gpu
 
 E, TOPK, DIM, INTER = 384, 8, 4096, 2048
 OD, SI = 8192, 2048          # out-projection K, shared expert intermediate
-LAYERS = 2
+LAYERS = 4           # as the bench stacks them
 TOL = 1e-3
 
 
@@ -122,6 +123,7 @@ def _run_gpu(lay, M, attn, h0):
             L.moe_prefill(h, idx, wts, *w["packed"], yr, M, DIM, INTER, E, TOPK, pws, stream=st)
         L.shared_expert_fp8_w13(h, *w["w13"], *w["w2"], ys, M, DIM, SI, sws, stream=st)
         s.update(lg=host(lg), idx=host(idx), w=host(wts), yr=host(yr), ys=host(ys))
+        s["packed"] = w["packed"]
         L.acc_f32(ys, yr, M * DIM, stream=st)
         L.acc_f32(yr, h, M * DIM, stream=st)
         s["h_out"] = host(h)
@@ -151,6 +153,18 @@ class _HostLayer:
                                 host(r[3][a:b]), host(r[4][c:d]), host(r[5][c:d]))
         return self._experts[e]
 
+    def views(self):
+        """H[i][e] for the staged check: expert e's i-th weight tensor."""
+        hl = self
+
+        class _V:
+            def __init__(self, i):
+                self.i = i
+
+            def __getitem__(self, e):
+                return hl.expert(int(e))[self.i]
+        return [_V(i) for i in range(6)]
+
     def routed(self, x, idx, wts):
         """The oracle's routed MoE on a compact slab of the picked experts
         (ascending expert id kept, so the summation order is the same)."""
@@ -158,6 +172,25 @@ class _HostLayer:
         slab = [np.concatenate([self.expert(e)[i] for e in uniq]) for i in range(6)]
         remap = np.array([uniq.index(int(e)) for e in idx], np.int32)
         return O.moe_routed(*slab, DIM, INTER, x, remap, wts)
+
+
+def _gpu_hidden(s, M, r):
+    """The GPU's re-quantised hidden state of row r's picks (decoded), from the
+    gate/up stage the layer ran: M = 1 the decode kernel (ws_expert_glu_quant_x,
+    row p for pick p), M > 1 the grouped one (slot route_pos[r * k + j])."""
+    P = s["packed"]
+    tab = O.e4m3_decode_table().astype(np.float64)
+    dec = lambda q, sc: tab[q] * np.repeat(2.0 ** (sc.astype(np.float64) - 127), 32, axis=-1)
+    if M == 1:
+        hq = torch.empty((TOPK, INTER), dtype=torch.uint8, device=DEV)
+        hs = torch.empty((TOPK, INTER // 32), dtype=torch.uint8, device=DEV)
+        L.expert_glu_quant_x(dev(s["h_mid"][0]), dev(s["idx"][0]), dev(s["w"][0]), P[0], P[1],
+                             P[2], P[3], hq, hs, INTER, DIM, E, TOPK)
+        h = dec(host(hq), host(hs))
+        return lambda j: h[j]
+    h, route_pos = _staged_hidden(s["h_mid"], dev(s["idx"]), dev(s["w"]), P, M, E, DIM, INTER,
+                                  TOPK)
+    return lambda j: h[route_pos[r * TOPK + j]]
 
 
 def _oracle_layer(hl, attn_row, h_in):
@@ -169,7 +202,8 @@ def _oracle_layer(hl, attn_row, h_in):
     return dict(o=o, h_mid=h_mid, lg=lg, idx=idx, w=wts)
 
 
-@pytest.mark.parametrize("M,rows", [(1, [0]), (8, [0, 5, 7]), (64, [0, 31, 50, 63])])
+@pytest.mark.parametrize("M,rows", [(1, [0]), (8, list(range(8))),
+                                    (64, [0, 9, 18, 27, 36, 45, 54, 63])])
 def test_config5_block_matches_oracle(block, M, rows):
     gen = torch.Generator(device=DEV)
     gen.manual_seed(5100 + M)
@@ -194,7 +228,11 @@ def test_config5_block_matches_oracle(block, M, rows):
                 assert np.array_equal(s["idx"][r], ri), (what, s["idx"][r], ri)
                 assert np.array_equal(s["w"][r].view(np.uint32), rw.view(np.uint32)), what
                 yr = hl.routed(s["h_mid"][r], ri, rw)
-                assert_close(s["yr"][r], yr, TOL, what + " routed")
+                if rel_err_stats(s["yr"][r], yr)[0] <= TOL:
+                    assert_close(s["yr"][r], yr, TOL, what + " routed")
+                else:   # an h element on an e4m3 rounding midpoint: check by stages
+                    check_routed_by_stages(s["yr"][r], s["h_mid"][r], ri, rw, hl.views(),
+                                           _gpu_hidden(s, M, r), what + " routed", DIM, INTER)
                 ys = O.shared_fp8(*hl.sh, DIM, SI, s["h_mid"][r])
                 assert_close(s["ys"][r], ys, TOL, what + " shared")
                 h_out = (s["h_mid"][r] + (yr + ys).astype(np.float32)).astype(np.float32)

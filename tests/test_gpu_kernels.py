@@ -364,3 +364,40 @@ def test_long_k_strip_split_matches_single_pass(m, n, k):
     assert L.gemm_workspace_size(m, n, k) > 0
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     assert_close(outs[0], host(single), GEMM_TOL, "strip split m=%d n=%d k=%d" % (m, n, k))
+
+
+def test_workspace_registered_under_one_mode_serves_both():
+    """set_gemm_workspace registers with both library builds: a NATIVE-mode
+    GEMM on a stream whose workspace was set while EXACT was active takes the
+    split-K path (it writes partials into the workspace) and gives the bits
+    of the same NATIVE GEMM registered under NATIVE."""
+    m, n, k = 128, 12288, 4096
+    gen = torch.Generator(device=DEV).manual_seed(77)
+    x = torch.randn((m, k), device=DEV, generator=gen)
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    asc = torch.empty((m, k // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, aq, asc, m * k)
+    wf = torch.randn((n, k), device=DEV, generator=gen) * 0.02
+    w = torch.empty((n, k), dtype=torch.uint8, device=DEV)
+    sw = torch.empty((n // 32, k // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(wf, w, sw, n, k)
+    ws = torch.full((L.gemm_workspace_size(m, n, k),), 0xAB, dtype=torch.uint8, device=DEV)
+    outs = []
+    try:
+        for reg_mode in (L.MATH_EXACT, L.MATH_NATIVE):
+            L.set_math_mode(reg_mode)
+            L.set_gemm_workspace(ws)
+            ws.fill_(0xAB)
+            L.set_math_mode(L.MATH_NATIVE)
+            announce("native fp8_gemm after a workspace set in mode %d" % reg_mode)
+            out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+            L.fp8_gemm(aq, asc, w, sw, out, m, n, k)
+            torch.cuda.synchronize()
+            assert (ws != 0xAB).any(), "the split-K path did not run"
+            outs.append(out)
+            L.set_gemm_workspace(None)
+    finally:
+        L.set_math_mode(L.MATH_EXACT)
+        torch.cuda.synchronize()
+        L.set_gemm_workspace(None)
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))

@@ -185,17 +185,25 @@ def test_config4_baseline_weights_prefill_matches_oracle(zipf):
     P = _packed(slabs, E, dim, inter)
     L.moe_prefill(dev(x), idx, w, *P, y, m, dim, inter, E, k, ws)
     gi, gw, gy = host(idx), host(w), host(y)
-    rows = np.linspace(0, m - 1, 6).astype(int)
-    H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
+    H = _host_experts(slabs, gi.ravel(), E, dim, inter)
     staged = None
-    for r in rows:
-        want = O.moe_routed(*H, dim, inter, x[r], gi[r], gw[r])
-        if rel_err_stats(gy[r], want)[0] <= MOE_TOL:
-            assert_close(gy[r], want, MOE_TOL, "config 4 row %d" % r)
+    ok = []
+    O.set_threads(16)   # the oracle's GEMV rows in threads: the same bits
+    try:
+        want = np.stack([O.moe_routed(*H, dim, inter, x[r], gi[r], gw[r]) for r in range(m)])
+    finally:
+        O.set_threads(1)
+    for r in range(m):   # every row of the benched batch
+        if rel_err_stats(gy[r], want[r])[0] <= MOE_TOL:
+            ok.append(r)
             continue
         if staged is None:
             staged = _staged_hidden(x, idx, w, P, m, E, dim, inter, k)
         _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
+    # the distribution over all rows that met the bar directly
+    print("[config 4 zipf %.3g] %d of %d rows direct, %d by stages" % (zipf, len(ok), m,
+                                                                      m - len(ok)), flush=True)
+    assert_close(gy[ok], want[ok], MOE_TOL, "config 4 zipf %.3g, all direct rows" % zipf)
 
 
 def _staged_hidden(x, idx, w, P, m, E, dim, inter, k):
@@ -222,6 +230,16 @@ def _staged_hidden(x, idx, w, P, m, E, dim, inter, k):
 
 def _check_by_stages(got_row, x_row, gi, gw, H, staged, r, k, dim, inter, limit=10.0):
     h_gpu, route_pos = staged
+    check_routed_by_stages(got_row, x_row, gi, gw, H, lambda j: h_gpu[route_pos[r * k + j]],
+                           "moe_prefill row %d" % r, dim, inter, limit)
+
+
+def check_routed_by_stages(got_row, x_row, gi, gw, H, h_of_pick, what, dim, inter, limit=10.0):
+    """A routed-MoE row that missed the tolerance: every element where the
+    GPU's re-quantised h (h_of_pick(j), decoded, for pick j) differs from the
+    oracle's must be a rounding-midpoint case, and the output must match the
+    oracle's down projection of the GPU's h. H[i][e]: expert e's w1, s1, w3,
+    s3, w2, s2 as the oracle takes them."""
     y = np.zeros(dim, np.float32)
     flips = 0
     for j in np.argsort(gi, kind="stable"):  # expert order, as moe.rs:75-84 sums
@@ -231,19 +249,18 @@ def _check_by_stages(got_row, x_row, gi, gw, H, staged, r, k, dim, inter, limit=
         g, u = np.minimum(g, limit), np.clip(u, -limit, limit)
         h_pre = g / (1.0 + np.exp(-g)) * u * rw
         h_or = O.fp8_snap(h_pre.astype(np.float32)).astype(np.float64)
-        hg = h_gpu[route_pos[r * k + j]]
+        hg = h_of_pick(j)
         for i in np.nonzero(hg != h_or)[0]:
             blk = np.abs(h_or[i // 32 * 32:(i // 32 + 1) * 32]).max()
             mid = 0.5 * (hg[i] + h_or[i])
-            assert abs(hg[i] - h_or[i]) <= blk / 8, "row %d h[%d]: not adjacent" % (r, i)
+            assert abs(hg[i] - h_or[i]) <= blk / 8, "%s h[%d]: not adjacent" % (what, i)
             assert abs(h_pre[i] - mid) <= 1e-4 * blk, \
-                "row %d h[%d]: %r vs %r, not a rounding midpoint" % (r, i, hg[i], h_or[i])
+                "%s h[%d]: %r vs %r, not a rounding midpoint" % (what, i, hg[i], h_or[i])
             flips += 1
         y += O.fp4_gemv(H[4][e], H[5][e], dim, inter, hg.astype(np.float32))
-    print("[moe_prefill row %d] %d h element(s) on an e4m3 rounding midpoint" % (r, flips),
-          flush=True)
-    assert flips > 0, "row %d misses the tolerance with h identical to the oracle's" % r
-    assert_close(got_row, y, MOE_TOL, "moe_prefill row %d (staged)" % r)
+    print("[%s] %d h element(s) on an e4m3 rounding midpoint" % (what, flips), flush=True)
+    assert flips > 0, "%s misses the tolerance with h identical to the oracle's" % what
+    assert_close(got_row, y, MOE_TOL, what + " (staged)")
 
 
 def test_prefill_of_one_token_matches_decode():

@@ -90,3 +90,67 @@ def test_rejects_bad_header(tmp_path):
     p.write_bytes((1 << 40).to_bytes(8, "little") + b"{}")
     with pytest.raises(ValueError, match="header length"):
         I.Shard(str(p))
+
+
+def test_read_config_merges_text_config(tmp_path):
+    """config.rs:109-130: a nested text_config wins; model_type, architectures
+    and quantization_config survive from the top level unless redeclared."""
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                          "config_1017_moe.json")
+    with open(golden) as f:
+        c = json.load(f)
+    c["quantization_config"] = {"fmt": "e4m3"}
+    c["text_config"]["model_type"] = "inner"
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump(c, f)
+    cfg = I.read_config(str(tmp_path))
+    assert cfg["hidden_size"] == 5120 and cfg["moe_intermediate_size"] == 2304
+    assert cfg["num_experts_per_tok"] == 6 and cfg["scoring_func"] == "sqrtsoftplus"
+    assert cfg["model_type"] == "inner"                       # redeclared inside
+    assert cfg["architectures"] == ["DeepseekV41ForCausalLM"]   # from the top level
+    assert cfg["quantization_config"] == {"fmt": "e4m3"}
+    del c["text_config"]["hidden_size"]
+    with open(tmp_path / "config.json", "w") as f:
+        json.dump(c, f)
+    with pytest.raises(ValueError, match="hidden_size"):
+        I.read_config(str(tmp_path))
+
+
+def test_load_moe_layer_assembles_gate_shared_and_w13(tmp_path):
+    E, dim, inter, si = 2, 64, 64, 64
+    rng = np.random.default_rng(3)
+    t = {}
+    for e in range(E):
+        for wn, (rows, cols) in (("w1", (inter, dim)), ("w3", (inter, dim)), ("w2", (dim, inter))):
+            base = "l.ffn.experts.%d.%s" % (e, wn)
+            t[base + ".weight"] = ("U8", (rows, cols // 2),
+                                   rng.integers(0, 256, (rows, cols // 2), dtype=np.uint8))
+            t[base + ".scale"] = ("U8", (rows, cols // 32),
+                                  rng.integers(118, 124, (rows, cols // 32), dtype=np.uint8))
+    sh = {}
+    for wn, (rows, cols) in (("w1", (si, dim)), ("w3", (si, dim)), ("w2", (dim, si))):
+        w = rng.integers(0, 126, (rows, cols), dtype=np.uint8)
+        s = rng.integers(118, 124, (rows // 32, cols // 32), dtype=np.uint8)
+        t["l.ffn.shared_experts.%s.weight" % wn] = ("F8_E4M3", w.shape, w)
+        t["l.ffn.shared_experts.%s.scale" % wn] = ("F8_E8M0", s.shape, s)
+        sh[wn] = (w, s)
+    gw = rng.integers(0, 1 << 16, (E, dim), dtype=np.uint16)
+    gb = rng.standard_normal(E).astype(np.float32)
+    t["l.ffn.gate.weight"] = ("BF16", (E, dim), gw.view(np.uint8))
+    t["l.ffn.gate.bias"] = ("F32", (E,), gb.view(np.uint8))
+    I.write_safetensors(str(tmp_path / "model.safetensors"), t)
+    ck = I.Checkpoint(str(tmp_path))
+    lay = I.load_moe_layer(ck, "l", E, dim, inter, si, device="cpu")
+    assert np.array_equal(lay["gate_w"].numpy().view(np.uint16), gw)
+    assert np.array_equal(lay["gate_bias"].numpy(), gb)
+    w13, s13 = lay["shared_w13"]
+    # engine.rs:962-964: w1's rows then w3's, scales likewise
+    assert np.array_equal(w13.numpy(), np.concatenate([sh["w1"][0], sh["w3"][0]]))
+    assert np.array_equal(s13.numpy(), np.concatenate([sh["w1"][1], sh["w3"][1]]))
+    for wn in ("w1", "w2", "w3"):
+        assert np.array_equal(lay["shared"][wn][0].numpy(), sh[wn][0])
+    assert len(lay["experts"]) == 6
+    with pytest.raises(ValueError, match="n % 32"):
+        I.load_fp8_combined_rows(ck, "l.ffn.shared_experts.w1", "l.ffn.shared_experts.w3", 48,
+                                 dim, device="cpu")
+    ck.close()

@@ -53,7 +53,7 @@ __global__ __launch_bounds__(256) void act_quant_f32s_kernel(const float *x, uin
     float amax = fmaxf(__builtin_fabsf(x0), __builtin_fabsf(x1));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
-    if (amax < 1e-4f) amax = 1e-4f;
+    if (!(amax >= 1e-4f)) amax = 1e-4f;  // an all-NaN block too, as the reference's `a > amax` scan
     float sc = amax / 448.0f;
     // inf / inf (a block holding an infinity) is the host's invalid-operation
     // NaN, sign bit set on x86: byte 0xFF, as block_byte

@@ -146,6 +146,64 @@ def load_fp8_linear(ck, name, n, k, device="cuda"):
             torch.from_numpy(s.copy()).view((n + 31) // 32, k // 32).to(device))
 
 
+def load_fp8_combined_rows(ck, name_a, name_b, n, k, device="cuda"):
+    """engine.rs:931-971 load_q8_combined_rows: two FP8 linears of the same K
+    stacked by rows (a's rows, then b's) with their UE8M0 scale rows
+    concatenated the same way: w [2n, k], s [2n/32, k/32]. n must be a
+    multiple of 32 so that b's scale rows start a fresh 32-row block."""
+    if n % 32:
+        raise ValueError("combined rows need n %% 32 == 0 (n = %d)" % n)
+    wa, sa = load_fp8_linear(ck, name_a, n, k, device)
+    wb, sb = load_fp8_linear(ck, name_b, n, k, device)
+    return torch.cat([wa, wb]), torch.cat([sa, sb])
+
+
+def load_gate(ck, prefix, n_experts, dim, device="cuda"):
+    """engine.rs:1482-1493: `<prefix>.ffn.gate.weight` bf16 [E, dim] (as the
+    raw 16-bit words, for ws_moe_gate_logits with w_bf16 = 1) and
+    `<prefix>.ffn.gate.bias` f32 [E]."""
+    w = _expect(ck, prefix + ".ffn.gate.weight", "bf16", n_experts * dim * 2)
+    b = _expect(ck, prefix + ".ffn.gate.bias", "f32", n_experts * 4)
+    return (torch.from_numpy(w.copy().view(np.int16)).view(n_experts, dim).to(device),
+            torch.from_numpy(b.copy().view(np.float32)).to(device))
+
+
+def load_moe_layer(ck, prefix, n_experts, dim, inter, shared_inter, device="cuda"):
+    """One MoE layer as engine.rs:1346-1530 assembles it: the gate (bf16
+    weight + f32 bias), the routed experts' raw slabs (load_expert_slabs),
+    the shared expert's FP8 w1 / w2 / w3 and the fused w13
+    (load_fp8_combined_rows). Returns a dict of device tensors."""
+    gate_w, gate_b = load_gate(ck, prefix, n_experts, dim, device)
+    sp = prefix + ".ffn.shared_experts."
+    shared = {wn: load_fp8_linear(ck, sp + wn, *(shape + (device,)))
+              for wn, shape in (("w1", (shared_inter, dim)), ("w3", (shared_inter, dim)),
+                                ("w2", (dim, shared_inter)))}
+    w13 = load_fp8_combined_rows(ck, sp + "w1", sp + "w3", shared_inter, dim, device)
+    return {"gate_w": gate_w, "gate_bias": gate_b,
+            "experts": load_expert_slabs(ck, prefix, n_experts, dim, inter, device),
+            "shared": shared, "shared_w13": w13}
+
+
+def read_config(path):
+    """The MoE fields of `config.json` (weightstream-core config.rs:19-130):
+    a nested `text_config` (the DS4.1F-1017 layout) is merged over the top
+    level as the reference does, model_type / architectures /
+    quantization_config surviving from the top level unless redeclared."""
+    with open(os.path.join(path, "config.json")) as f:
+        cfg = json.load(f)
+    inner = cfg.pop("text_config", None)
+    if inner is not None:
+        for key in ("model_type", "architectures", "quantization_config"):
+            if key not in inner and key in cfg:
+                inner[key] = cfg[key]
+        cfg = inner
+    for key in ("hidden_size", "qk_rope_head_dim", "vocab_size", "num_hidden_layers",
+                "num_attention_heads"):
+        if key not in cfg:
+            raise ValueError("config.json lacks %s" % key)
+    return cfg
+
+
 def load_expert_slabs(ck, prefix, n_experts, dim, inter, device="cuda"):
     """Routed experts of one layer (`<prefix>.ffn.experts.<e>.w{1,2,3}`),
     concatenated into raw slabs (w1, s1, w3, s3, w2, s2): w1/w3 [E*inter,

@@ -160,11 +160,17 @@ def set_gemm_workspace(ws, stream=None):
     """Register (a uint8 device tensor) or clear (None) the split-K workspace
     of `stream` (default: the current stream) on the current device; GEMMs
     issued on that stream use it. The caller keeps `ws` alive while it is
-    set."""
-    if ws is None:
-        _call("ws_set_gemm_workspace", None, 0, _s(stream))
-    else:
-        _call("ws_set_gemm_workspace", _ptr(ws), ws.numel() * ws.element_size(), _s(stream))
+    set. The registration goes to every library build (EXACT and NATIVE), so a
+    GEMM on `stream` takes the split-K path whichever math mode it runs in."""
+    ptr, size = (None, 0) if ws is None else (_ptr(ws), ws.numel() * ws.element_size())
+    for native in (False, True):
+        try:
+            lib = _lib.load(native=native)
+        except RuntimeError:
+            if native != _native():
+                continue        # that build is absent; only the active one must exist
+            raise
+        _lib.check("ws_set_gemm_workspace", lib.ws_set_gemm_workspace(ptr, size, _s(stream)))
 
 
 
@@ -469,7 +475,15 @@ def moe_grouped_tl(kind, a, sfa, weights, sfb, order, tile_expert, out, tiles, t
 
 
 moe_grouped_tl_cached = moe_grouped_tl
-moe_grouped_tl_cached_on = moe_grouped_tl
+
+
+def moe_grouped_tl_cached_on(kind, a, sfa, weights, sfb, order, tile_expert, out, tiles, tokens,
+                             top_k, stream, *, n, k, n_experts):
+    """launch.rs:542 argument order: the stream right after top_k; the slab's
+    shape (n, k, n_experts), which the reference reads from its tensor map,
+    as keywords."""
+    moe_grouped_tl(kind, a, sfa, weights, sfb, order, tile_expert, out, tiles, tokens, top_k, n,
+                   k, n_experts, stream=stream)
 
 
 def moe_swiglu_route(gate, up, weights, out, inter, rows, stream=None):
