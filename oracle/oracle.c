@@ -575,6 +575,19 @@ void or_expert_fp4(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, cons
     free(g); free(u); free(h);
 }
 
+/* The hidden state of or_expert_fp4 before its FP8 re-quantisation (the
+ * input or_fp4_gemv snaps for the down projection): moe.rs:162-200. */
+void or_expert_hidden_fp4(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
+                          const uint8_t *s3, size_t dim, size_t inter, const float *x, float rw,
+                          float limit, float *h) {
+    float *g = (float *)malloc(inter * sizeof(float));
+    float *u = (float *)malloc(inter * sizeof(float));
+    or_fp4_gemv(w1, s1, inter, dim, x, g);
+    or_fp4_gemv(w3, s3, inter, dim, x, u);
+    swiglu(g, u, inter, limit, rw, 1, h);
+    free(g); free(u);
+}
+
 /* moe.rs:210-250 */
 void or_shared_fp8(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
                    const uint8_t *w2, const uint8_t *s2, size_t dim, size_t inter,

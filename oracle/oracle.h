@@ -92,6 +92,9 @@ void or_expert_fp4(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, cons
                    const uint8_t *w2, const uint8_t *s2, size_t dim, size_t inter,
                    const float *x, float rw, float limit, float *y);
 /* shared expert: fp8 gate/up/down, no routing weight */
+void or_expert_hidden_fp4(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3,
+                          const uint8_t *s3, size_t dim, size_t inter, const float *x, float rw,
+                          float limit, float *h);
 void or_shared_fp8(const uint8_t *w1, const uint8_t *s1, const uint8_t *w3, const uint8_t *s3,
                    const uint8_t *w2, const uint8_t *s2, size_t dim, size_t inter,
                    const float *x, float limit, float *y);

@@ -66,6 +66,8 @@ _sigs = {
     "or_route": (None, [_f32p, _f32p, _sz, _sz, C.c_int, C.c_float, _i32p, _f32p]),
     "or_expert_fp4": (None, [_u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _f32p,
                              C.c_float, C.c_float, _f32p]),
+    "or_expert_hidden_fp4": (None, [_u8p, _u8p, _u8p, _u8p, _sz, _sz, _f32p, C.c_float,
+                                     C.c_float, _f32p]),
     "or_shared_fp8": (None, [_u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _f32p,
                              C.c_float, _f32p]),
     "or_moe_routed": (None, [_u8p, _u8p, _u8p, _u8p, _u8p, _u8p, _sz, _sz, _f32p, _i32p,
@@ -270,6 +272,16 @@ def expert_fp4(w1, s1, w3, s3, w2, s2, dim, inter, x, rw, limit=10.0):
     lib.or_expert_fp4(*[_p(v, _u8p) for v in a], dim, inter, _p(x, _f32p), rw, limit,
                       _p(y, _f32p))
     return y
+
+
+def expert_hidden_fp4(w1, s1, w3, s3, dim, inter, x, rw, limit=10.0):
+    """The expert's SwiGLU hidden state (times rw) before its FP8 snap."""
+    a = [_c(v, np.uint8) for v in (w1, s1, w3, s3)]
+    x = _c(x, np.float32)
+    h = np.empty(inter, np.float32)
+    lib.or_expert_hidden_fp4(*[_p(v, _u8p) for v in a], dim, inter, _p(x, _f32p), rw, limit,
+                             _p(h, _f32p))
+    return h
 
 
 def shared_fp8(w1, s1, w3, s3, w2, s2, dim, inter, x, limit=10.0):

@@ -244,11 +244,11 @@ def check_routed_by_stages(got_row, x_row, gi, gw, H, h_of_pick, what, dim, inte
     flips = 0
     for j in np.argsort(gi, kind="stable"):  # expert order, as moe.rs:75-84 sums
         e, rw = int(gi[j]), float(gw[j])
-        g = O.fp4_gemv(H[0][e], H[1][e], inter, dim, x_row).astype(np.float64)
-        u = O.fp4_gemv(H[2][e], H[3][e], inter, dim, x_row).astype(np.float64)
-        g, u = np.minimum(g, limit), np.clip(u, -limit, limit)
-        h_pre = g / (1.0 + np.exp(-g)) * u * rw
-        h_or = O.fp8_snap(h_pre.astype(np.float32)).astype(np.float64)
+        # the oracle's own f32 hidden state and its snap, as moe_routed computes them
+        h32 = O.expert_hidden_fp4(H[0][e], H[1][e], H[2][e], H[3][e], dim, inter, x_row, rw,
+                                  limit)
+        h_pre = h32.astype(np.float64)
+        h_or = O.fp8_snap(h32).astype(np.float64)
         hg = h_of_pick(j)
         for i in np.nonzero(hg != h_or)[0]:
             blk = np.abs(h_or[i // 32 * 32:(i // 32 + 1) * 32]).max()

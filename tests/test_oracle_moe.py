@@ -214,3 +214,27 @@ def test_threaded_oracle_is_bit_identical():
     finally:
         O.set_threads(1)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_expert_hidden_composes_to_the_routed_expert():
+    """or_expert_hidden_fp4 is the hidden state or_moe_routed feeds its down
+    GEMV: the down projection of it equals a one-pick routed MoE bit for bit,
+    and it equals silu(min(g, L)) * clamp(u, +-L) * rw of the two GEMVs to
+    f32 rounding."""
+    rng = np.random.default_rng(12)
+    dim, inter = 256, 128
+    w1, w3 = (rng.integers(0, 256, (inter, dim // 2), dtype=np.uint8) for _ in range(2))
+    s1, s3 = (rng.integers(118, 124, (inter, dim // 32), dtype=np.uint8) for _ in range(2))
+    w2 = rng.integers(0, 256, (dim, inter // 2), dtype=np.uint8)
+    s2 = rng.integers(118, 124, (dim, inter // 32), dtype=np.uint8)
+    x = rng.standard_normal(dim).astype(np.float32)
+    h = O.expert_hidden_fp4(w1, s1, w3, s3, dim, inter, x, 0.7, 2.0)
+    y = O.fp4_gemv(w2, s2, dim, inter, h)
+    y1 = O.moe_routed(w1[None], s1[None], w3[None], s3[None], w2[None], s2[None], dim, inter, x,
+                      np.array([0], np.int32), np.array([0.7], np.float32), 2.0)
+    assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+    g = O.fp4_gemv(w1, s1, inter, dim, x).astype(np.float64)
+    u = O.fp4_gemv(w3, s3, inter, dim, x).astype(np.float64)
+    g, u = np.minimum(g, 2.0), np.clip(u, -2.0, 2.0)
+    ref = g / (1.0 + np.exp(-g)) * u * 0.7
+    assert np.allclose(h, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
