@@ -401,3 +401,52 @@ def test_workspace_registered_under_one_mode_serves_both():
         torch.cuda.synchronize()
         L.set_gemm_workspace(None)
     assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+
+
+@pytest.mark.parametrize("m,n,k", [(100, 4096, 4096), (65, 3072, 2048), (128, 5120, 1024),
+                                   (127, 3104, 4096)])
+@pytest.mark.parametrize("native", [False, True])
+def test_line_gemm_ragged_rows_vs_fp64_dequant(m, n, k, native):
+    """The 64 x 32 line kernel (M in 65-128, 192-384 column-block pairs, K a
+    multiple of 512): ragged last row blocks, the XCD-paired tile order and
+    (n = 3104: 194 workgroups) the plain order, UE8M0 and f32 scales, f32
+    and bf16 outputs, against an f64 matmul of the dequantised operands.
+    EXACT within 1e-3; NATIVE within its own 5e-2 (tests/test_gpu_native.py)."""
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(m + n + k)
+    tol = 5e-2 if native else GEMM_TOL
+    announce("line gemm m=%d n=%d k=%d native=%d" % (m, n, k, native))
+    x = torch.randn((m, k), device=DEV, generator=gen)
+    x = torch.where(torch.rand((m, k), device=DEV, generator=gen) < 0.01, x * 20, x)
+    w = torch.randn((n, k), device=DEV, generator=gen) * 0.02
+    aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    as_ = torch.empty((m, k // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, aq, as_, m * k)
+    wq = torch.empty((n, k), dtype=torch.uint8, device=DEV)
+    ws = torch.empty((n // 32, k // 32), dtype=torch.uint8, device=DEV)
+    L.weight_quant_fp8(w, wq, ws, n, k)
+    table = torch.from_numpy(O.e4m3_decode_table().astype(np.float64)).to(DEV)
+    pw = lambda s: torch.pow(2.0, s.to(torch.float64) - 127)
+    da = table[aq.long()] * pw(as_).repeat_interleave(32, 1)
+    dw = table[wq.long()] * pw(ws).repeat_interleave(32, 0).repeat_interleave(32, 1)
+    want = (da @ dw.T).cpu().numpy()
+    # f32 scales: the same codes with per-block f32 scales (128 x 128 / 1 x 128)
+    af = torch.rand((m, k // 128), device=DEV, generator=gen) * 0.01 + 1e-3
+    wf = torch.rand((n // 128 + (n % 128 > 0), k // 128), device=DEV, generator=gen) * 1e-4 + 1e-5
+    daf = table[aq.long()] * af.double().repeat_interleave(128, 1)
+    dwf = table[wq.long()] * wf.double().repeat_interleave(128, 0)[:n].repeat_interleave(128, 1)
+    want_f = (daf @ dwf.T).cpu().numpy()
+    prev = L.set_math_mode(L.MATH_NATIVE if native else L.MATH_EXACT)
+    try:
+        out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+        L.fp8_gemm(aq, as_, wq, ws, out, m, n, k)
+        assert_close(host(out), want, tol, "line gemm %dx%dx%d" % (m, n, k))
+        ob = torch.empty((m, n), dtype=torch.int16, device=DEV)
+        L.fp8_gemm_bf16(aq, as_, wq, ws, ob, m, n, k)
+        got = (host(ob).astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        assert_close(got, want, 2.0 ** -8 + tol, "line gemm bf16 %dx%dx%d" % (m, n, k))
+        outf = torch.empty((m, n), dtype=torch.float32, device=DEV)
+        L.fp8_gemm_f32s(aq, af, wq, wf, outf, m, n, k)
+        assert_close(host(outf), want_f, tol, "line gemm f32s %dx%dx%d" % (m, n, k))
+    finally:
+        L.set_math_mode(prev)

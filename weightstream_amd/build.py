@@ -21,7 +21,7 @@ BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libweightstream_hip.so")
 LIB_NATIVE = os.path.join(PKG, "libweightstream_hip_native.so")
 
-SOURCES = ["common.hip", "pack.hip", "gemm.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip",
+SOURCES = ["common.hip", "pack.hip", "gemm.hip", "gemm_line.hip", "moe_route.hip", "moe_decode.hip", "moe_grouped.hip",
            "moe_shared.hip"]
 
 HIPCC_FLAGS = [

@@ -1180,7 +1180,13 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
             const long cus = cu_count();
             const long wg64 = (long)(N / 32) * ((M + 63) / 64), wg32 = (long)(N / 32) * ((M + 31) / 32);
             if (wg64 * 4 >= cus * 3 && wg64 * 2 <= cus * 3) {
-                rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+                // 64 x 32 tiles: the line kernel (whole-line LDS stages of
+                // 512 K, XCD-paired row blocks) when K allows its stages;
+                // measured at M=128, N=4096, K=4096: 13.8 against 16.6 us
+                if (!BFP4 && K % 512 == 0 && M > 64)
+                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 0);
+                if (rc < 0)
+                    rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
             } else if (wg32 * 4 >= cus * 3 && wg32 * 2 <= cus * 3) {
                 // 32-row blocks: the A-resident kernel (K <= 4096), else kp
                 if (!BFP4) rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);

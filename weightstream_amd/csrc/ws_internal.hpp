@@ -41,4 +41,9 @@ int gate_w13_launch(const float *h, const float *gw, float *logits, const uint8_
                     const uint8_t *s13, float *hs, int64_t m, int64_t dim, int64_t n_experts,
                     int64_t inter, float limit, hipStream_t stream);
 
+// gemm_line.hip: the FP8 GEMM for row blocks of 33-128 rows with whole-K
+// tiles (configuration cfg); -1 when the shape does not fit that tiling.
+int line_gemm(int smode, int omode, const uint8_t *a, const void *sa, const uint8_t *b,
+              const void *sb, void *out, int m, int n, int k, hipStream_t stream, int cfg);
+
 }  // namespace ws
