@@ -404,11 +404,12 @@ def test_workspace_registered_under_one_mode_serves_both():
 
 
 @pytest.mark.parametrize("m,n,k", [(100, 4096, 4096), (65, 3072, 2048), (128, 5120, 1024),
-                                   (127, 3104, 4096)])
+                                   (127, 3104, 4096), (100, 2048, 4096), (40, 4096, 2048)])
 @pytest.mark.parametrize("native", [False, True])
 def test_line_gemm_ragged_rows_vs_fp64_dequant(m, n, k, native):
-    """The 64 x 32 line kernel (M in 65-128, 192-384 column-block pairs, K a
-    multiple of 512): ragged last row blocks, the XCD-paired tile order and
+    """The line kernel (K a multiple of 512): 64 x 32 tiles for M in 65-128
+    with 192-384 workgroups, 32 x 32 tiles for 32-row blocks (n = 2048 at
+    M = 100; M = 40); ragged last row blocks, the XCD-paired tile order and
     (n = 3104: 194 workgroups) the plain order, UE8M0 and f32 scales, f32
     and bf16 outputs, against an f64 matmul of the dequantised operands.
     EXACT within 1e-3; NATIVE within its own 5e-2 (tests/test_gpu_native.py)."""

@@ -1169,6 +1169,14 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
     int cfg = forced_cfg();
     if (cfg < 0) {
         int rc = -1;
+        static const int line_knob = [] {  // measurement knob: force a line-kernel tiling
+            const char *e = getenv("WS_GEMM_LINE");
+            return e ? atoi(e) : -1;
+        }();
+        if (!BFP4 && line_knob >= 0 && M > 16) {
+            rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, line_knob);
+            if (rc >= 0) return rc;
+        }
         // 1. 32-column strips when they give the chip one round of workgroups:
         // 64-row blocks (M=128, N=4096) or 32-row blocks (M=128, N=2048;
         // M=64, N=4096). Measured at K=4096: 16.4 us (kp) and 10.0 us (A in
@@ -1188,8 +1196,12 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
                 if (rc < 0)
                     rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
             } else if (wg32 * 4 >= cus * 3 && wg32 * 2 <= cus * 3) {
-                // 32-row blocks: the A-resident kernel (K <= 4096), else kp
-                if (!BFP4) rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
+                // 32-row blocks: the line kernel with 32 x 32 tiles (M=128,
+                // N=2048, K=4096: 9.95 against 10.9 us for the A-resident
+                // kernel), else the A-resident kernel (K <= 4096), else kp
+                if (!BFP4 && K % 512 == 0)
+                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 2);
+                if (!BFP4 && rc < 0) rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
                 if (rc < 0)
                     rc = launch_kp<2, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
             }

@@ -1,5 +1,6 @@
-// FP8 block-scaled GEMM for row blocks of 33-128 rows (
-// M = 128, K = 4096): the "line" kernel.
+// FP8 block-scaled GEMM for blocks of 32 or 64 rows with K a multiple of 512
+// (M = 128, K = 4096, N = 4096 and 2048): the "line"
+// kernel.
 //
 // Reference semantics: weightstream-cuda/kernels/fp8_gemm_tile.cu:28-92 and
 // weightstream-ref actquant.rs:110-140 (y = sum over K blocks of the
@@ -310,6 +311,8 @@ static int launch_line(const uint8_t *a, const void *sa, const uint8_t *b, const
     switch (cfg) {
         // 64 x 32 tiles, 4 waves on the 4 sub-steps of 512-K stages, 3 stages
         case 0: return launch_line_cfg<64, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
+        // 32 x 32 tiles (four row blocks per column block on one XCD), 3 stages
+        case 2: return launch_line_cfg<32, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
         default: return -1;
     }
 }
