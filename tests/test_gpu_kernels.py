@@ -209,9 +209,9 @@ def test_config2_fp8_gemm_f32s_full_size_matches_oracle(n, gemm_path):
     outliers x20 quantised per 1x128 on the device (bit-exact with the
     oracle); f32 and bf16 outputs against the oracle's sequential
     dequantise-then-f32-accumulate GEMM (or_gemm_f32s) on every row. Runs
-    with and without the split-K workspace (the 128 x 256 split-K pipeline at
-    N = 12288, the 64 x 32 strips at N = 4096, the A-resident kernel at
-    N = 2048)."""
+    with and without the split-K workspace (the line kernel takes all three
+    N: 128 x 48 tiles at N = 12288, 64 x 32 at N = 4096, 32 x 32 at
+    N = 2048; the split-K pipeline is covered by the model shapes below)."""
     m, k = 128, 4096
     rng = np.random.default_rng(3100 + n)
     x = activations(rng, m, k)
@@ -371,7 +371,7 @@ def test_workspace_registered_under_one_mode_serves_both():
     GEMM on a stream whose workspace was set while EXACT was active takes the
     split-K path (it writes partials into the workspace) and gives the bits
     of the same NATIVE GEMM registered under NATIVE."""
-    m, n, k = 128, 12288, 4096
+    m, n, k = 128, 8192, 2048     # the split-K pipeline's shape (no line tiling)
     gen = torch.Generator(device=DEV).manual_seed(77)
     x = torch.randn((m, k), device=DEV, generator=gen)
     aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
@@ -404,12 +404,14 @@ def test_workspace_registered_under_one_mode_serves_both():
 
 
 @pytest.mark.parametrize("m,n,k", [(100, 4096, 4096), (65, 3072, 2048), (128, 5120, 1024),
-                                   (127, 3104, 4096), (100, 2048, 4096), (40, 4096, 2048)])
+                                   (127, 3104, 4096), (100, 2048, 4096), (40, 4096, 2048),
+                                   (120, 12288, 4096), (128, 9216, 768)])
 @pytest.mark.parametrize("native", [False, True])
 def test_line_gemm_ragged_rows_vs_fp64_dequant(m, n, k, native):
     """The line kernel (K a multiple of 512): 64 x 32 tiles for M in 65-128
     with 192-384 workgroups, 32 x 32 tiles for 32-row blocks (n = 2048 at
-    M = 100; M = 40); ragged last row blocks, the XCD-paired tile order and
+    M = 100; M = 40), 128 x 48 tiles for wide N (12288; 9216 at K = 768,
+    three 256-K stages); ragged last row blocks, the XCD-paired tile order and
     (n = 3104: 194 workgroups) the plain order, UE8M0 and f32 scales, f32
     and bf16 outputs, against an f64 matmul of the dequantised operands.
     EXACT within 1e-3; NATIVE within its own 5e-2 (tests/test_gpu_native.py)."""

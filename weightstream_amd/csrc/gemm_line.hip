@@ -313,6 +313,9 @@ static int launch_line(const uint8_t *a, const void *sa, const uint8_t *b, const
         case 0: return launch_line_cfg<64, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
         // 32 x 32 tiles (four row blocks per column block on one XCD), 3 stages
         case 2: return launch_line_cfg<32, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
+        // 128 x 48 tiles (two 64-row halves x two K sub-steps of 256-K
+        // stages), 3 stages: wide N (M=128, N=12288)
+        case 4: return launch_line_cfg<128, 48, 2, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
         default: return -1;
     }
 }
