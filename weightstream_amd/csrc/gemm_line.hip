@@ -180,11 +180,12 @@ __global__ __launch_bounds__(256) void gemm_line_kernel(const uint8_t *A, const 
 #pragma unroll
         for (int j = 0; j < NJ; j++) acc[f][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    // f32 scales: acc += P * (sa[row] * sb) once per 128-K step
+    // f32 scales: acc += P * (sa[row] * sb) once per 128-K step, one fused
+    // multiply-add (the GEMM tolerance covers the accumulation order anyway)
     auto scale_add = [&](v4f &a, const v4f &p, const Raw &x, int f, int j) {
         const float sbf = __uint_as_float(x.sb[j]);
 #pragma unroll
-        for (int v = 0; v < 4; v++) a[v] = a[v] + p[v] * (__uint_as_float(x.sa[f][v]) * sbf);
+        for (int v = 0; v < 4; v++) a[v] = __builtin_fmaf(p[v], __uint_as_float(x.sa[f][v]) * sbf, a[v]);
     };
     auto math = [&](const Raw &x) {
         if (EXACT) {
