@@ -245,6 +245,117 @@ __host__ __device__ constexpr size_t g_tile_lds(int rows, int K) {
     return g_a_lds(rows, K) + ((size_t)rows * (K / 32) + 255) / 256 * 256;
 }
 
+// The A block as exact bf16 (the e4m3 bytes times their UE8M0 scales, each
+// value converted once when the block is staged instead of once per weight
+// band that meets it): abf[rows][K] with a row pitch of 2K + 16 bytes (the
+// pad spreads an MFMA fragment's 16 rows over the LDS banks).
+__host__ __device__ constexpr size_t g_abf_lds(int rows, int K) {
+    return (size_t)rows * (2 * K + 16);
+}
+// K bound of the bf16 block: 32 rows of it fit the 160 KB of LDS
+constexpr int kAbfMaxK = 2304;
+
+// Stage `rows` A rows (FP8 + UE8M0 per 1x32) into abf. Thread t converts
+// 16-byte pieces t, t + kGThreads, ...: four pieces' loads are issued before
+// their conversions. Row i of A starts at arow(i), its scales at srow(i).
+// The caller orders the LDS writes before the reads with a barrier.
+template <class ARow, class SRow>
+__device__ __forceinline__ void g_stage_abf(ARow arow, SRow srow, int rows, int K, int t,
+                                            uint8_t *abf) {
+    const int per_row = K / 16, n = rows * per_row, pitch = 2 * K + 16;
+    for (int i0 = t; i0 < n; i0 += 4 * kGThreads) {
+        uint4 q[4];
+        uint32_t sb[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = min(i0 + j * kGThreads, n - 1);
+            const int row = i / per_row, c = i - row * per_row;
+            q[j] = *(const uint4 *)(arow(row) + c * 16);
+            sb[j] = srow(row)[c >> 1];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int i = i0 + j * kGThreads;
+            if (i >= n) break;
+            const int row = i / per_row, c = i - row * per_row;
+            const float sc = e8m0_to_f32(sb[j]);
+            const uint32_t wq[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+            u32x4v o[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                o[h] = pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wq[2 * h], sc, false),
+                           __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wq[2 * h], sc, true),
+                           __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wq[2 * h + 1], sc, false),
+                           __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(wq[2 * h + 1], sc, true));
+            u32x4v *dst = (u32x4v *)(abf + (size_t)row * pitch + c * 32);
+            dst[0] = o[0];
+            dst[1] = o[1];
+        }
+    }
+}
+
+// g_compute2 (EXACT) against a bf16 A block: the same MFMAs in the same
+// order on the same bf16 operands, so the same sums bit for bit.
+template <int NF>
+__device__ __forceinline__ void g_compute2_abf(const Fp4Stage &s0, const Fp4Stage &s1,
+                                               v4f acc[2][2], const uint8_t *abf, int K, int ks0,
+                                               int kend, int lane) {
+    const int r = lane & 15, g = lane >> 4, pitch = 2 * K + 16;
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        const int ks = ks0 + u;
+        if (ks >= kend) continue;  // uniform
+        const float f0 = e8m0_to_f32(stage_scale(s0, u)), f1 = e8m0_to_f32(stage_scale(s1, u));
+        const uint32_t q0[4] = {s0.w[u].x, s0.w[u].y, s0.w[u].z, s0.w[u].w};
+        const uint32_t q1[4] = {s1.w[u].x, s1.w[u].y, s1.w[u].z, s1.w[u].w};
+        v8bf a[NF][4];
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const v8bf *ap = (const v8bf *)(abf + (size_t)(i * 16 + r) * pitch + ks * 256 + g * 64);
+#pragma unroll
+            for (int j = 0; j < 4; j++) a[i][j] = ap[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const v8bf b0 = __builtin_bit_cast(
+                v8bf, pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 0),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 1),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 2),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q0[j], f0, 3)));
+            const v8bf b1 = __builtin_bit_cast(
+                v8bf, pk4(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 0),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 1),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 2),
+                          __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q1[j], f1, 3)));
+#pragma unroll
+            for (int i = 0; i < NF; i++) {
+                acc[0][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][j], b0, acc[0][i], 0, 0, 0);
+                acc[1][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i][j], b1, acc[1][i], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// g_compute (EXACT) against a bf16 A block, the same sums bit for bit.
+template <int NF>
+__device__ __forceinline__ void g_compute_abf(const Fp4Stage &st, v4f acc[NF], const uint8_t *abf,
+                                              int K, int ks0, int kend, int lane) {
+    const int r = lane & 15, g = lane >> 4, pitch = 2 * K + 16;
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+        const int ks = ks0 + u;
+        if (ks >= kend) continue;  // uniform
+        v8bf bq[4];
+        cvt_fp4x32(st.w[u], e8m0_to_f32(stage_scale(st, u)), bq);
+#pragma unroll
+        for (int i = 0; i < NF; i++) {
+            const v8bf *ap = (const v8bf *)(abf + (size_t)(i * 16 + r) * pitch + ks * 256 + g * 64);
+            const v8bf aq[4] = {ap[0], ap[1], ap[2], ap[3]};
+            acc[i] = mfma_bf16_k128(aq, bq, acc[i]);
+        }
+    }
+}
+
 // Steps [ks0, kend) (at most kU) of a band, held in one stage, times the NF
 // 16-slot A fragments in LDS (row stride K + 16 bytes, scales
 // as_l[slot][K/32]). D[m][n]: slot 4*(lane/16)+v of fragment i, band row
@@ -613,7 +724,9 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 // slot rows. num_tiles == nullptr: the used tiles are counted from
 // tile_expert (the dispatch puts them first, the rest hold -1), as a caller
 // of the reference's grouped GEMM passes no count.
-template <bool EXACT, int CB, bool GATHER = false>
+// ABF (EXACT, inter <= kAbfMaxK): the A block is staged as bf16 (g_stage_abf)
+// and the waves convert only their weights.
+template <bool EXACT, int CB, bool GATHER = false, bool ABF = false>
 __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
     const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ exp_off,
@@ -621,8 +734,10 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
     int dim, int inter, int n_experts, int tiles, int top_k, int tokens) {
     extern __shared__ __align__(16) uint8_t g_lds[];
-    uint8_t *a_l = g_lds;                                // [32][inter + 16]
+    static_assert(!ABF || EXACT, "the bf16 A block serves the exact math");
+    uint8_t *a_l = g_lds;                                // [32][inter + 16] (ABF: abf)
     uint8_t *as_l = g_lds + g_a_lds(kTile, inter);      // [32][inter/32] (+ padding)
+    __shared__ int row_l[kTile];                         // ABF: the A row of each slot
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int r = lane & 15, g = lane >> 4;
     ChunkStream cs;
@@ -686,8 +801,13 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
                     real = (uint32_t)__ballot(has);
                     if (GATHER) my_row = has ? min(route / top_k, tokens - 1) : 0;
                 }
+                if (ABF && w == 0 && lane < kTile) row_l[lane] = GATHER ? my_row : slot0 + lane;
                 lds_barrier();       // every wave is done with the previous tile
-                if (GATHER)
+                if (ABF)
+                    g_stage_abf([&](int i) { return hq + (size_t)row_l[i] * inter; },
+                                [&](int i) { return hs + (size_t)row_l[i] * (inter / 32); },
+                                (real >> 16) == 0 ? 16 : kTile, inter, t, a_l);
+                else if (GATHER)
                     g_dma_tile([&](int i) { return hq + (size_t)__shfl(my_row, i, 64) * inter; },
                                [&](int i) {
                                    return hs + (size_t)__shfl(my_row, i, 64) * (inter / 32);
@@ -697,7 +817,7 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
                     g_dma_tile([&](int i) { return hq + (size_t)(slot0 + i) * inter; },
                                [&](int i) { return hs + (size_t)(slot0 + i) * (inter / 32); },
                                (real >> 16) == 0 ? 16 : kTile, inter, w, lane, a_l, as_l);
-                __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
+                if (!ABF) __builtin_amdgcn_s_waitcnt(0);  // this wave's copies have landed
                 lds_barrier();
                 cur_tile = tile;
             }
@@ -705,7 +825,17 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
             for (int h = 0; h < 2; h++) acc[h][0] = acc[h][1] = v4f{0.f, 0.f, 0.f, 0.f};
         }
         const bool lo16 = (real >> 16) == 0;  // uniform
-        if (CB == 2) {
+        if (ABF && CB == 2) {
+            if (lo16)
+                g_compute2_abf<1>(st.h[0], st.h[1], acc, a_l, inter, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute2_abf<2>(st.h[0], st.h[1], acc, a_l, inter, cs.cb(q), cs.ce(q), lane);
+        } else if (ABF) {
+            if (lo16)
+                g_compute_abf<1>(st.h[0], acc[0], a_l, inter, cs.cb(q), cs.ce(q), lane);
+            else
+                g_compute_abf<2>(st.h[0], acc[0], a_l, inter, cs.cb(q), cs.ce(q), lane);
+        } else if (CB == 2) {
             if (lo16)
                 g_compute2<EXACT, 1>(st.h[0], st.h[1], acc, a_l, as_l, inter, cs.cb(q), cs.ce(q), lane);
             else
@@ -959,20 +1089,24 @@ static int grouped_gemm_launch(const uint8_t *hq, const uint8_t *hs, const int32
                                const uint8_t *s2, float *out, int64_t dim, int64_t inter,
                                int64_t n_experts, int64_t tiles, bool gather, int64_t top_k,
                                int64_t tokens, ws_stream_t stream) {
-    const size_t lds = g_tile_lds(kTile, (int)inter);
+    const bool abf = math_mode() == WS_MATH_EXACT && inter <= kAbfMaxK;
+    const size_t lds = abf ? g_abf_lds(kTile, (int)inter) : g_tile_lds(kTile, (int)inter);
     dim3 grid((unsigned)cu_count());
-#define WS_DOWN(E, CB, G)                                                                      \
-    hipLaunchKernelGGL((grouped_down_kernel<E, CB, G>), grid, dim3(kGThreads), lds, stream, hq,  \
-                       hs, tile_expert, num_tiles, exp_off, exp_cnt, order, w2, s2, out,        \
+#define WS_DOWN(E, CB, G, A)                                                                   \
+    hipLaunchKernelGGL((grouped_down_kernel<E, CB, G, A>), grid, dim3(kGThreads), lds, stream,  \
+                       hq, hs, tile_expert, num_tiles, exp_off, exp_cnt, order, w2, s2, out,    \
                        (int)dim, (int)inter,                                                    \
                        (int)n_experts, (int)tiles, (int)top_k, (int)tokens)
     const bool wide = wide_units(tiles);
-    if (math_mode() == WS_MATH_EXACT) {
-        if (gather) { if (wide) WS_DOWN(true, 2, true); else WS_DOWN(true, 1, true); }
-        else if (wide) WS_DOWN(true, 2, false); else WS_DOWN(true, 1, false);
+    if (abf) {
+        if (gather) { if (wide) WS_DOWN(true, 2, true, true); else WS_DOWN(true, 1, true, true); }
+        else if (wide) WS_DOWN(true, 2, false, true); else WS_DOWN(true, 1, false, true);
+    } else if (math_mode() == WS_MATH_EXACT) {
+        if (gather) { if (wide) WS_DOWN(true, 2, true, false); else WS_DOWN(true, 1, true, false); }
+        else if (wide) WS_DOWN(true, 2, false, false); else WS_DOWN(true, 1, false, false);
     } else {
-        if (gather) { if (wide) WS_DOWN(false, 2, true); else WS_DOWN(false, 1, true); }
-        else if (wide) WS_DOWN(false, 2, false); else WS_DOWN(false, 1, false);
+        if (gather) { if (wide) WS_DOWN(false, 2, true, false); else WS_DOWN(false, 1, true, false); }
+        else if (wide) WS_DOWN(false, 2, false, false); else WS_DOWN(false, 1, false, false);
     }
 #undef WS_DOWN
     return launch_status();
