@@ -29,6 +29,14 @@ constexpr int kDispThreads = 1024;
 constexpr int kMaxExpertsG = 1024;
 constexpr int kTile = 32;
 constexpr int kDispHeld = 4;  // route chunks the dispatch keeps in registers
+constexpr int kEsGroup = 2;   // tiles of one expert whose weights the stationary body streams once
+
+// The expert-stationary body streams a group's weights once for its (up to
+// kEsGroup) tiles; it pays when at least a sixth of the nt tiles share a group
+// with another (ng groups; skewed routing: measured 247 against 258 us at
+// M=132 under Zipf(1.1)). With (nearly) one tile per expert the
+// tile-streaming body is faster.
+__host__ __device__ constexpr bool es_pays(int nt, int ng) { return 6 * (nt - ng) >= nt; }
 
 // ---- dispatch (one workgroup) -------------------------------------------
 // An expert id as the dispatch sees it: ids outside [0, E) (a pick another
@@ -47,11 +55,13 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     int32_t *__restrict__ tile_expert, int32_t *__restrict__ count_out,
     int32_t *__restrict__ offset_out, int32_t *__restrict__ psum_out,
     int32_t *__restrict__ num_tiles_out, int routes, int tiles, int n_experts,
-    const float *__restrict__ xf, uint8_t *__restrict__ xq, uint8_t *__restrict__ xs, int64_t nx) {
+    const float *__restrict__ xf, uint8_t *__restrict__ xq, uint8_t *__restrict__ xs, int64_t nx,
+    uint16_t *__restrict__ xbf, int32_t *__restrict__ select_out) {
     if (blockIdx.x > 0) {
         // workgroups 1..: the tokens' FP8 1x32 quantisation (the act_quant
         // rule, a 32-lane half-wave per block; nx % 32 == 0), independent of
-        // the dispatch and run beside it in the same launch
+        // the dispatch and run beside it in the same launch; with xbf also
+        // the exact bf16 of each quantised value (byte times block scale)
         const int64_t i = (int64_t)(blockIdx.x - 1) * kDispThreads + threadIdx.x;
         const bool live = i < nx;
         uint32_t sb;
@@ -59,6 +69,9 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
         if (live) {
             xq[i] = (uint8_t)qb;
             if ((threadIdx.x & 31) == 0) xs[i / 32] = (uint8_t)sb;
+            if (xbf)
+                xbf[i] = (uint16_t)__builtin_bit_cast(
+                    uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(qb, e8m0_to_f32(sb), false));
         }
         return;
     }
@@ -66,6 +79,7 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     __shared__ int32_t wcnt[kDispThreads / 64][kMaxExpertsG];
     __shared__ int32_t scan[kMaxExpertsG];
     __shared__ int32_t wsum[kDispThreads / 64];
+    __shared__ int32_t gsum[kDispThreads / 64];
     const int t = threadIdx.x, w = t >> 6, lane = t & 63;
     base[t] = 0;
     // the first kDispHeld chunks of routes are loaded once, up front (one
@@ -149,6 +163,18 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
         psum_out[t] = offset + count;
     }
     if (t == 0) *num_tiles_out = used;
+    if (select_out) {  // the prefill's choice of body (es_pays over the used tiles)
+        int g = (padded / kTile + kEsGroup - 1) / kEsGroup;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) g += __shfl_xor(g, off, 64);
+        if (lane == 0) gsum[w] = g;
+        __syncthreads();
+        if (t == 0) {
+            int ng = 0;
+            for (int ww = 0; ww < kDispThreads / 64; ww++) ng += gsum[ww];
+            *select_out = es_pays(used, ng) ? 1 : 0;
+        }
+    }
     __syncthreads();
     // every used slot starts as padding (coalesced stores); pass 2
     // overwrites the slots that hold routes, after the barrier (which waits
@@ -559,17 +585,33 @@ struct ChunkStream {
 // The K parts meet in LDS (gu: part 0 stores, part 1 adds); then a half-wave
 // per (slot row, 32-column block) applies SwiGLU, the routing weight and the
 // FP8 1x32 quantisation (one block = 32 columns).
+struct GluArgs {
+    const uint8_t *xq, *xs;
+    const int32_t *order;
+    const float *layout_w;
+    const int32_t *tile_expert, *num_tiles, *exp_off, *exp_cnt;
+    const uint8_t *w1, *s1, *w3, *s3;
+    uint8_t *hq, *hs;
+    int dim, inter, n_experts, top_k;
+    float limit;
+};
+
 template <bool EXACT, int ROWS, int CB>
-__global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
-    const uint8_t *xq, const uint8_t *xs, const int32_t *__restrict__ order,
-    const float *__restrict__ layout_w, const int32_t *__restrict__ tile_expert,
-    const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ exp_off,
-    const int32_t *__restrict__ exp_cnt, const uint8_t *__restrict__ w1,
-    const uint8_t *__restrict__ s1, const uint8_t *__restrict__ w3,
-    const uint8_t *__restrict__ s3, uint8_t *__restrict__ hq, uint8_t *__restrict__ hs, int dim,
-    int inter, int n_experts, int top_k, float limit) {
+__device__ __forceinline__ void grouped_glu_body(const GluArgs &ga, uint8_t *g_lds) {
+    const uint8_t *xq = ga.xq, *xs = ga.xs;
+    const int32_t *__restrict__ order = ga.order;
+    const float *__restrict__ layout_w = ga.layout_w;
+    const int32_t *__restrict__ tile_expert = ga.tile_expert;
+    const int32_t *__restrict__ num_tiles = ga.num_tiles;
+    const int32_t *__restrict__ exp_off = ga.exp_off;
+    const int32_t *__restrict__ exp_cnt = ga.exp_cnt;
+    const uint8_t *__restrict__ w1 = ga.w1, *__restrict__ s1 = ga.s1;
+    const uint8_t *__restrict__ w3 = ga.w3, *__restrict__ s3 = ga.s3;
+    uint8_t *__restrict__ hq = ga.hq;
+    uint8_t *__restrict__ hs = ga.hs;
+    const int dim = ga.dim, inter = ga.inter, n_experts = ga.n_experts, top_k = ga.top_k;
+    const float limit = ga.limit;
     constexpr int NF = ROWS / 16, H = kTile / ROWS;
-    extern __shared__ __align__(16) uint8_t g_lds[];
     uint8_t *a_l = g_lds;                              // [ROWS][dim + 16]
     uint8_t *as_l = g_lds + g_a_lds(ROWS, dim);        // [ROWS][dim/32] (+ padding)
     constexpr int UC = kGCols * CB;                   // columns per unit
@@ -711,6 +753,12 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
     if (q < cs.total) step(st0, q);
 }
 
+template <bool EXACT, int ROWS, int CB>
+__global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(GluArgs ga) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    grouped_glu_body<EXACT, ROWS, CB>(ga, g_lds);
+}
+
 // ---- grouped down ---------------------------------------------------------
 // Unit = (tile, 128 * CB output columns nt); wave w owns the CB 16-column
 // bands from nt*128*CB + 16*CB*w over the whole K = inter (chunk stream of
@@ -726,14 +774,26 @@ __global__ __launch_bounds__(kGThreads) void grouped_glu_quant_kernel(
 // of the reference's grouped GEMM passes no count.
 // ABF (EXACT, inter <= kAbfMaxK): the A block is staged as bf16 (g_stage_abf)
 // and the waves convert only their weights.
+struct DownArgs {
+    const uint8_t *hq, *hs;
+    const int32_t *tile_expert, *num_tiles, *exp_off, *exp_cnt, *order;
+    const uint8_t *w2, *s2;
+    float *out;
+    int dim, inter, n_experts, tiles, top_k, tokens;
+};
+
 template <bool EXACT, int CB, bool GATHER = false, bool ABF = false>
-__global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
-    const uint8_t *hq, const uint8_t *hs, const int32_t *__restrict__ tile_expert,
-    const int32_t *__restrict__ num_tiles, const int32_t *__restrict__ exp_off,
-    const int32_t *__restrict__ exp_cnt, const int32_t *__restrict__ order,
-    const uint8_t *__restrict__ w2, const uint8_t *__restrict__ s2, float *__restrict__ out,
-    int dim, int inter, int n_experts, int tiles, int top_k, int tokens) {
-    extern __shared__ __align__(16) uint8_t g_lds[];
+__device__ __forceinline__ void grouped_down_body(const DownArgs &da, uint8_t *g_lds) {
+    const uint8_t *hq = da.hq, *hs = da.hs;
+    const int32_t *__restrict__ tile_expert = da.tile_expert;
+    const int32_t *__restrict__ num_tiles = da.num_tiles;
+    const int32_t *__restrict__ exp_off = da.exp_off;
+    const int32_t *__restrict__ exp_cnt = da.exp_cnt;
+    const int32_t *__restrict__ order = da.order;
+    const uint8_t *__restrict__ w2 = da.w2, *__restrict__ s2 = da.s2;
+    float *__restrict__ out = da.out;
+    const int dim = da.dim, inter = da.inter, n_experts = da.n_experts, tiles = da.tiles,
+              top_k = da.top_k, tokens = da.tokens;
     static_assert(!ABF || EXACT, "the bf16 A block serves the exact math");
     uint8_t *a_l = g_lds;                                // [32][inter + 16] (ABF: abf)
     uint8_t *as_l = g_lds + g_a_lds(kTile, inter);      // [32][inter/32] (+ padding)
@@ -870,6 +930,575 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(
     if (q < cs.total) step(s0, q);
 }
 
+template <bool EXACT, int CB, bool GATHER = false, bool ABF = false>
+__global__ __launch_bounds__(kGThreads) void grouped_down_kernel(DownArgs da) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    grouped_down_body<EXACT, CB, GATHER, ABF>(da, g_lds);
+}
+
+// ---- expert-stationary grouped GEMM (exact math, ws_moe_prefill) --------
+// The tile-streaming kernels above read an expert's weights once per tile.
+// Here a workgroup takes a unit = (group, column block): a group is a run of
+// up to kTG consecutive tiles of one expert, and every weight byte of the
+// column block is loaded and converted once and multiplied into all the
+// group's tiles. The A rows arrive as exact bf16 (the e4m3 bytes times their
+// UE8M0 scales, written once by the step before) through direct global->LDS
+// loads into a ring of kRing 128-K steps, so the waves convert only weights.
+// Four waves, one per SIMD (512 registers each); wave w owns four 16-row
+// bands over the whole K: gate/up the w1 and the w3 bands of intermediate
+// columns 32w .. 32w + 31 of the block (SwiGLU pairs and whole FP8 blocks in
+// one wave's registers), down output columns 64w .. 64w + 63. The
+// workgroup's steps form one stream across its units: the loads of step
+// q + kAhead are issued while step q is multiplied, with one workgroup
+// barrier per step (ring slot (q - 1) % kRing is free once every wave is
+// past it). Every step issues the same number of loads (the tiles a group
+// lacks get a 4-byte stand-in copy), so one fixed count (vmcnt) says when a
+// step's copies have landed. Every global access goes through a buffer
+// descriptor sized to its array (out-of-range reads return zeros, writes are
+// dropped). Units go out sorted by group size and dealt to the workgroups in
+// snake order, which evens out the work per workgroup.
+namespace es {
+constexpr int kTG = kEsGroup;                        // tiles per group
+constexpr int kRing = 8;                      // ring slots (LDS and registers), one 128-K step each
+constexpr int kRowB = 256;                    // bytes of one A row per step (128 bf16)
+constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
+constexpr int kMaxGroups = 1024;
+constexpr int kThreads = 512;                 // 8 waves: two per SIMD
+static_assert(kThreads == kGThreads, "the select kernels run both bodies in one workgroup");
+constexpr int kStepLoads = 4 + kTG;           // loads per step and wave: weights + copies
+constexpr size_t kLds = (size_t)kRing * kSlotB;
+constexpr size_t kLdsAll = kLds + 2 * kMaxGroups * sizeof(int);  // ring + group table
+}  // namespace es
+
+typedef __amdgpu_buffer_rsrc_t es_rsrc;
+// raw buffer of `bytes` bytes at p (gfx9 descriptor word 3)
+__device__ __forceinline__ es_rsrc es_buf(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
+                                             (int)(uint32_t)min(bytes, (size_t)0xFFFFFFFFu),
+                                             0x00020000);
+}
+__device__ __forceinline__ void es_dma(es_rsrc r, uint32_t off, uint32_t lds, int bytes) {
+    auto *l = (__attribute__((address_space(3))) void *)(uintptr_t)lds;
+    if (bytes == 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 16, off, 0, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(r, l, 4, off, 0, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void es_vmcnt() {
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// s_waitcnt vmcnt(n) for a run-time n in [LO, HI]
+template <int LO, int HI>
+__device__ __forceinline__ void es_wait_vm(int n) {
+    if constexpr (LO == HI) {
+        es_vmcnt<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n <= MID) es_wait_vm<LO, MID>(n);
+        else es_wait_vm<MID + 1, HI>(n);
+    }
+}
+// Loads through the scalar cache into SGPRs (uniform address; nothing in this
+// launch writes the data), complete when the statement ends; they count in
+// lgkmcnt, not in the vmcnt of the stream.
+typedef int es_i4 __attribute__((ext_vector_type(4)));
+typedef float es_f16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ int es_sload1(const int32_t *p) {
+    int v;
+    __asm__ volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ es_i4 es_sload4(const int32_t *p) {
+    es_i4 v;
+    __asm__ volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ es_f16 es_sload16(const float *p) {
+    es_f16 v;
+    __asm__ volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+    return v;
+}
+// four 16-byte loads, one round trip
+__device__ __forceinline__ void es_sload4x4(const int32_t *p0, const int32_t *p1, const int32_t *p2,
+                                            const int32_t *p3, es_i4 o[4]) {
+    __asm__ volatile(
+        "s_load_dwordx4 %0, %4, 0x0\n\ts_load_dwordx4 %1, %5, 0x0\n\t"
+        "s_load_dwordx4 %2, %6, 0x0\n\ts_load_dwordx4 %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
+        : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
+        : "s"(p0), "s"(p1), "s"(p2), "s"(p3)
+        : "memory");
+}
+// 32 consecutive floats (two 64-byte loads), one round trip
+__device__ __forceinline__ void es_sload32(const float *p, es_f16 o[2]) {
+    __asm__ volatile(
+        "s_load_dwordx16 %0, %2, 0x0\n\ts_load_dwordx16 %1, %2, 0x40\n\ts_waitcnt lgkmcnt(0)"
+        : "=&s"(o[0]), "=&s"(o[1])
+        : "s"(p)
+        : "memory");
+}
+// An LDS word, complete when the statement ends (no ordinary LDS access, so
+// the compiler does not wait for the stream's direct-to-LDS copies).
+__device__ __forceinline__ int es_lds_word(const int *p) {
+    int v;
+    __asm__ volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+// One 16-row A fragment of one tile and step, 4 x 16 bytes: reads at a[jj]
+// + OFF, complete when the statement ends.
+template <int OFF>
+__device__ __forceinline__ void es_lds_frag(const uint32_t a[4], u32x4v o[4]) {
+    __asm__ volatile(
+        "ds_read_b128 %0, %4 offset:%8\n\tds_read_b128 %1, %5 offset:%8\n\t"
+        "ds_read_b128 %2, %6 offset:%8\n\tds_read_b128 %3, %7 offset:%8\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "n"(OFF)
+        : "memory");
+}
+
+struct EsArgs {
+    const uint8_t *abf;        // A rows, bf16: gate/up xbf [a_rows][K], down hbf [a_rows][K]
+    const int32_t *order;      // [slots] route index or -1
+    const float *layout_w;     // [slots] routing weight
+    const int32_t *tile_expert, *num_tiles, *exp_off, *exp_cnt;
+    const uint8_t *wa, *sa, *wb, *sb;  // gate/up: w1 | s1, w3 | s3; down: w2 | s2 (wb unused)
+    uint8_t *hbf;              // gate/up out: bf16 h [slots][N]
+    float *out;                // down out: f32 [slots][N]
+    int K, N, n_experts, top_k, a_rows, slots;
+    float limit;
+};
+
+struct EsStep {  // one wave's weight loads of one step: two bands
+    u32x4v q[2];
+    uint32_t s[2];
+};
+// an LDS word written / read, complete when the statement ends (no ordinary
+// LDS access, so the compiler adds no wait for the stream's LDS copies)
+__device__ __forceinline__ void es_lds_put(float *p, float v) {
+    __asm__ volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(lds_addr(p)), "v"(v) : "memory");
+}
+__device__ __forceinline__ float es_lds_getf(const float *p) {
+    float v;
+    __asm__ volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
+    return v;
+}
+// eight LDS words at p + 4 k (byte offsets 0, 4, ..., 28 from a) written;
+// complete when the statement ends
+__device__ __forceinline__ void es_lds_put8(uint32_t a, const float v[8]) {
+    __asm__ volatile(
+        "ds_write_b32 %0, %1\n\tds_write_b32 %0, %2 offset:4\n\tds_write_b32 %0, %3 offset:8\n\t"
+        "ds_write_b32 %0, %4 offset:12\n\tds_write_b32 %0, %5 offset:16\n\t"
+        "ds_write_b32 %0, %6 offset:20\n\tds_write_b32 %0, %7 offset:24\n\t"
+        "ds_write_b32 %0, %8 offset:28\n\ts_waitcnt lgkmcnt(0)"
+        :
+        : "v"(a), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]),
+          "v"(v[7])
+        : "memory");
+}
+// eight LDS words at a (byte offsets 0, 4, ..., 28) read; complete when the
+// statement ends
+__device__ __forceinline__ void es_lds_get8(uint32_t a, float v[8]) {
+    __asm__ volatile(
+        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:4\n\tds_read_b32 %2, %8 offset:8\n\t"
+        "ds_read_b32 %3, %8 offset:12\n\tds_read_b32 %4, %8 offset:16\n\t"
+        "ds_read_b32 %5, %8 offset:20\n\tds_read_b32 %6, %8 offset:24\n\t"
+        "ds_read_b32 %7, %8 offset:28\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+          "=&v"(v[6]), "=&v"(v[7])
+        : "v"(a)
+        : "memory");
+}
+
+// one of four wave-uniform values by a per-lane index 0..3 (selects, no
+// indexed private array)
+__device__ __forceinline__ float es_pick4(int g, float a, float b, float c, float d) {
+    const float lo = (g & 1) ? b : a, hi = (g & 1) ? d : c;
+    return (g & 2) ? hi : lo;
+}
+
+// MODE 0: gate/up + SwiGLU + routing weight + FP8 1x32 re-quantisation of h,
+// written as the exact bf16 of the quantised values (the down step's A).
+// MODE 1: down, f32 out for the slots that hold routes.
+template <int MODE>
+__device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
+    using namespace es;
+    constexpr int kAhead = MODE == 0 ? 5 : 7;  // steps issued ahead of the one multiplied
+    constexpr int NW = kThreads / 64;
+    // g_lds: the A ring (kLds bytes), then the group table
+    int *grp_l = (int *)(g_lds + kLds);   // [kMaxGroups] tile | T << 16 | expert << 19
+    int *nrl_l = grp_l + kMaxGroups;      // [kMaxGroups] slots with routes of tile j: byte j
+    __shared__ int cnt_l[NW][kTG + 1];
+    __shared__ float am_l[NW][kTG * kTile];          // gate/up: per-row maxima of a wave's 16 columns
+    const int t = threadIdx.x, lane = t & 63;
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int NS = a.K / 128;                            // steps per unit
+    const int NCG = MODE == 0 ? a.N / 128 : a.N / 256;  // column blocks per group
+    const int nt = min(*a.num_tiles, min(kMaxGroups, a.slots / kTile));
+
+    // ---- the groups, sorted by size (largest first), then by tile
+    constexpr int PL = kMaxGroups / kThreads;  // tiles per lane
+    int gk[PL], gt[PL], gn[PL];
+#pragma unroll
+    for (int h = 0; h < PL; h++) {
+        const int tt = (w * PL + h) * 64 + lane;
+        gk[h] = -1;
+        gt[h] = gn[h] = 0;
+        if (tt < nt) {
+            const int e = g_expert(a.tile_expert, tt, a.n_experts);
+            const int off = a.exp_off[e], cnt = a.exp_cnt[e];
+            const int rel = tt - off / kTile;
+            const int ntile = (cnt + kTile - 1) / kTile;
+            if (rel >= 0 && rel % kTG == 0) {
+                gt[h] = max(1, min(kTG, min(ntile - rel, nt - tt)));
+                gk[h] = tt | (gt[h] << 16) | (e << 19);
+                // an expert's routes fill its slots in order from its offset
+#pragma unroll
+                for (int j = 0; j < kTG; j++)
+                    gn[h] |= min(max(cnt - ((tt + j) * kTile - off), 0), kTile) << (8 * j);
+            }
+        }
+    }
+    uint64_t bal[PL][kTG + 1];
+#pragma unroll
+    for (int T = 1; T <= kTG; T++) {
+        int c = 0;
+#pragma unroll
+        for (int h = 0; h < PL; h++) {
+            bal[h][T] = __ballot(gt[h] == T);
+            c += __popcll(bal[h][T]);
+        }
+        if (lane == 0) cnt_l[w][T] = c;
+    }
+    lds_barrier();
+    int cls = 0, mine[kTG + 1];
+#pragma unroll
+    for (int T = kTG; T >= 1; T--) {  // classes in size order, waves in order within one
+        int off = cls;
+        for (int ww = 0; ww < NW; ww++) {
+            if (ww == w) mine[T] = off;
+            off += cnt_l[ww][T];
+        }
+        cls = off;
+    }
+    const int ng = cls;
+    const uint64_t below = (1ull << lane) - 1;
+#pragma unroll
+    for (int T = 1; T <= kTG; T++) {
+        int pos = mine[T];
+#pragma unroll
+        for (int h = 0; h < PL; h++) {
+            if (gt[h] == T) {
+                grp_l[pos + __popcll(bal[h][T] & below)] = gk[h];
+                nrl_l[pos + __popcll(bal[h][T] & below)] = gn[h];
+            }
+            pos += __popcll(bal[h][T]);
+        }
+    }
+    lds_barrier();
+
+    // ---- this workgroup's units: unit k of the sorted order goes to round
+    // k / G, workgroup k % G in even rounds and G - 1 - k % G in odd ones
+    const int G = gridDim.x, b = blockIdx.x;
+    const int U = ng * NCG;
+    auto unit_k = [&](int ri) { return ri * G + ((ri & 1) ? G - 1 - b : b); };
+    const int n_units = U / G + (unit_k(U / G) < U ? 1 : 0);
+    if (n_units == 0) return;  // whole workgroup
+    const int total = n_units * NS;
+    const size_t wmat = (size_t)a.N * (a.K / 2);
+    const size_t smat = (size_t)packed_fp4_scale_bytes(a.N, a.K);
+    const uint32_t ring = lds_addr(g_lds);
+    const es_rsrc abuf = es_buf(a.abf, (size_t)a.a_rows * a.K * 2);
+
+    // ---- issue side: the unit whose steps are being loaded
+    int ri_i = 0, s_i = 0, Ti = 1;
+    es_rsrc wr[2], sr[2];     // the unit's expert matrices (gate/up: w1, w3; down: w2)
+    uint32_t bo[2], so[2];    // this lane's byte offsets of step 0 per band (weights, scales)
+    uint32_t ao[kTG];         // this lane's A row offset per tile (rows 4w .. 4w + 3)
+    auto open_issue = [&]() {
+        const int k = unit_k(ri_i);
+        const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
+        const int cg = k % NCG, t0 = v & 0xFFFF, e = v >> 19;
+        Ti = (v >> 16) & 7;
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            wr[m] = es_buf((m == 0 || MODE == 1 ? a.wa : a.wb) + (size_t)e * wmat, wmat);
+            sr[m] = es_buf((m == 0 || MODE == 1 ? a.sa : a.sb) + (size_t)e * smat, smat);
+        }
+        const int ks8 = (NS + 7) / 8;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int rt = MODE == 0 ? cg * 8 + w : cg * 16 + 2 * w + h;
+            bo[h] = (uint32_t)(((size_t)rt * NS * 64 + lane) * 16);
+            so[h] = (uint32_t)(((size_t)rt * ks8 * 64 + lane) * 8);
+        }
+        // row 4w + g of each tile; a row's 16-byte pieces are stored
+        // XOR-permuted by the row (bank spread)
+        const int row = 4 * w + g;
+        es_i4 o[2];
+        if (MODE == 0) {
+            es_i4 o4[4];
+            const int32_t *o0 = a.order + (size_t)t0 * kTile + 4 * w;
+            const int32_t *o1 = a.order + (size_t)(t0 + min(1, Ti - 1)) * kTile + 4 * w;
+            es_sload4x4(o0, o0, o1, o1, o4);
+            o[0] = o4[0];
+            o[1] = o4[2];
+        }
+        static_assert(kTG == 2, "two tiles per group");
+#pragma unroll
+        for (int j = 0; j < kTG; j++) {
+            const int tj = t0 + min(j, Ti - 1);
+            uint32_t arow;
+            if (MODE == 0) {
+                const es_i4 &oc = o[j];
+                const int lo = (g & 1) ? oc[1] : oc[0], hi = (g & 1) ? oc[3] : oc[2];
+                const int route = (g & 2) ? hi : lo;
+                arow = route >= 0 ? (uint32_t)(route / a.top_k) : 0u;
+            } else {
+                arow = (uint32_t)(tj * kTile + row);
+            }
+            ao[j] = arow * (uint32_t)a.K * 2u + ((r ^ (row & 15)) << 4);
+        }
+    };
+    // the loads of the next step of the stream (its unit opened) into
+    // register slot x and ring slot `slot`: kStepLoads per wave. Past the end
+    // of the stream (real == false) the last step's loads are repeated and
+    // not used, so that every step has the same loads in flight after it.
+    auto issue = [&](EsStep &x, int slot, bool real) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int m = MODE == 0 ? h : 0;
+            x.q[h] = __builtin_bit_cast(
+                u32x4v, __builtin_amdgcn_raw_buffer_load_b128(wr[m], bo[h] + (uint32_t)s_i * 1024u, 0, 0));
+            // the scale word holding this step's byte (byte s % 4, taken at use)
+            x.s[h] = __builtin_amdgcn_raw_buffer_load_b32(
+                sr[m], so[h] + (uint32_t)(s_i >> 3) * 512u + (uint32_t)(s_i & 4), 0, 0);
+        }
+        const uint32_t lb = ring + slot * kSlotB + 4 * w * kRowB;
+#pragma unroll
+        for (int j = 0; j < kTG; j++)
+            es_dma(abuf, ao[j] + (uint32_t)s_i * kRowB,  // tiles >= Ti: a valid row
+                   lb + j * kTile * kRowB, j < Ti ? 16 : 4);
+        if (real && ++s_i == NS) {
+            s_i = 0;
+            ri_i++;
+        }
+    };
+
+    // ---- compute side: the unit being multiplied
+    int ri_c = 0, s_c = 0, Tc = 1, t0c = 0, cgc = 0, lo16 = 0, nrc = 0;
+    auto open_compute = [&]() {
+        const int k = unit_k(ri_c);
+        const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
+        nrc = __builtin_amdgcn_readfirstlane(es_lds_word(&nrl_l[k / NCG]));
+        cgc = k % NCG;
+        t0c = v & 0xFFFF;
+        Tc = (v >> 16) & 7;
+        lo16 = 0;  // bit j: tile j's slots 16.. are padding
+#pragma unroll
+        for (int j = 0; j < kTG; j++)
+            if (((nrc >> (8 * j)) & 0xFF) <= 16) lo16 |= 1 << j;
+    };
+    v4f acc[kTG][2][2];  // [tile][band][16-row fragment]
+    const uint64_t tab = ws_lane_exp2f_tab(lane);
+
+    auto multiply = [&](const EsStep &x, uint32_t sbase) {
+        __asm__ volatile("" : "+s"(sbase));  // opaque: the slot's addresses are formed per step
+        if (s_c == 0) {
+#pragma unroll
+            for (int j = 0; j < kTG; j++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) acc[j][h][0] = acc[j][h][1] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+        v8bf bq[2][4];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            cvt_fp4x32(uint4{x.q[h][0], x.q[h][1], x.q[h][2], x.q[h][3]},
+                       e8m0_to_f32((x.s[h] >> (8 * (s_c & 3))) & 0xFF), bq[h]);
+#pragma unroll
+        for (int j = 0; j < kTG; j++) {
+            if (j >= Tc) continue;  // uniform
+            uint32_t ad[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+                ad[jj] = sbase + (j * kTile + r) * kRowB + (((4 * g + jj) ^ r) << 4);
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                if (i == 1 && ((lo16 >> j) & 1)) continue;  // uniform: rows 16.. are padding
+                u32x4v av[4];
+                if (i == 0) es_lds_frag<0>(ad, av);
+                else es_lds_frag<4096>(ad, av);
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const v8bf am = __builtin_bit_cast(v8bf, av[jj]);
+#pragma unroll
+                    for (int h = 0; h < 2; h++)
+                        acc[j][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bq[h][jj],
+                                                                               acc[j][h][i], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    const es_rsrc obuf = MODE == 0 ? es_buf(a.hbf, (size_t)a.slots * a.N * 2)
+                                   : es_buf(a.out, (size_t)a.slots * a.N * 4);
+    auto epilogue = [&]() {
+        if (MODE == 1) {
+            // f32 out of the slots that hold routes, straight from the
+            // accumulators (each tile unrolled)
+#pragma unroll
+            for (int j = 0; j < kTG; j++) {
+                if (j >= Tc) continue;  // uniform
+                const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
+                const int nr = (nrc >> (8 * j)) & 0xFF;
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int row = 16 * i + 4 * g + v;
+                        if (row >= nr) continue;
+#pragma unroll
+                        for (int h = 0; h < 2; h++)
+                            __builtin_amdgcn_raw_buffer_store_b32(
+                                __float_as_uint(acc[j][h][i][v]), obuf,
+                                (uint32_t)((slot0 + row) * a.N + cgc * 256 + 32 * w + 16 * h + r) * 4u,
+                                0, 0);
+                    }
+            }
+            return;
+        }
+        // gate/up: h = silu(gate) * up * routing weight for this wave's 16
+        // columns; a row's FP8 1x32 block spans this wave and its partner
+        // (w ^ 1), which meet in LDS. Per tile: all eight rows of the lane
+        // first (independent chains), then one exchange.
+        const int col = cgc * 128 + 16 * w + r;
+#pragma unroll
+        for (int j = 0; j < kTG; j++) {
+            if (j >= Tc) continue;  // uniform
+            const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
+            const int nr = (nrc >> (8 * j)) & 0xFF;
+            es_f16 lw[2];  // the tile's routing weights
+            es_sload32(a.layout_w + slot0, lw);
+            float hv[8], m[8];  // [4 i + v]: row 16 i + 4 g + v
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = 16 * i + 4 * g + v;
+                    const float rw = es_pick4(g, lw[i][v], lw[i][4 + v], lw[i][8 + v], lw[i][12 + v]);
+                    float gv = acc[j][0][i][v], uv = acc[j][1][i][v];
+                    if (a.limit > 0.0f) {
+                        uv = rclamp(uv, -a.limit, a.limit);
+                        gv = fminf(gv, a.limit);
+                    }
+                    const float hh = ws_silu_lanes(gv, tab) * uv * rw;
+                    hv[4 * i + v] = row < nr ? hh : 0.0f;
+                    m[4 * i + v] = __builtin_fabsf(hv[4 * i + v]);
+                }
+#pragma unroll
+            for (int o = 8; o > 0; o >>= 1)
+#pragma unroll
+                for (int k = 0; k < 8; k++) m[k] = fmaxf(m[k], __shfl_xor(m[k], o, 64));
+            // lane r == 0 of group g holds rows 4g + v (i = 0) and 16 + 4g + v
+            // (i = 1): stored as am_l[w][j][g][i][v]
+            const uint32_t base = lds_addr(&am_l[0][0]) + (uint32_t)(j * kTile + 8 * g) * 4u;
+            if (r == 0) es_lds_put8(base + (uint32_t)w * kTG * kTile * 4u, m);
+            raw_barrier();  // the partner's half-block maxima of tile j
+            float mp[8];
+            es_lds_get8(base + (uint32_t)(w ^ 1) * kTG * kTile * 4u, mp);
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = 16 * i + 4 * g + v;
+                    // the rule of quant_fp8_block32 on the 1x32 block
+                    float mm = fmaxf(m[4 * i + v], mp[4 * i + v]);
+                    if (!(mm >= 1e-4f)) mm = 1e-4f;
+                    const int ex = log2_ceil_div448(mm);
+                    const v2bf hb = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                        block_byte(hv[4 * i + v], block_inv_scale(ex)),
+                        e8m0_to_f32((uint32_t)(ex + 127) & 0xFF), false);
+                    __builtin_amdgcn_raw_buffer_store_b16(
+                        (uint16_t)__builtin_bit_cast(uint32_t, hb), obuf,
+                        (uint32_t)((slot0 + row) * a.N + col) * 2u, 0, 0);
+                }
+        }
+    };
+
+    // ---- the stream, unrolled by the ring (static register slots); NS is a
+    // multiple of kRing, so units end on the last step of an iteration. Every
+    // iteration issues one step (past the end a repeat), so when step q is
+    // waited for, exactly the loads of steps q + 1 .. q + kAhead - 1 are newer.
+    EsStep st[kRing];
+    open_compute();
+#pragma unroll
+    for (int u = 0; u < kAhead; u++) {
+        if (s_i == 0) open_issue();
+        issue(st[u], u, true);
+    }
+    auto step = [&](EsStep &x, EsStep &next, int u, int q) {
+        // step q's copies have landed: at most the loads of the kAhead - 1
+        // steps issued after it are in flight (a wave holds at most 63, the
+        // counter's range: the oldest are complete when more were issued)
+        es_vmcnt<((kAhead - 1) * kStepLoads < 63 ? (kAhead - 1) * kStepLoads : 63)>();
+        raw_barrier();  // every wave's copies of step q are in LDS; slot q - 1 is free
+        const bool real = q + kAhead < total;
+        if (real && s_i == 0) open_issue();
+        issue(next, (u + kAhead) % kRing, real);
+        multiply(x, ring + u * kSlotB);
+        s_c++;
+    };
+    static_assert(kRing == 8 && kAhead < kRing, "eight ring slots");
+    for (int q = 0; q < total; q += kRing) {
+        step(st[0], st[(0 + kAhead) % kRing], 0, q);
+        step(st[1], st[(1 + kAhead) % kRing], 1, q + 1);
+        step(st[2], st[(2 + kAhead) % kRing], 2, q + 2);
+        step(st[3], st[(3 + kAhead) % kRing], 3, q + 3);
+        step(st[4], st[(4 + kAhead) % kRing], 4, q + 4);
+        step(st[5], st[(5 + kAhead) % kRing], 5, q + 5);
+        step(st[6], st[(6 + kAhead) % kRing], 6, q + 6);
+        step(st[7], st[(7 + kAhead) % kRing], 7, q + 7);
+        if (s_c == NS) {
+            epilogue();
+            s_c = 0;
+            ri_c++;
+            if (ri_c < n_units) open_compute();
+        }
+    }
+    // the repeated loads of the last steps end here
+    es_vmcnt<0>();
+#pragma unroll
+    for (int u = 0; u < kRing; u++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) __asm__ volatile("" ::"v"(st[u].q[h]), "v"(st[u].s[h]));
+}
+
+// One launch per half of the prefill that runs the expert-stationary body
+// when the dispatch found that its groups pay (*select, es_pays) and the
+// tile-streaming body otherwise; every workgroup takes the same branch.
+template <int ROWS, int CB>
+__global__ __launch_bounds__(kGThreads) void glu_select_kernel(const int32_t *select, EsArgs ea,
+                                                              GluArgs ga) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    if (__builtin_amdgcn_readfirstlane(*select)) es_body<0>(ea, g_lds);
+    else grouped_glu_body<true, ROWS, CB>(ga, g_lds);
+}
+
+template <int CB, bool ABF>
+__global__ __launch_bounds__(kGThreads) void down_select_kernel(const int32_t *select, EsArgs ea,
+                                                               DownArgs da) {
+    extern __shared__ __align__(16) uint8_t g_lds[];
+    if (__builtin_amdgcn_readfirstlane(*select)) es_body<1>(ea, g_lds);
+    else grouped_down_body<true, CB, false, ABF>(da, g_lds);
+}
+
+// The expert-stationary pair serves exact math, dim a multiple of 256 (whole
+// 256-column down blocks), K steps (dim / 128, inter / 128) in whole rounds of
+// the ring and at most kMaxGroups tiles.
+static bool es_fits(int64_t dim, int64_t inter, int64_t tiles) {
+    return math_mode() == WS_MATH_EXACT && dim % 256 == 0 && inter % 128 == 0 &&
+           (dim / 128) % es::kRing == 0 && (inter / 128) % es::kRing == 0 &&
+           tiles <= es::kMaxGroups;
+}
+
 // ---- combine: y[row] = sum of its routes' outputs in ascending slot order --
 // V columns per thread (V = 4: 16-byte loads, dim % 4 == 0)
 template <int V>
@@ -966,12 +1595,13 @@ static int dispatch_launch(const int32_t *topk_idx, const float *topk_w, int32_t
                            int32_t *expert_count, int32_t *expert_offset, int32_t *expert_psum,
                            int32_t *num_tiles, int64_t rows, int64_t top_k, int64_t tiles,
                            int64_t n_experts, const float *xf, uint8_t *xq, uint8_t *xs,
-                           int64_t nx, ws_stream_t stream) {
+                           int64_t nx, ws_stream_t stream, uint16_t *xbf = nullptr,
+                           int32_t *select = nullptr) {
     const int64_t qblocks = (nx + kDispThreads - 1) / kDispThreads;
     hipLaunchKernelGGL(dispatch_kernel<int32_t>, dim3((unsigned)(1 + qblocks)), dim3(kDispThreads),
                        0, stream, topk_idx, topk_w, order, layout_w, route_pos, tile_expert,
                        expert_count, expert_offset, expert_psum, num_tiles, (int)(rows * top_k),
-                       (int)tiles, (int)n_experts, xf, xq, xs, nx);
+                       (int)tiles, (int)n_experts, xf, xq, xs, nx, xbf, select);
     return launch_status();
 }
 
@@ -989,7 +1619,7 @@ int ws_moe_dispatch_tl(const int64_t *topk_idx, const float *topk_weights, int32
     hipLaunchKernelGGL(dispatch_kernel<int64_t>, dim3(1), dim3(kDispThreads), 0, stream, topk_idx,
                        topk_weights, order, layout_weights, route_pos, tile_expert, expert_count,
                        expert_offset, expert_psum, num_tiles, (int)(rows * top_k), (int)tiles,
-                       (int)n_experts, nullptr, nullptr, nullptr, (int64_t)0);
+                       (int)n_experts, nullptr, nullptr, nullptr, (int64_t)0, nullptr, nullptr);
     return launch_status();
 }
 
@@ -1030,13 +1660,13 @@ static int grouped_glu_launch(const uint8_t *xq, const uint8_t *xs, const int32_
     // the A block (ROWS x dim bytes) lives in LDS: 32 rows up to dim 4096,
     // 16-row halves of each tile up to 8192
     if (dim > 8192) return WS_ERR_SHAPE;
+    const GluArgs ga{xq, xs, order, layout_w, tile_expert, num_tiles, exp_off, exp_cnt, w1, s1,
+                     w3, s3, hq, hs, (int)dim, (int)inter, (int)n_experts, (int)top_k,
+                     swiglu_limit};
     dim3 grid((unsigned)cu_count());
 #define WS_GLU(E, R, CB)                                                                      \
     hipLaunchKernelGGL((grouped_glu_quant_kernel<E, R, CB>), grid, dim3(kGThreads),          \
-                       g_tile_lds(R, (int)dim), stream, xq, xs, order, layout_w, tile_expert,  \
-                       num_tiles, exp_off, exp_cnt, w1, s1, w3, s3, hq, hs, (int)dim,        \
-                       (int)inter,                                                            \
-                       (int)n_experts, (int)top_k, swiglu_limit)
+                       g_tile_lds(R, (int)dim), stream, ga)
 #define WS_GLU_CB(E, R)                       \
     if (wide_units(tiles)) WS_GLU(E, R, 2);   \
     else WS_GLU(E, R, 1);
@@ -1091,12 +1721,13 @@ static int grouped_gemm_launch(const uint8_t *hq, const uint8_t *hs, const int32
                                int64_t tokens, ws_stream_t stream) {
     const bool abf = math_mode() == WS_MATH_EXACT && inter <= kAbfMaxK;
     const size_t lds = abf ? g_abf_lds(kTile, (int)inter) : g_tile_lds(kTile, (int)inter);
+    const DownArgs da{hq, hs, tile_expert, num_tiles, exp_off, exp_cnt, order, w2, s2, out,
+                      (int)dim, (int)inter, (int)n_experts, (int)tiles, (int)top_k,
+                      (int)tokens};
     dim3 grid((unsigned)cu_count());
 #define WS_DOWN(E, CB, G, A)                                                                   \
     hipLaunchKernelGGL((grouped_down_kernel<E, CB, G, A>), grid, dim3(kGThreads), lds, stream,  \
-                       hq, hs, tile_expert, num_tiles, exp_off, exp_cnt, order, w2, s2, out,    \
-                       (int)dim, (int)inter,                                                    \
-                       (int)n_experts, (int)tiles, (int)top_k, (int)tokens)
+                       da)
     const bool wide = wide_units(tiles);
     if (abf) {
         if (gather) { if (wide) WS_DOWN(true, 2, true, true); else WS_DOWN(true, 1, true, true); }
@@ -1169,7 +1800,8 @@ size_t ws_moe_prefill_workspace_size(int64_t rows, int64_t dim, int64_t inter, i
     const int64_t slots = tiles * kTile;
     return a256(rows * dim) + a256(rows * (dim / 32)) + a256(slots * 4) * 2 + a256(routes * 4) +
            a256(tiles * 4) + a256(n_experts * 4) * 3 + a256(4) + a256(slots * inter) +
-           a256(slots * (inter / 32)) + a256(slots * dim * 4);
+           a256(slots * (inter / 32)) + a256(slots * dim * 4) + a256(rows * dim * 2) +
+           a256(slots * inter * 2);
 }
 
 int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
@@ -1203,16 +1835,58 @@ int ws_moe_prefill(const float *x, const int32_t *topk_idx, const float *topk_w,
     int32_t *cnt = (int32_t *)take(n_experts * 4);
     int32_t *off = (int32_t *)take(n_experts * 4);
     int32_t *psum = (int32_t *)take(n_experts * 4);
-    int32_t *ntiles = (int32_t *)take(4);
+    int32_t *ntiles = (int32_t *)take(4);  // [0] used tiles; [1] the stationary choice
+    int32_t *sel = ntiles + 1;             // (a256: the slot holds 256 bytes)
     uint8_t *hq = take(slots * inter);
     uint8_t *hs = take(slots * (inter / 32));
     float *down = (float *)take(slots * dim * 4);
+    uint16_t *xbf = (uint16_t *)take(rows * dim * 2);
+    uint16_t *hbf = (uint16_t *)take(slots * inter * 2);
     // the dispatch and the tokens' quantisation in one launch
     if (n_experts > kMaxExpertsG || routes > (1 << 26) || tiles > (1 << 24)) return WS_ERR_SHAPE;
+    const bool stationary = es_fits(dim, inter, tiles);
     int rc = dispatch_launch(topk_idx, topk_w, order, layout_w, route_pos, tile_expert, cnt, off,
                              psum, ntiles, rows, top_k, tiles, n_experts, x, xq, xs, rows * dim,
-                             stream);
+                             stream, stationary ? xbf : nullptr, stationary ? sel : nullptr);
     if (rc) return rc;
+    if (stationary) {
+        // both halves run the body the dispatch chose on the device (*sel)
+        const dim3 grid((unsigned)cu_count());
+        const EsArgs ea{(const uint8_t *)xbf, order, layout_w, tile_expert, ntiles, off, cnt,
+                        w1, s1, w3, s3, (uint8_t *)hbf, nullptr, (int)dim, (int)inter,
+                        (int)n_experts, (int)top_k, (int)rows, (int)slots, swiglu_limit};
+        const GluArgs ga{xq, xs, order, layout_w, tile_expert, ntiles, off, cnt, w1, s1, w3, s3,
+                         hq, hs, (int)dim, (int)inter, (int)n_experts, (int)top_k,
+                         swiglu_limit};
+        const bool wide = wide_units(tiles);
+        const int grows = dim <= 4096 ? 32 : 16;
+        const size_t glds = std::max(es::kLdsAll, g_tile_lds(grows, (int)dim));
+        if (grows == 32) {
+            if (wide) hipLaunchKernelGGL((glu_select_kernel<32, 2>), grid, dim3(kGThreads), glds, stream, sel, ea, ga);
+            else hipLaunchKernelGGL((glu_select_kernel<32, 1>), grid, dim3(kGThreads), glds, stream, sel, ea, ga);
+        } else {
+            if (wide) hipLaunchKernelGGL((glu_select_kernel<16, 2>), grid, dim3(kGThreads), glds, stream, sel, ea, ga);
+            else hipLaunchKernelGGL((glu_select_kernel<16, 1>), grid, dim3(kGThreads), glds, stream, sel, ea, ga);
+        }
+        if ((rc = launch_status())) return rc;
+        const EsArgs eb{(const uint8_t *)hbf, order, layout_w, tile_expert, ntiles, off, cnt,
+                        w2, s2, nullptr, nullptr, nullptr, down, (int)inter, (int)dim,
+                        (int)n_experts, (int)top_k, (int)slots, (int)slots, 0.0f};
+        const DownArgs da{hq, hs, tile_expert, ntiles, off, cnt, order, w2, s2, down, (int)dim,
+                          (int)inter, (int)n_experts, (int)tiles, 1, 1};
+        const bool abf = inter <= kAbfMaxK;
+        const size_t dlds = std::max(es::kLdsAll, abf ? g_abf_lds(kTile, (int)inter)
+                                                      : g_tile_lds(kTile, (int)inter));
+        if (abf) {
+            if (wide) hipLaunchKernelGGL((down_select_kernel<2, true>), grid, dim3(kGThreads), dlds, stream, sel, eb, da);
+            else hipLaunchKernelGGL((down_select_kernel<1, true>), grid, dim3(kGThreads), dlds, stream, sel, eb, da);
+        } else {
+            if (wide) hipLaunchKernelGGL((down_select_kernel<2, false>), grid, dim3(kGThreads), dlds, stream, sel, eb, da);
+            else hipLaunchKernelGGL((down_select_kernel<1, false>), grid, dim3(kGThreads), dlds, stream, sel, eb, da);
+        }
+        if ((rc = launch_status())) return rc;
+        return ws_moe_combine_f32(down, route_pos, y, dim, top_k, rows, tiles, stream);
+    }
     rc = grouped_glu_launch(xq, xs, order, layout_w, tile_expert, ntiles, off, cnt, w1, s1, w3, s3,
                             hq, hs, dim, inter, n_experts, top_k, tiles, swiglu_limit, stream);
     if (rc) return rc;
