@@ -160,6 +160,23 @@ def _fp4_normal_slab(gen, E, rows, cols, chunk=64):
     return q, s
 
 
+def _a256(v):
+    return (v + 255) // 256 * 256
+
+
+def _stationary_choice(ws, m, dim, k, E):
+    """The body ws_moe_prefill's dispatch chose (1: expert-stationary, 0:
+    tile-streaming), the int32 after the used-tile count in the workspace,
+    whose regions (in order, each 256-byte aligned) are xq, xs, order,
+    layout_w, route_pos, tile_expert, three per-expert arrays, the tile
+    count."""
+    routes = m * k
+    slots = L.moe_tiles(routes, E) * 32
+    off = (_a256(m * dim) + _a256(m * dim // 32) + 2 * _a256(slots * 4) + _a256(routes * 4) +
+           _a256(slots // 32 * 4) + 3 * _a256(E * 4))
+    return int(host(ws[off + 4:off + 8]).view(np.int32)[0])
+
+
 @pytest.mark.parametrize("zipf", [1.1, 0.275])
 def test_config4_baseline_weights_prefill_matches_oracle(zipf):
     """BASELINE config 4 as the bench runs it: M = 132 tokens, 384 experts of
@@ -184,6 +201,9 @@ def test_config4_baseline_weights_prefill_matches_oracle(zipf):
     y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
     P = _packed(slabs, E, dim, inter)
     L.moe_prefill(dev(x), idx, w, *P, y, m, dim, inter, E, k, ws)
+    # the skewed draw runs the expert-stationary bodies, the mild one the
+    # tile-streaming pair: both are checked here
+    assert _stationary_choice(ws, m, dim, k, E) == (1 if zipf > 1 else 0)
     gi, gw, gy = host(idx), host(w), host(y)
     H = _host_experts(slabs, gi.ravel(), E, dim, inter)
     staged = None
