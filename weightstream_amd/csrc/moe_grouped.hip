@@ -958,7 +958,8 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(DownArgs da) {
 // dropped). Units go out sorted by group size and dealt to the workgroups in
 // snake order, which evens out the work per workgroup.
 namespace es {
-constexpr int kTG = kEsGroup;                        // tiles per group
+constexpr int kTG = kEsGroup;
+                        // tiles per group
 constexpr int kRing = 8;                      // ring slots (LDS and registers), one 128-K step each
 constexpr int kRowB = 256;                    // bytes of one A row per step (128 bf16)
 constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
@@ -986,37 +987,10 @@ template <int N>
 __device__ __forceinline__ void es_vmcnt() {
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// s_waitcnt vmcnt(n) for a run-time n in [LO, HI]
-template <int LO, int HI>
-__device__ __forceinline__ void es_wait_vm(int n) {
-    if constexpr (LO == HI) {
-        es_vmcnt<LO>();
-    } else {
-        constexpr int MID = (LO + HI) / 2;
-        if (n <= MID) es_wait_vm<LO, MID>(n);
-        else es_wait_vm<MID + 1, HI>(n);
-    }
-}
 // Loads through the scalar cache into SGPRs (uniform address; nothing in this
 // launch writes the data), complete when the statement ends; they count in
 // lgkmcnt, not in the vmcnt of the stream.
 typedef int es_i4 __attribute__((ext_vector_type(4)));
-typedef float es_f16 __attribute__((ext_vector_type(16)));
-__device__ __forceinline__ int es_sload1(const int32_t *p) {
-    int v;
-    __asm__ volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return v;
-}
-__device__ __forceinline__ es_i4 es_sload4(const int32_t *p) {
-    es_i4 v;
-    __asm__ volatile("s_load_dwordx4 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return v;
-}
-__device__ __forceinline__ es_f16 es_sload16(const float *p) {
-    es_f16 v;
-    __asm__ volatile("s_load_dwordx16 %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
-    return v;
-}
 // four 16-byte loads, one round trip
 __device__ __forceinline__ void es_sload4x4(const int32_t *p0, const int32_t *p1, const int32_t *p2,
                                             const int32_t *p3, es_i4 o[4]) {
@@ -1025,14 +999,6 @@ __device__ __forceinline__ void es_sload4x4(const int32_t *p0, const int32_t *p1
         "s_load_dwordx4 %2, %6, 0x0\n\ts_load_dwordx4 %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
         : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
         : "s"(p0), "s"(p1), "s"(p2), "s"(p3)
-        : "memory");
-}
-// 32 consecutive floats (two 64-byte loads), one round trip
-__device__ __forceinline__ void es_sload32(const float *p, es_f16 o[2]) {
-    __asm__ volatile(
-        "s_load_dwordx16 %0, %2, 0x0\n\ts_load_dwordx16 %1, %2, 0x40\n\ts_waitcnt lgkmcnt(0)"
-        : "=&s"(o[0]), "=&s"(o[1])
-        : "s"(p)
         : "memory");
 }
 // An LDS word, complete when the statement ends (no ordinary LDS access, so
@@ -1070,16 +1036,6 @@ struct EsStep {  // one wave's weight loads of one step: two bands
     u32x4v q[2];
     uint32_t s[2];
 };
-// an LDS word written / read, complete when the statement ends (no ordinary
-// LDS access, so the compiler adds no wait for the stream's LDS copies)
-__device__ __forceinline__ void es_lds_put(float *p, float v) {
-    __asm__ volatile("ds_write_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : : "v"(lds_addr(p)), "v"(v) : "memory");
-}
-__device__ __forceinline__ float es_lds_getf(const float *p) {
-    float v;
-    __asm__ volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_addr(p)) : "memory");
-    return v;
-}
 // eight LDS words at p + 4 k (byte offsets 0, 4, ..., 28 from a) written;
 // complete when the statement ends
 __device__ __forceinline__ void es_lds_put8(uint32_t a, const float v[8]) {
@@ -1107,12 +1063,6 @@ __device__ __forceinline__ void es_lds_get8(uint32_t a, float v[8]) {
         : "memory");
 }
 
-// one of four wave-uniform values by a per-lane index 0..3 (selects, no
-// indexed private array)
-__device__ __forceinline__ float es_pick4(int g, float a, float b, float c, float d) {
-    const float lo = (g & 1) ? b : a, hi = (g & 1) ? d : c;
-    return (g & 2) ? hi : lo;
-}
 
 // MODE 0: gate/up + SwiGLU + routing weight + FP8 1x32 re-quantisation of h,
 // written as the exact bf16 of the quantised values (the down step's A).
@@ -1285,6 +1235,10 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 
     // ---- compute side: the unit being multiplied
     int ri_c = 0, s_c = 0, Tc = 1, t0c = 0, cgc = 0, lo16 = 0, nrc = 0;
+    // gate/up: the routing weights of the lane's rows 4g .. 4g + 3 and
+    // 16 + 4g .. of each tile, loaded when the unit opens (used at its end)
+    const es_rsrc lwbuf = es_buf(a.layout_w, (size_t)a.slots * 4);
+    u32x4v rwv[kTG][2];
     auto open_compute = [&]() {
         const int k = unit_k(ri_c);
         const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
@@ -1296,6 +1250,16 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 #pragma unroll
         for (int j = 0; j < kTG; j++)
             if (((nrc >> (8 * j)) & 0xFF) <= 16) lo16 |= 1 << j;
+        if (MODE == 0)
+#pragma unroll
+            for (int j = 0; j < kTG; j++) {
+                const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+                    rwv[j][i] = __builtin_bit_cast(
+                        u32x4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                    lwbuf, (uint32_t)(slot0 + 16 * i + 4 * g) * 4u, 0, 0));
+            }
     };
     v4f acc[kTG][2][2];  // [tile][band][16-row fragment]
     const uint64_t tab = ws_lane_exp2f_tab(lane);
@@ -1375,15 +1339,13 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
             if (j >= Tc) continue;  // uniform
             const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
             const int nr = (nrc >> (8 * j)) & 0xFF;
-            es_f16 lw[2];  // the tile's routing weights
-            es_sload32(a.layout_w + slot0, lw);
             float hv[8], m[8];  // [4 i + v]: row 16 i + 4 g + v
 #pragma unroll
             for (int i = 0; i < 2; i++)
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int row = 16 * i + 4 * g + v;
-                    const float rw = es_pick4(g, lw[i][v], lw[i][4 + v], lw[i][8 + v], lw[i][12 + v]);
+                    const float rw = __uint_as_float(rwv[j][i][v]);
                     float gv = acc[j][0][i][v], uv = acc[j][1][i][v];
                     if (a.limit > 0.0f) {
                         uv = rclamp(uv, -a.limit, a.limit);
