@@ -944,22 +944,23 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(DownArgs da) {
 // group's tiles. The A rows arrive as exact bf16 (the e4m3 bytes times their
 // UE8M0 scales, written once by the step before) through direct global->LDS
 // loads into a ring of kRing 128-K steps, so the waves convert only weights.
-// Four waves, one per SIMD (512 registers each); wave w owns four 16-row
-// bands over the whole K: gate/up the w1 and the w3 bands of intermediate
-// columns 32w .. 32w + 31 of the block (SwiGLU pairs and whole FP8 blocks in
-// one wave's registers), down output columns 64w .. 64w + 63. The
-// workgroup's steps form one stream across its units: the loads of step
-// q + kAhead are issued while step q is multiplied, with one workgroup
-// barrier per step (ring slot (q - 1) % kRing is free once every wave is
-// past it). Every step issues the same number of loads (the tiles a group
+// Eight waves, two per SIMD; wave w owns two 16-row bands over the whole K:
+// gate/up the w1 and the w3 bands of intermediate columns 16w .. 16w + 15
+// of a 128-column block (a row's FP8 1x32 block spans wave w and its partner
+// w ^ 1, which trade their maxima through LDS), down output columns
+// 32w .. 32w + 31 of a 256-column block. The workgroup's steps form one
+// stream across its units: the loads of step q + kAhead are issued while
+// step q is multiplied, with one workgroup barrier per two steps (at an even
+// step each wave waits for its copies of steps q and q + 1, then the
+// barrier; the ring slot the next issues fill, that of step
+// q + kAhead - kRing <= q - 2, was read before the last barrier). Every step issues the same number of loads (the tiles a group
 // lacks get a 4-byte stand-in copy), so one fixed count (vmcnt) says when a
 // step's copies have landed. Every global access goes through a buffer
 // descriptor sized to its array (out-of-range reads return zeros, writes are
 // dropped). Units go out sorted by group size and dealt to the workgroups in
 // snake order, which evens out the work per workgroup.
 namespace es {
-constexpr int kTG = kEsGroup;
-                        // tiles per group
+constexpr int kTG = kEsGroup;                 // tiles per group
 constexpr int kRing = 8;                      // ring slots (LDS and registers), one 128-K step each
 constexpr int kRowB = 256;                    // bytes of one A row per step (128 bf16)
 constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
@@ -1070,7 +1071,7 @@ __device__ __forceinline__ void es_lds_get8(uint32_t a, float v[8]) {
 template <int MODE>
 __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     using namespace es;
-    constexpr int kAhead = MODE == 0 ? 5 : 7;  // steps issued ahead of the one multiplied
+    constexpr int kAhead = 6;  // steps issued ahead of the one multiplied
     constexpr int NW = kThreads / 64;
     // g_lds: the A ring (kLds bytes), then the group table
     int *grp_l = (int *)(g_lds + kLds);   // [kMaxGroups] tile | T << 16 | expert << 19
@@ -1387,8 +1388,9 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 
     // ---- the stream, unrolled by the ring (static register slots); NS is a
     // multiple of kRing, so units end on the last step of an iteration. Every
-    // iteration issues one step (past the end a repeat), so when step q is
-    // waited for, exactly the loads of steps q + 1 .. q + kAhead - 1 are newer.
+    // iteration issues one step (past the end a repeat), so when steps q and
+    // q + 1 are waited for, exactly the loads of steps q + 2 .. q + kAhead - 1
+    // are newer.
     EsStep st[kRing];
     open_compute();
 #pragma unroll
@@ -1397,18 +1399,20 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         issue(st[u], u, true);
     }
     auto step = [&](EsStep &x, EsStep &next, int u, int q) {
-        // step q's copies have landed: at most the loads of the kAhead - 1
-        // steps issued after it are in flight (a wave holds at most 63, the
-        // counter's range: the oldest are complete when more were issued)
-        es_vmcnt<((kAhead - 1) * kStepLoads < 63 ? (kAhead - 1) * kStepLoads : 63)>();
-        raw_barrier();  // every wave's copies of step q are in LDS; slot q - 1 is free
+        if ((u & 1) == 0) {
+            // steps q and q + 1 have landed: at most the loads of the
+            // kAhead - 2 steps issued after them are in flight (a wave holds
+            // at most 63, the counter's range)
+            es_vmcnt<((kAhead - 2) * kStepLoads < 63 ? (kAhead - 2) * kStepLoads : 63)>();
+            raw_barrier();  // every wave's copies of both steps are in LDS
+        }
         const bool real = q + kAhead < total;
         if (real && s_i == 0) open_issue();
         issue(next, (u + kAhead) % kRing, real);
         multiply(x, ring + u * kSlotB);
         s_c++;
     };
-    static_assert(kRing == 8 && kAhead < kRing, "eight ring slots");
+    static_assert(kRing == 8 && kAhead <= kRing - 2, "eight ring slots, slot q - 2 the newest reused");
     for (int q = 0; q < total; q += kRing) {
         step(st[0], st[(0 + kAhead) % kRing], 0, q);
         step(st[1], st[(1 + kAhead) % kRing], 1, q + 1);
