@@ -1147,10 +1147,15 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     lds_barrier();
 
     // ---- this workgroup's units: unit k of the sorted order goes to round
-    // k / G, workgroup k % G in even rounds and G - 1 - k % G in odd ones
+    // k / G, position p = k % G in even rounds and G - 1 - k % G in odd ones;
+    // position p is workgroup (p % (G / 8)) * 8 + p / (G / 8), so the column
+    // blocks of a group (consecutive positions) run on one XCD (the hardware
+    // deals workgroup b to XCD b % 8) and read the group's A rows from that
+    // XCD's L2
     const int G = gridDim.x, b = blockIdx.x;
+    const int pb = (G % 8 == 0) ? (b % 8) * (G / 8) + b / 8 : b;
     const int U = ng * NCG;
-    auto unit_k = [&](int ri) { return ri * G + ((ri & 1) ? G - 1 - b : b); };
+    auto unit_k = [&](int ri) { return ri * G + ((ri & 1) ? G - 1 - pb : pb); };
     const int n_units = U / G + (unit_k(U / G) < U ? 1 : 0);
     if (n_units == 0) return;  // whole workgroup
     const int total = n_units * NS;
