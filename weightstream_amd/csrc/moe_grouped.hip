@@ -988,20 +988,6 @@ template <int N>
 __device__ __forceinline__ void es_vmcnt() {
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Loads through the scalar cache into SGPRs (uniform address; nothing in this
-// launch writes the data), complete when the statement ends; they count in
-// lgkmcnt, not in the vmcnt of the stream.
-typedef int es_i4 __attribute__((ext_vector_type(4)));
-// four 16-byte loads, one round trip
-__device__ __forceinline__ void es_sload4x4(const int32_t *p0, const int32_t *p1, const int32_t *p2,
-                                            const int32_t *p3, es_i4 o[4]) {
-    __asm__ volatile(
-        "s_load_dwordx4 %0, %4, 0x0\n\ts_load_dwordx4 %1, %5, 0x0\n\t"
-        "s_load_dwordx4 %2, %6, 0x0\n\ts_load_dwordx4 %3, %7, 0x0\n\ts_waitcnt lgkmcnt(0)"
-        : "=&s"(o[0]), "=&s"(o[1]), "=&s"(o[2]), "=&s"(o[3])
-        : "s"(p0), "s"(p1), "s"(p2), "s"(p3)
-        : "memory");
-}
 // An LDS word, complete when the statement ends (no ordinary LDS access, so
 // the compiler does not wait for the stream's direct-to-LDS copies).
 __device__ __forceinline__ int es_lds_word(const int *p) {
@@ -1169,6 +1155,20 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     es_rsrc wr[2], sr[2];     // the unit's expert matrices (gate/up: w1, w3; down: w2)
     uint32_t bo[2], so[2];    // this lane's byte offsets of step 0 per band (weights, scales)
     uint32_t ao[kTG];         // this lane's A row offset per tile (rows 4w .. 4w + 3)
+    // gate/up: the route of row 4w + g of each tile of the next unit to open,
+    // loaded one unit ahead (a vector load; the unit's first issue uses it)
+    const es_rsrc ordbuf = es_buf(a.order, (size_t)a.slots * 4);
+    int on[kTG];
+    auto pre_order = [&](int ri) {
+        if (MODE != 0) return;
+        const int k = unit_k(min(ri, n_units - 1));
+        const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
+        const int t0 = v & 0xFFFF, T = (v >> 16) & 7;
+#pragma unroll
+        for (int j = 0; j < kTG; j++)
+            on[j] = (int)__builtin_amdgcn_raw_buffer_load_b32(
+                ordbuf, (uint32_t)(((t0 + min(j, T - 1)) * kTile + 4 * w + g) * 4), 0, 0);
+    };
     auto open_issue = [&]() {
         const int k = unit_k(ri_i);
         const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
@@ -1189,30 +1189,19 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         // row 4w + g of each tile; a row's 16-byte pieces are stored
         // XOR-permuted by the row (bank spread)
         const int row = 4 * w + g;
-        es_i4 o[2];
-        if (MODE == 0) {
-            es_i4 o4[4];
-            const int32_t *o0 = a.order + (size_t)t0 * kTile + 4 * w;
-            const int32_t *o1 = a.order + (size_t)(t0 + min(1, Ti - 1)) * kTile + 4 * w;
-            es_sload4x4(o0, o0, o1, o1, o4);
-            o[0] = o4[0];
-            o[1] = o4[2];
-        }
-        static_assert(kTG == 2, "two tiles per group");
 #pragma unroll
         for (int j = 0; j < kTG; j++) {
             const int tj = t0 + min(j, Ti - 1);
             uint32_t arow;
             if (MODE == 0) {
-                const es_i4 &oc = o[j];
-                const int lo = (g & 1) ? oc[1] : oc[0], hi = (g & 1) ? oc[3] : oc[2];
-                const int route = (g & 2) ? hi : lo;
+                const int route = on[j];
                 arow = route >= 0 ? (uint32_t)(route / a.top_k) : 0u;
             } else {
                 arow = (uint32_t)(tj * kTile + row);
             }
             ao[j] = arow * (uint32_t)a.K * 2u + ((r ^ (row & 15)) << 4);
         }
+        pre_order(ri_i + 1);
     };
     // the loads of the next step of the stream (its unit opened) into
     // register slot x and ring slot `slot`: kStepLoads per wave. Past the end
@@ -1397,6 +1386,7 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     // q + 1 are waited for, exactly the loads of steps q + 2 .. q + kAhead - 1
     // are newer.
     EsStep st[kRing];
+    pre_order(0);
     open_compute();
 #pragma unroll
     for (int u = 0; u < kAhead; u++) {
