@@ -973,6 +973,7 @@ constexpr size_t kLdsAll = kLds + 2 * kMaxGroups * sizeof(int);  // ring + group
 }  // namespace es
 
 typedef __amdgpu_buffer_rsrc_t es_rsrc;
+typedef unsigned int es_u2 __attribute__((ext_vector_type(2)));
 // raw buffer of `bytes` bytes at p (gfx9 descriptor word 3)
 __device__ __forceinline__ es_rsrc es_buf(const void *p, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0,
@@ -1023,29 +1024,18 @@ struct EsStep {  // one wave's weight loads of one step: two bands
     u32x4v q[2];
     uint32_t s[2];
 };
-// eight LDS words at p + 4 k (byte offsets 0, 4, ..., 28 from a) written;
-// complete when the statement ends
-__device__ __forceinline__ void es_lds_put8(uint32_t a, const float v[8]) {
-    __asm__ volatile(
-        "ds_write_b32 %0, %1\n\tds_write_b32 %0, %2 offset:4\n\tds_write_b32 %0, %3 offset:8\n\t"
-        "ds_write_b32 %0, %4 offset:12\n\tds_write_b32 %0, %5 offset:16\n\t"
-        "ds_write_b32 %0, %6 offset:20\n\tds_write_b32 %0, %7 offset:24\n\t"
-        "ds_write_b32 %0, %8 offset:28\n\ts_waitcnt lgkmcnt(0)"
-        :
-        : "v"(a), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]),
-          "v"(v[7])
-        : "memory");
+// two LDS words at a and a + 64 written / read; complete when the statement
+// ends
+__device__ __forceinline__ void es_lds_put2(uint32_t a, float v0, float v1) {
+    __asm__ volatile("ds_write_b32 %0, %1\n\tds_write_b32 %0, %2 offset:64\n\ts_waitcnt lgkmcnt(0)"
+                     :
+                     : "v"(a), "v"(v0), "v"(v1)
+                     : "memory");
 }
-// eight LDS words at a (byte offsets 0, 4, ..., 28) read; complete when the
-// statement ends
-__device__ __forceinline__ void es_lds_get8(uint32_t a, float v[8]) {
+__device__ __forceinline__ void es_lds_get2(uint32_t a, float &v0, float &v1) {
     __asm__ volatile(
-        "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:4\n\tds_read_b32 %2, %8 offset:8\n\t"
-        "ds_read_b32 %3, %8 offset:12\n\tds_read_b32 %4, %8 offset:16\n\t"
-        "ds_read_b32 %5, %8 offset:20\n\tds_read_b32 %6, %8 offset:24\n\t"
-        "ds_read_b32 %7, %8 offset:28\n\ts_waitcnt lgkmcnt(0)"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
-          "=&v"(v[6]), "=&v"(v[7])
+        "ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:64\n\ts_waitcnt lgkmcnt(0)"
+        : "=&v"(v0), "=&v"(v1)
         : "v"(a)
         : "memory");
 }
@@ -1230,10 +1220,10 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 
     // ---- compute side: the unit being multiplied
     int ri_c = 0, s_c = 0, Tc = 1, t0c = 0, cgc = 0, lo16 = 0, nrc = 0;
-    // gate/up: the routing weights of the lane's rows 4g .. 4g + 3 and
-    // 16 + 4g .. of each tile, loaded when the unit opens (used at its end)
+    // gate/up: the routing weights of the lane's rows r and 16 + r of each
+    // tile, loaded when the unit opens (used at its end)
     const es_rsrc lwbuf = es_buf(a.layout_w, (size_t)a.slots * 4);
-    u32x4v rwv[kTG][2];
+    float rwf[kTG][2];
     auto open_compute = [&]() {
         const int k = unit_k(ri_c);
         const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
@@ -1251,12 +1241,14 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
                 const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
 #pragma unroll
                 for (int i = 0; i < 2; i++)
-                    rwv[j][i] = __builtin_bit_cast(
-                        u32x4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                    lwbuf, (uint32_t)(slot0 + 16 * i + 4 * g) * 4u, 0, 0));
+                    rwf[j][i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        lwbuf, (uint32_t)(slot0 + 16 * i + r) * 4u, 0, 0));
             }
     };
-    v4f acc[kTG][2][2];  // [tile][band][16-row fragment]
+    // [tile][band][16-row fragment]: the weights are the MFMA's first
+    // operand, so lane (r, g) holds columns 4g .. 4g + 3 of the band for
+    // row r of the fragment (four adjacent columns of one row)
+    v4f acc[kTG][2][2];
     const uint64_t tab = ws_lane_exp2f_tab(lane);
 
     auto multiply = [&](const EsStep &x, uint32_t sbase) {
@@ -1290,7 +1282,7 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
                     const v8bf am = __builtin_bit_cast(v8bf, av[jj]);
 #pragma unroll
                     for (int h = 0; h < 2; h++)
-                        acc[j][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(am, bq[h][jj],
+                        acc[j][h][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[h][jj], am,
                                                                                acc[j][h][i], 0, 0, 0);
                 }
             }
@@ -1301,82 +1293,81 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
                                    : es_buf(a.out, (size_t)a.slots * a.N * 4);
     auto epilogue = [&]() {
         if (MODE == 1) {
-            // f32 out of the slots that hold routes, straight from the
-            // accumulators (each tile unrolled)
+            // f32 out of the slots that hold routes: four adjacent columns
+            // per lane and row, straight from the accumulators
 #pragma unroll
             for (int j = 0; j < kTG; j++) {
                 if (j >= Tc) continue;  // uniform
                 const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
                 const int nr = (nrc >> (8 * j)) & 0xFF;
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < 2; i++) {
+                    const int row = 16 * i + r;
+                    if (row >= nr) continue;
 #pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        const int row = 16 * i + 4 * g + v;
-                        if (row >= nr) continue;
-#pragma unroll
-                        for (int h = 0; h < 2; h++)
-                            __builtin_amdgcn_raw_buffer_store_b32(
-                                __float_as_uint(acc[j][h][i][v]), obuf,
-                                (uint32_t)((slot0 + row) * a.N + cgc * 256 + 32 * w + 16 * h + r) * 4u,
-                                0, 0);
-                    }
+                    for (int h = 0; h < 2; h++)
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(u32x4v, acc[j][h][i]), obuf,
+                            (uint32_t)((slot0 + row) * a.N + cgc * 256 + 32 * w + 16 * h + 4 * g) * 4u,
+                            0, 0);
+                }
             }
             return;
         }
         // gate/up: h = silu(gate) * up * routing weight for this wave's 16
-        // columns; a row's FP8 1x32 block spans this wave and its partner
-        // (w ^ 1), which meet in LDS. Per tile: all eight rows of the lane
-        // first (independent chains), then one exchange.
-        const int col = cgc * 128 + 16 * w + r;
+        // columns; a row's FP8 1x32 block spans this wave (lanes g = 0..3 of
+        // the row's r) and its partner (w ^ 1), which meet in LDS
+        const int col = cgc * 128 + 16 * w + 4 * g;
 #pragma unroll
         for (int j = 0; j < kTG; j++) {
             if (j >= Tc) continue;  // uniform
             const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
             const int nr = (nrc >> (8 * j)) & 0xFF;
-            float hv[8], m[8];  // [4 i + v]: row 16 i + 4 g + v
+            float hv[2][4], m[2];  // [i][v]: row 16 i + r, column col + v
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < 2; i++) {
+                const int row = 16 * i + r;
+                const float rw = rwf[j][i];
+                m[i] = 0.0f;
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const int row = 16 * i + 4 * g + v;
-                    const float rw = __uint_as_float(rwv[j][i][v]);
                     float gv = acc[j][0][i][v], uv = acc[j][1][i][v];
                     if (a.limit > 0.0f) {
                         uv = rclamp(uv, -a.limit, a.limit);
                         gv = fminf(gv, a.limit);
                     }
                     const float hh = ws_silu_lanes(gv, tab) * uv * rw;
-                    hv[4 * i + v] = row < nr ? hh : 0.0f;
-                    m[4 * i + v] = __builtin_fabsf(hv[4 * i + v]);
+                    hv[i][v] = row < nr ? hh : 0.0f;
+                    m[i] = fmaxf(m[i], __builtin_fabsf(hv[i][v]));
                 }
+                m[i] = fmaxf(m[i], __shfl_xor(m[i], 16, 64));
+                m[i] = fmaxf(m[i], __shfl_xor(m[i], 32, 64));
+            }
+            // the row maxima of the wave's 16 columns: am_l[w][j * 32 + row]
+            const uint32_t base = lds_addr(&am_l[0][0]) + (uint32_t)(j * kTile + r) * 4u;
+            if (g == 0) es_lds_put2(base + (uint32_t)w * kTG * kTile * 4u, m[0], m[1]);
+            raw_barrier();  // the partner's maxima of tile j
+            float mp[2];
+            es_lds_get2(base + (uint32_t)(w ^ 1) * kTG * kTile * 4u, mp[0], mp[1]);
 #pragma unroll
-            for (int o = 8; o > 0; o >>= 1)
+            for (int i = 0; i < 2; i++) {
+                const int row = 16 * i + r;
+                // the rule of quant_fp8_block32 on the 1x32 block
+                float mm = fmaxf(m[i], mp[i]);
+                if (!(mm >= 1e-4f)) mm = 1e-4f;
+                const int ex = log2_ceil_div448(mm);
+                const float inv = block_inv_scale(ex), sc = e8m0_to_f32((uint32_t)(ex + 127) & 0xFF);
+                uint32_t hb[2];  // the bf16 of the four quantised values, two per word
 #pragma unroll
-                for (int k = 0; k < 8; k++) m[k] = fmaxf(m[k], __shfl_xor(m[k], o, 64));
-            // lane r == 0 of group g holds rows 4g + v (i = 0) and 16 + 4g + v
-            // (i = 1): stored as am_l[w][j][g][i][v]
-            const uint32_t base = lds_addr(&am_l[0][0]) + (uint32_t)(j * kTile + 8 * g) * 4u;
-            if (r == 0) es_lds_put8(base + (uint32_t)w * kTG * kTile * 4u, m);
-            raw_barrier();  // the partner's half-block maxima of tile j
-            float mp[8];
-            es_lds_get8(base + (uint32_t)(w ^ 1) * kTG * kTile * 4u, mp);
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int row = 16 * i + 4 * g + v;
-                    // the rule of quant_fp8_block32 on the 1x32 block
-                    float mm = fmaxf(m[4 * i + v], mp[4 * i + v]);
-                    if (!(mm >= 1e-4f)) mm = 1e-4f;
-                    const int ex = log2_ceil_div448(mm);
-                    const v2bf hb = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                        block_byte(hv[4 * i + v], block_inv_scale(ex)),
-                        e8m0_to_f32((uint32_t)(ex + 127) & 0xFF), false);
-                    __builtin_amdgcn_raw_buffer_store_b16(
-                        (uint16_t)__builtin_bit_cast(uint32_t, hb), obuf,
-                        (uint32_t)((slot0 + row) * a.N + col) * 2u, 0, 0);
-                }
+                for (int p = 0; p < 2; p++)
+                    hb[p] = __builtin_bit_cast(
+                        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
+                                      block_byte(hv[i][2 * p], inv) |
+                                          (block_byte(hv[i][2 * p + 1], inv) << 8),
+                                      sc, false));
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    (es_u2){hb[0], hb[1]}, obuf, (uint32_t)((slot0 + row) * a.N + col) * 2u, 0, 0);
+            }
         }
     };
 
