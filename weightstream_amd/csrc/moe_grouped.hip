@@ -1316,19 +1316,22 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         }
         // gate/up: h = silu(gate) * up * routing weight for this wave's 16
         // columns; a row's FP8 1x32 block spans this wave (lanes g = 0..3 of
-        // the row's r) and its partner (w ^ 1), which meet in LDS
+        // the row's r) and its partner (w ^ 1), which meet in LDS (both
+        // tiles' maxima across one barrier)
         const int col = cgc * 128 + 16 * w + 4 * g;
+        float hv[kTG][2][4], m[kTG][2];  // [j][i][v]: tile j, row 16 i + r, column col + v
 #pragma unroll
         for (int j = 0; j < kTG; j++) {
-            if (j >= Tc) continue;  // uniform
-            const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
             const int nr = (nrc >> (8 * j)) & 0xFF;
-            float hv[2][4], m[2];  // [i][v]: row 16 i + r, column col + v
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int row = 16 * i + r;
                 const float rw = rwf[j][i];
-                m[i] = 0.0f;
+                m[j][i] = 0.0f;
+#pragma unroll
+                for (int v = 0; v < 4; v++) hv[j][i][v] = 0.0f;
+                // uniform: a tile the group lacks, rows 16.. of padding
+                if (j >= Tc || (i == 1 && ((lo16 >> j) & 1))) continue;
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     float gv = acc[j][0][i][v], uv = acc[j][1][i][v];
@@ -1337,23 +1340,33 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
                         gv = fminf(gv, a.limit);
                     }
                     const float hh = ws_silu_lanes(gv, tab) * uv * rw;
-                    hv[i][v] = row < nr ? hh : 0.0f;
-                    m[i] = fmaxf(m[i], __builtin_fabsf(hv[i][v]));
+                    hv[j][i][v] = row < nr ? hh : 0.0f;
+                    m[j][i] = fmaxf(m[j][i], __builtin_fabsf(hv[j][i][v]));
                 }
-                m[i] = fmaxf(m[i], __shfl_xor(m[i], 16, 64));
-                m[i] = fmaxf(m[i], __shfl_xor(m[i], 32, 64));
+                m[j][i] = fmaxf(m[j][i], __shfl_xor(m[j][i], 16, 64));
+                m[j][i] = fmaxf(m[j][i], __shfl_xor(m[j][i], 32, 64));
             }
-            // the row maxima of the wave's 16 columns: am_l[w][j * 32 + row]
-            const uint32_t base = lds_addr(&am_l[0][0]) + (uint32_t)(j * kTile + r) * 4u;
-            if (g == 0) es_lds_put2(base + (uint32_t)w * kTG * kTile * 4u, m[0], m[1]);
-            raw_barrier();  // the partner's maxima of tile j
-            float mp[2];
-            es_lds_get2(base + (uint32_t)(w ^ 1) * kTG * kTile * 4u, mp[0], mp[1]);
+        }
+        // the row maxima of the wave's 16 columns: am_l[w][j * 32 + row]
+        const uint32_t base = lds_addr(&am_l[0][0]) + (uint32_t)r * 4u;
+        static_assert(kTG == 2, "two tiles per group");
+        if (g == 0) {
+            es_lds_put2(base + (uint32_t)w * kTG * kTile * 4u, m[0][0], m[0][1]);
+            es_lds_put2(base + (uint32_t)(w * kTG + 1) * kTile * 4u, m[1][0], m[1][1]);
+        }
+        raw_barrier();  // the partner's maxima
+        float mp[kTG][2];
+        es_lds_get2(base + (uint32_t)(w ^ 1) * kTG * kTile * 4u, mp[0][0], mp[0][1]);
+        es_lds_get2(base + (uint32_t)((w ^ 1) * kTG + 1) * kTile * 4u, mp[1][0], mp[1][1]);
+#pragma unroll
+        for (int j = 0; j < kTG; j++) {
+            if (j >= Tc) continue;  // uniform
+            const int slot0 = min(t0c + j, a.slots / kTile - 1) * kTile;
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const int row = 16 * i + r;
                 // the rule of quant_fp8_block32 on the 1x32 block
-                float mm = fmaxf(m[i], mp[i]);
+                float mm = fmaxf(m[j][i], mp[j][i]);
                 if (!(mm >= 1e-4f)) mm = 1e-4f;
                 const int ex = log2_ceil_div448(mm);
                 const float inv = block_inv_scale(ex), sc = e8m0_to_f32((uint32_t)(ex + 127) & 0xFF);
@@ -1362,8 +1375,8 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
                 for (int p = 0; p < 2; p++)
                     hb[p] = __builtin_bit_cast(
                         uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(
-                                      block_byte(hv[i][2 * p], inv) |
-                                          (block_byte(hv[i][2 * p + 1], inv) << 8),
+                                      block_byte(hv[j][i][2 * p], inv) |
+                                          (block_byte(hv[j][i][2 * p + 1], inv) << 8),
                                       sc, false));
                 __builtin_amdgcn_raw_buffer_store_b64(
                     (es_u2){hb[0], hb[1]}, obuf, (uint32_t)((slot0 + row) * a.N + col) * 2u, 0, 0);
