@@ -967,7 +967,7 @@ constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
 constexpr int kMaxGroups = 1024;
 constexpr int kThreads = 512;                 // 8 waves: two per SIMD
 static_assert(kThreads == kGThreads, "the select kernels run both bodies in one workgroup");
-constexpr int kStepLoads = 4 + kTG;           // loads per step and wave: weights + copies
+constexpr int kStepLoads = 2 + kTG;           // loads per step and wave: weights + copies
 constexpr size_t kLds = (size_t)kRing * kSlotB;
 constexpr size_t kLdsAll = kLds + 2 * kMaxGroups * sizeof(int);  // ring + group table
 }  // namespace es
@@ -1022,7 +1022,6 @@ struct EsArgs {
 
 struct EsStep {  // one wave's weight loads of one step: two bands
     u32x4v q[2];
-    uint32_t s[2];
 };
 // two LDS words at a and a + 64 written / read; complete when the statement
 // ends
@@ -1203,9 +1202,6 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
             const int m = MODE == 0 ? h : 0;
             x.q[h] = __builtin_bit_cast(
                 u32x4v, __builtin_amdgcn_raw_buffer_load_b128(wr[m], bo[h] + (uint32_t)s_i * 1024u, 0, 0));
-            // the scale word holding this step's byte (byte s % 4, taken at use)
-            x.s[h] = __builtin_amdgcn_raw_buffer_load_b32(
-                sr[m], so[h] + (uint32_t)(s_i >> 3) * 512u + (uint32_t)(s_i & 4), 0, 0);
         }
         const uint32_t lb = ring + slot * kSlotB + 4 * w * kRowB;
 #pragma unroll
@@ -1251,7 +1247,20 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     v4f acc[kTG][2][2];
     const uint64_t tab = ws_lane_exp2f_tab(lane);
 
-    auto multiply = [&](const EsStep &x, uint32_t sbase) {
+    // The scale bytes of four steps (one per step and lane: a word) sit in
+    // sw[b][band] for the 4-step block b of the 8-step iteration. Block b's
+    // word is loaded at the end of step 4b + 3 of the iteration before (after
+    // that step's multiply, the last read of the old word), five steps before
+    // its first use; the issue side then points two steps into that block.
+    uint32_t sw[2][2];
+    auto load_scales = [&](int b, int back) {
+        const int s0 = max(s_i - back, 0);  // the block's first step (0 past the end)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            sw[b][h] = __builtin_amdgcn_raw_buffer_load_b32(
+                sr[MODE == 0 ? h : 0], so[h] + (uint32_t)(s0 >> 3) * 512u + (uint32_t)(s0 & 4), 0, 0);
+    };
+    auto multiply = [&](const EsStep &x, uint32_t sbase, int u) {
         __asm__ volatile("" : "+s"(sbase));  // opaque: the slot's addresses are formed per step
         if (s_c == 0) {
 #pragma unroll
@@ -1263,7 +1272,7 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 #pragma unroll
         for (int h = 0; h < 2; h++)
             cvt_fp4x32(uint4{x.q[h][0], x.q[h][1], x.q[h][2], x.q[h][3]},
-                       e8m0_to_f32((x.s[h] >> (8 * (s_c & 3))) & 0xFF), bq[h]);
+                       e8m0_to_f32((sw[u >> 2][h] >> (8 * (u & 3))) & 0xFF), bq[h]);
 #pragma unroll
         for (int j = 0; j < kTG; j++) {
             if (j >= Tc) continue;  // uniform
@@ -1386,9 +1395,11 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 
     // ---- the stream, unrolled by the ring (static register slots); NS is a
     // multiple of kRing, so units end on the last step of an iteration. Every
-    // iteration issues one step (past the end a repeat), so when steps q and
-    // q + 1 are waited for, exactly the loads of steps q + 2 .. q + kAhead - 1
-    // are newer.
+    // step issues one step (past the end a repeat), and steps 3 and 7 of an
+    // iteration load a block of scale words, so when steps q and q + 1 are
+    // waited for, the loads of steps q + 2 .. q + kAhead - 1 and the scale
+    // loads at the ends of steps q - 5 .. q - 1 are newer.
+    static_assert(kAhead == 6, "the scale blocks are loaded five steps ahead");
     EsStep st[kRing];
     pre_order(0);
     open_compute();
@@ -1397,18 +1408,21 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         if (s_i == 0) open_issue();
         issue(st[u], u, true);
     }
+    load_scales(0, 6);  // steps 0 .. 3
+    load_scales(1, 2);  // steps 4 .. 7
     auto step = [&](EsStep &x, EsStep &next, int u, int q) {
         if ((u & 1) == 0) {
-            // steps q and q + 1 have landed: at most the loads of the
-            // kAhead - 2 steps issued after them are in flight (a wave holds
-            // at most 63, the counter's range)
-            es_vmcnt<((kAhead - 2) * kStepLoads < 63 ? (kAhead - 2) * kStepLoads : 63)>();
+            // steps q and q + 1 have landed: at most the newer loads are in
+            // flight (four steps, and two or one scale blocks of two words)
+            if ((u & 3) == 0) es_vmcnt<4 * kStepLoads + 4>();
+            else es_vmcnt<4 * kStepLoads + 2>();
             raw_barrier();  // every wave's copies of both steps are in LDS
         }
         const bool real = q + kAhead < total;
         if (real && s_i == 0) open_issue();
         issue(next, (u + kAhead) % kRing, real);
-        multiply(x, ring + u * kSlotB);
+        multiply(x, ring + u * kSlotB, u);
+        if ((u & 3) == 3) load_scales(u >> 2, 2);  // the block five steps on
         s_c++;
     };
     static_assert(kRing == 8 && kAhead <= kRing - 2, "eight ring slots, slot q - 2 the newest reused");
@@ -1433,7 +1447,11 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 #pragma unroll
     for (int u = 0; u < kRing; u++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) __asm__ volatile("" ::"v"(st[u].q[h]), "v"(st[u].s[h]));
+        for (int h = 0; h < 2; h++) __asm__ volatile("" ::"v"(st[u].q[h]));
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) __asm__ volatile("" ::"v"(sw[b][h]));
 }
 
 // One launch per half of the prefill that runs the expert-stationary body
