@@ -953,9 +953,11 @@ __global__ __launch_bounds__(kGThreads) void grouped_down_kernel(DownArgs da) {
 // step q is multiplied, with one workgroup barrier per two steps (at an even
 // step each wave waits for its copies of steps q and q + 1, then the
 // barrier; the ring slot the next issues fill, that of step
-// q + kAhead - kRing <= q - 2, was read before the last barrier). Every step issues the same number of loads (the tiles a group
-// lacks get a 4-byte stand-in copy), so one fixed count (vmcnt) says when a
-// step's copies have landed. Every global access goes through a buffer
+// q + kAhead - kRing <= q - 2, was read before the last barrier). A step
+// issues two weight loads and one copy per tile of its group, and every
+// fourth step a block of scale words; the waves keep the tile counts of the
+// steps in flight, so the count of newer loads (vmcnt) says when a step's
+// copies have landed. Every global access goes through a buffer
 // descriptor sized to its array (out-of-range reads return zeros, writes are
 // dropped). Units go out sorted by group size and dealt to the workgroups in
 // snake order, which evens out the work per workgroup.
@@ -967,7 +969,6 @@ constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
 constexpr int kMaxGroups = 1024;
 constexpr int kThreads = 512;                 // 8 waves: two per SIMD
 static_assert(kThreads == kGThreads, "the select kernels run both bodies in one workgroup");
-constexpr int kStepLoads = 2 + kTG;           // loads per step and wave: weights + copies
 constexpr size_t kLds = (size_t)kRing * kSlotB;
 constexpr size_t kLdsAll = kLds + 2 * kMaxGroups * sizeof(int);  // ring + group table
 }  // namespace es
@@ -988,6 +989,17 @@ __device__ __forceinline__ void es_dma(es_rsrc r, uint32_t off, uint32_t lds, in
 template <int N>
 __device__ __forceinline__ void es_vmcnt() {
     __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// s_waitcnt vmcnt(n) for a wave-uniform run-time n in [LO, HI]
+template <int LO, int HI>
+__device__ __forceinline__ void es_wait_vm(int n) {
+    if constexpr (LO == HI) {
+        es_vmcnt<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n <= MID) es_wait_vm<LO, MID>(n);
+        else es_wait_vm<MID + 1, HI>(n);
+    }
 }
 // An LDS word, complete when the statement ends (no ordinary LDS access, so
 // the compiler does not wait for the stream's direct-to-LDS copies).
@@ -1192,8 +1204,9 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         }
         pre_order(ri_i + 1);
     };
+    int nT[kRing];  // tiles of the step in each ring slot: its copies
     // the loads of the next step of the stream (its unit opened) into
-    // register slot x and ring slot `slot`: kStepLoads per wave. Past the end
+    // register slot x and ring slot `slot`: 2 + Ti per wave. Past the end
     // of the stream (real == false) the last step's loads are repeated and
     // not used, so that every step has the same loads in flight after it.
     auto issue = [&](EsStep &x, int slot, bool real) {
@@ -1206,8 +1219,9 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         const uint32_t lb = ring + slot * kSlotB + 4 * w * kRowB;
 #pragma unroll
         for (int j = 0; j < kTG; j++)
-            es_dma(abuf, ao[j] + (uint32_t)s_i * kRowB,  // tiles >= Ti: a valid row
-                   lb + j * kTile * kRowB, j < Ti ? 16 : 4);
+            if (j < Ti)  // uniform: the tiles the group has
+                es_dma(abuf, ao[j] + (uint32_t)s_i * kRowB, lb + j * kTile * kRowB, 16);
+        nT[slot] = Ti;
         if (real && ++s_i == NS) {
             s_i = 0;
             ri_i++;
@@ -1413,9 +1427,11 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     auto step = [&](EsStep &x, EsStep &next, int u, int q) {
         if ((u & 1) == 0) {
             // steps q and q + 1 have landed: at most the newer loads are in
-            // flight (four steps, and two or one scale blocks of two words)
-            if ((u & 3) == 0) es_vmcnt<4 * kStepLoads + 4>();
-            else es_vmcnt<4 * kStepLoads + 2>();
+            // flight (four steps of 2 + T loads, and two or one scale blocks
+            // of two words)
+            const int n = 8 + nT[(u + 2) % kRing] + nT[(u + 3) % kRing] + nT[(u + 4) % kRing] +
+                          nT[(u + 5) % kRing] + ((u & 3) == 0 ? 4 : 2);
+            es_wait_vm<8 + 4 + 2, 8 + 4 * kTG + 4>(n);
             raw_barrier();  // every wave's copies of both steps are in LDS
         }
         const bool real = q + kAhead < total;
