@@ -109,6 +109,8 @@ def _host_experts(slabs, experts, E, dim, inter):
 
 @pytest.mark.parametrize("m,E,dim,inter,k,check", [(40, 64, 1024, 512, 6, 40),
                                                     (132, 384, 4096, 2048, 8, 6),
+                                                    # few tiles: the tile-streaming pair
+                                                    (8, 384, 4096, 2048, 8, 8),
                                                     (5, 16, 512, 256, 4, 5),
                                                     (96, 64, 5120, 2304, 6, 6),
                                                     (33, 8, 8192, 4096, 2, 4),
@@ -132,6 +134,9 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
                      device=DEV)
     y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
     L.moe_prefill(dev(x), idx, w, *_packed(slabs, E, dim, inter), y, m, dim, inter, E, k, ws)
+    want_choice = _stationary_expected(idx, E, dim, inter)
+    if want_choice is not None:
+        assert _stationary_choice(ws, m, dim, k, E) == want_choice
     gi, gw, gy = host(idx), host(w), host(y)
     rows = np.linspace(0, m - 1, check).astype(int)
     H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
@@ -162,6 +167,22 @@ def _fp4_normal_slab(gen, E, rows, cols, chunk=64):
 
 def _a256(v):
     return (v + 255) // 256 * 256
+
+
+def _stationary_expected(idx, E, dim, inter):
+    """The choice the dispatch should make (None where the stationary
+    bodies do not serve the shape): with t_e = ceil(routes of expert e / 32)
+    tiles, nt = sum t_e and ng = sum ceil(t_e / 2) groups, the stationary
+    bodies when 6 (nt - ng) >= nt or nt >= 96."""
+    cnt = np.bincount(host(idx).ravel(), minlength=E)
+    t = (cnt + 31) // 32
+    nt, ng = int(t.sum()), int(((t + 1) // 2).sum())
+    tiles = L.moe_tiles(host(idx).size, E)
+    fits = (dim % 256 == 0 and (dim // 128) % 8 == 0 and (inter // 128) % 8 == 0 and
+            tiles <= 1024)
+    if not fits:
+        return None
+    return 1 if (6 * (nt - ng) >= nt or nt >= 96) else 0
 
 
 def _stationary_choice(ws, m, dim, k, E):
@@ -201,9 +222,10 @@ def test_config4_baseline_weights_prefill_matches_oracle(zipf):
     y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
     P = _packed(slabs, E, dim, inter)
     L.moe_prefill(dev(x), idx, w, *P, y, m, dim, inter, E, k, ws)
-    # the skewed draw runs the expert-stationary bodies, the mild one the
-    # tile-streaming pair: both are checked here
-    assert _stationary_choice(ws, m, dim, k, E) == (1 if zipf > 1 else 0)
+    # both draws run the expert-stationary bodies (the skewed one for its
+    # shared groups, the mild one for its tile count)
+    assert _stationary_expected(idx, E, dim, inter) == 1
+    assert _stationary_choice(ws, m, dim, k, E) == 1
     gi, gw, gy = host(idx), host(w), host(y)
     H = _host_experts(slabs, gi.ravel(), E, dim, inter)
     staged = None

@@ -32,11 +32,14 @@ constexpr int kDispHeld = 4;  // route chunks the dispatch keeps in registers
 constexpr int kEsGroup = 2;   // tiles of one expert whose weights the stationary body streams once
 
 // The expert-stationary body streams a group's weights once for its (up to
-// kEsGroup) tiles; it pays when at least a sixth of the nt tiles share a group
-// with another (ng groups; skewed routing: measured 247 against 258 us at
-// M=132 under Zipf(1.1)). With (nearly) one tile per expert the
-// tile-streaming body is faster.
-__host__ __device__ constexpr bool es_pays(int nt, int ng) { return 6 * (nt - ng) >= nt; }
+// kEsGroup) tiles. It is taken when at least a sixth of the nt tiles share a
+// group with another (ng groups; skewed routing), or when there are at least
+// 96 tiles: measured with 384 experts (dim 4096, inter 2048) at M=132 and
+// Zipf(0.25) (237-248 tiles) 620 against 670 us, at M=64 (~140 tiles) 383
+// against 416 us; at M=8 (~51 tiles, one per expert) the two are even.
+__host__ __device__ constexpr bool es_pays(int nt, int ng) {
+    return 6 * (nt - ng) >= nt || nt >= 96;
+}
 
 // ---- dispatch (one workgroup) -------------------------------------------
 // An expert id as the dispatch sees it: ids outside [0, E) (a pick another
