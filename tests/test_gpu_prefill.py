@@ -111,6 +111,10 @@ def _host_experts(slabs, experts, E, dim, inter):
                                                     (132, 384, 4096, 2048, 8, 6),
                                                     # few tiles: the tile-streaming pair
                                                     (8, 384, 4096, 2048, 8, 8),
+                                                    # the expert-stationary pair at other
+                                                    # shapes (K of one ring round: 1024)
+                                                    (128, 16, 2048, 1024, 4, 8),
+                                                    (200, 32, 1024, 1024, 6, 8),
                                                     (5, 16, 512, 256, 4, 5),
                                                     (96, 64, 5120, 2304, 6, 6),
                                                     (33, 8, 8192, 4096, 2, 4),
@@ -136,7 +140,10 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
     L.moe_prefill(dev(x), idx, w, *_packed(slabs, E, dim, inter), y, m, dim, inter, E, k, ws)
     want_choice = _stationary_expected(idx, E, dim, inter)
     if want_choice is not None:
-        assert _stationary_choice(ws, m, dim, k, E) == want_choice
+        got = _stationary_choice(ws, m, dim, k, E)
+        print("[moe_prefill m=%d E=%d dim=%d inter=%d] %s bodies" %
+              (m, E, dim, inter, "expert-stationary" if got else "tile-streaming"), flush=True)
+        assert got == want_choice
     gi, gw, gy = host(idx), host(w), host(y)
     rows = np.linspace(0, m - 1, check).astype(int)
     H = _host_experts(slabs, gi[rows].ravel(), E, dim, inter)
