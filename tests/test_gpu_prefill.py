@@ -115,6 +115,7 @@ def _host_experts(slabs, experts, E, dim, inter):
                                                     # shapes (K of one ring round: 1024)
                                                     (128, 16, 2048, 1024, 4, 8),
                                                     (200, 32, 1024, 1024, 6, 8),
+                                                    (400, 16, 8192, 4096, 2, 4),
                                                     (5, 16, 512, 256, 4, 5),
                                                     (96, 64, 5120, 2304, 6, 6),
                                                     (33, 8, 8192, 4096, 2, 4),
