@@ -968,7 +968,7 @@ namespace es {
 constexpr int kTG = kEsGroup;                 // tiles per group
 constexpr int kRing = 8;                      // ring slots (LDS and registers), one 128-K step each
 constexpr int kRowB = 256;                    // bytes of one A row per step (128 bf16)
-constexpr int kSlotB = kTG * kTile * kRowB;   // 32 KB per ring slot
+constexpr int kSlotB = kTG * kTile * kRowB;   // 16 KB per ring slot
 constexpr int kMaxGroups = 1024;
 constexpr int kThreads = 512;                 // 8 waves: two per SIMD
 static_assert(kThreads == kGThreads, "the select kernels run both bodies in one workgroup");
