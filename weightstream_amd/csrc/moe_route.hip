@@ -17,6 +17,9 @@
 // sqrtsoftplus uses ws_logf and sqrtf: ws_logf equals glibc logf on every
 // input (ws_logf.h), sqrtf is correctly rounded, so the scores are the CPU's
 // bits.
+#include <type_traits>
+#include <utility>
+
 #include "ws_internal.hpp"
 #include "ws_route.hpp"
 #include "ws_gate.hpp"
@@ -83,13 +86,39 @@ __global__ __launch_bounds__(64) void gate_logits_kernel(const float *__restrict
 // of kGC-element chunks by direct global->LDS loads, kGS-1 chunks ahead of the
 // chains, which read them back from LDS: the sequential adds never wait on
 // global memory. Small blocks (4 experts for one token) spread the weight
-// stream over many CUs. Rows keep their 16-byte pieces permuted by the row
-// index so that rows read at one position fall on distinct banks.
+// stream over many CUs. Rows of 1 KB (tokens, f32 weights) sit 1040 bytes
+// apart in a stage, so rows read at one position fall on distinct banks and
+// every read is the row's base plus a constant (no address arithmetic in the
+// chains' loop); bf16 weight rows (512 bytes, two per direct load) keep their
+// 16-byte pieces permuted by the row index instead.
+template <int TE, int TM, bool BF16>
+struct PipeGeom {
+    using G = GateGeom<TE, TM, BF16>;
+    static_assert(G::kXRow == 1024, "one token row chunk per direct load");
+    static constexpr int kXP = G::kXRow + 16;                  // token row pitch
+    static constexpr int kWP = BF16 ? G::kWRow : G::kWRow + 16;  // weight row pitch
+    static constexpr int kXs = TM * kXP;
+    static constexpr int kStage = kXs + TE * kWP;
+};
+
+template <int OFF>
+__device__ __forceinline__ u32x4v lds_read_b128_at(uint32_t a) {
+    u32x4v v;
+    __asm__ volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "n"(OFF));
+    return v;
+}
+
+template <class F, int... I>
+__device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
 template <int TE, int TM, bool BF16>
 __global__ __launch_bounds__(64) void gate_logits_pipe_kernel(const float *x, const void *gw,
                                                               float *__restrict__ logits,
                                                               int m_rows, int dim, int n_experts) {
     using G = GateGeom<TE, TM, BF16>;
+    using P = PipeGeom<TE, TM, BF16>;
     extern __shared__ __align__(16) uint8_t g_lds[];
     const int lane = threadIdx.x;
     const int e0 = blockIdx.x * TE, m0 = blockIdx.y * TM;
@@ -97,34 +126,61 @@ __global__ __launch_bounds__(64) void gate_logits_pipe_kernel(const float *x, co
     constexpr int kEB = BF16 ? 2 : 4;
 
     // a lane's direct-load sources: fixed rows, the chunk offset moves
+    // direct load j: token row j, f32 weight row j - TM, or bf16 weight rows
+    // 2 (j - TM) and 2 (j - TM) + 1; its LDS offset in the stage is dst(j)
     const uint8_t *src[G::kLoads];
 #pragma unroll
     for (int j = 0; j < G::kLoads; j++) {
         const int o = j * 1024 + lane * 16;
         if (o < G::kX) {
-            const int row = o / G::kXRow, c = (o % G::kXRow) / 16;
-            src[j] = (const uint8_t *)(x + (size_t)min(m0 + row, m_rows - 1) * dim) +
-                     (c ^ (row & 15)) * 16;
+            src[j] = (const uint8_t *)(x + (size_t)min(m0 + j, m_rows - 1) * dim) + lane * 16;
         } else {
             const int oo = o - G::kX;
             const int row = oo / G::kWRow, c = (oo % G::kWRow) / 16;
             src[j] = (const uint8_t *)gw + (size_t)min(e0 + row, n_experts - 1) * dim * kEB +
-                     (c ^ (row & 15)) * 16;
+                     (BF16 ? (c ^ (row & 15)) : c) * 16;
         }
     }
+    auto dst = [](int j) {
+        return j * 1024 < G::kX ? j * P::kXP
+                                : P::kXs + (BF16 ? (j * 1024 - G::kX) : (j - TM) * P::kWP);
+    };
     auto issue = [&](int buf, int chunk) {
-        uint8_t *base = g_lds + buf * G::kStage;
+        uint8_t *base = g_lds + buf * P::kStage;
 #pragma unroll
         for (int j = 0; j < G::kLoads; j++) {
             const int off = j * 1024 < G::kX ? chunk * G::kXRow : chunk * G::kWRow;
             __builtin_amdgcn_global_load_lds(
                 (const void *)(src[j] + off),
-                (__attribute__((address_space(3))) void *)(base + j * 1024), 16, 0, 0);
+                (__attribute__((address_space(3))) void *)(base + dst(j)), 16, 0, 0);
         }
     };
 
     const int tm = min(lane / TE, TM - 1), te = lane % TE;
     float s = 0.0f;
+    // 16 elements at a time (a group): 4 pieces of the token row and 4
+    // (f32) or 2 (bf16) of the weight row; the next group's reads are issued
+    // before a group's adds, so LDS latency overlaps the chain
+    constexpr int kWP = BF16 ? 2 : 4;        // weight pieces per group
+    constexpr int kRd = 4 + kWP;             // LDS reads per group
+    constexpr int kNG = kGC / 16;            // groups per chunk
+    auto reads = [&](auto gc, uint32_t xb, uint32_t wb, u32x4v *xr, u32x4v *wr) {
+        constexpr int grp = decltype(gc)::value;
+        xr[0] = lds_read_b128_at<(grp * 4 + 0) * 16>(xb);
+        xr[1] = lds_read_b128_at<(grp * 4 + 1) * 16>(xb);
+        xr[2] = lds_read_b128_at<(grp * 4 + 2) * 16>(xb);
+        xr[3] = lds_read_b128_at<(grp * 4 + 3) * 16>(xb);
+        if constexpr (BF16) {
+#pragma unroll
+            for (int k = 0; k < kWP; k++)
+                wr[k] = lds_read_b128(wb + ((grp * kWP + k) ^ (te & 15)) * 16);
+        } else {
+            wr[0] = lds_read_b128_at<(grp * 4 + 0) * 16>(wb);
+            wr[1] = lds_read_b128_at<(grp * 4 + 1) * 16>(wb);
+            wr[2] = lds_read_b128_at<(grp * 4 + 2) * 16>(wb);
+            wr[3] = lds_read_b128_at<(grp * 4 + 3) * 16>(wb);
+        }
+    };
 #pragma unroll
     for (int p = 0; p < kGS - 1; p++)
         if (p < nc) issue(p, p);
@@ -133,26 +189,15 @@ __global__ __launch_bounds__(64) void gate_logits_pipe_kernel(const float *x, co
         wait_newer<G::kLoads, kGS - 2>(min(nc - 1 - i, kGS - 2));
         raw_barrier();  // chunk i is in LDS; chunk i-1's buffer is free
         if (i + kGS - 1 < nc) issue((i + kGS - 1) % kGS, i + kGS - 1);
-        const uint32_t xb = lds_addr(g_lds) + (i % kGS) * G::kStage + tm * G::kXRow;
-        const uint32_t wb = lds_addr(g_lds) + (i % kGS) * G::kStage + G::kX + te * G::kWRow;
-        // 16 elements at a time: 4 pieces of the token row and 4 (f32) or 2
-        // (bf16) of the weight row; the next group's reads are issued before
-        // this group's adds, so LDS latency overlaps the chain
-        constexpr int kWP = BF16 ? 2 : 4;        // weight pieces per group
-        constexpr int kRd = 4 + kWP;             // LDS reads per group
+        const uint32_t xb = lds_addr(g_lds) + (i % kGS) * P::kStage + tm * P::kXP;
+        const uint32_t wb = lds_addr(g_lds) + (i % kGS) * P::kStage + P::kXs + te * P::kWP;
         u32x4v xv[2][4], wv[2][4];
-        auto reads = [&](int grp, u32x4v *xr, u32x4v *wr) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) xr[k] = lds_read_b128(xb + ((grp * 4 + k) ^ (tm & 15)) * 16);
-#pragma unroll
-            for (int k = 0; k < kWP; k++) wr[k] = lds_read_b128(wb + ((grp * kWP + k) ^ (te & 15)) * 16);
-        };
-        reads(0, xv[0], wv[0]);
-#pragma unroll
-        for (int grp = 0; grp < kGC / 16; grp++) {
-            const int cur = grp & 1;
-            if (grp + 1 < kGC / 16) {
-                reads(grp + 1, xv[cur ^ 1], wv[cur ^ 1]);
+        reads(std::integral_constant<int, 0>{}, xb, wb, xv[0], wv[0]);
+        unroll_seq([&](auto gc) {
+            constexpr int grp = decltype(gc)::value;
+            constexpr int cur = grp & 1;
+            if constexpr (grp + 1 < kNG) {
+                reads(std::integral_constant<int, grp + 1>{}, xb, wb, xv[cur ^ 1], wv[cur ^ 1]);
                 lds_wait<kRd>();
             } else {
                 lds_wait<0>();
@@ -177,7 +222,7 @@ __global__ __launch_bounds__(64) void gate_logits_pipe_kernel(const float *x, co
             }
 #pragma unroll
             for (int j = 0; j < 16; j++) s = s + pr[j];
-        }
+        }, std::make_integer_sequence<int, kNG>{});
     }
     if (lane < TE * TM && m0 + tm < m_rows && e0 + te < n_experts)
         logits[(size_t)(m0 + tm) * n_experts + e0 + te] = s;
@@ -189,11 +234,11 @@ static void gate_pipe_launch(const float *x, const void *gw, int bf16, float *lo
     dim3 g((unsigned)((n_experts + TE - 1) / TE), (unsigned)((m + TM - 1) / TM));
     if (bf16)
         hipLaunchKernelGGL((gate_logits_pipe_kernel<TE, TM, true>), g, dim3(64),
-                           (kGS * GateGeom<TE, TM, true>::kStage), stream, x, gw, logits, (int)m,
+                           (kGS * PipeGeom<TE, TM, true>::kStage), stream, x, gw, logits, (int)m,
                            (int)dim, (int)n_experts);
     else
         hipLaunchKernelGGL((gate_logits_pipe_kernel<TE, TM, false>), g, dim3(64),
-                           (kGS * GateGeom<TE, TM, false>::kStage), stream, x, gw, logits, (int)m,
+                           (kGS * PipeGeom<TE, TM, false>::kStage), stream, x, gw, logits, (int)m,
                            (int)dim, (int)n_experts);
 }
 
