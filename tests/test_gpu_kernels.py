@@ -371,7 +371,7 @@ def test_workspace_registered_under_one_mode_serves_both():
     GEMM on a stream whose workspace was set while EXACT was active takes the
     split-K path (it writes partials into the workspace) and gives the bits
     of the same NATIVE GEMM registered under NATIVE."""
-    m, n, k = 128, 8192, 2048     # the split-K pipeline's shape (no line tiling)
+    m, n, k = 128, 8192, 2304     # the split-K pipeline's shape (K not a multiple of 512)
     gen = torch.Generator(device=DEV).manual_seed(77)
     x = torch.randn((m, k), device=DEV, generator=gen)
     aq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
@@ -405,14 +405,20 @@ def test_workspace_registered_under_one_mode_serves_both():
 
 @pytest.mark.parametrize("m,n,k", [(100, 4096, 4096), (65, 3072, 2048), (128, 5120, 1024),
                                    (127, 3104, 4096), (100, 2048, 4096), (40, 4096, 2048),
-                                   (120, 12288, 4096), (128, 9216, 768)])
+                                   (120, 12288, 4096), (128, 9216, 768),
+                                   # K > 4096, N > 4096 or few tiles
+                                   (64, 4096, 8192), (96, 5120, 5120), (24, 2048, 4096),
+                                   (64, 12288, 4096), (128, 1280, 8192)])
 @pytest.mark.parametrize("native", [False, True])
 def test_line_gemm_ragged_rows_vs_fp64_dequant(m, n, k, native):
     """The line kernel (K a multiple of 512): 64 x 32 tiles for M in 65-128
     with 192-384 workgroups, 32 x 32 tiles for 32-row blocks (n = 2048 at
     M = 100; M = 40), 128 x 48 tiles for wide N (12288; 9216 at K = 768,
     three 256-K stages); ragged last row blocks, the XCD-paired tile order and
-    (n = 3104: 194 workgroups) the plain order, UE8M0 and f32 scales, f32
+    (n = 3104: 194 workgroups) the plain order; the other shapes it stages
+    (K > 4096, N > 4096, few tiles: 32 x 32 tiles when they fit one round of
+    workgroups, else 64 x 32; at most 32 rows, 32 x 32 with 64 or more
+    tiles), UE8M0 and f32 scales, f32
     and bf16 outputs, against an f64 matmul of the dequantised operands.
     EXACT within 1e-3; NATIVE within its own 5e-2 (tests/test_gpu_native.py)."""
     gen = torch.Generator(device=DEV)

@@ -1216,7 +1216,29 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
                 rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 4);
         }
         if (rc >= 0) return rc;
-        // 3. M > 64: the pipelined split-K kernel (128-row tiles)
+        // 3. the line kernel at the other shapes it stages (K a multiple of
+        // 512; K > 4096, N > 4096 or few tiles): 32 x 32 tiles when they fit
+        // one round of workgroups, else 64 x 32. Cold weights, against the
+        // kernels below with a split-K workspace registered: M=64 all engine
+        // projection shapes faster (N=25600, K=5120 86.6 -> 57.8 us; N=5120,
+        // K=2048 15.6 -> 8.5; N=4096, K=8192 19.8 -> 14.9); M=128 faster with
+        // one round of tiles or K <= 4096 (N=512, K=5120 17.3 -> 9.7; N=8192,
+        // K=2048 23.0 -> 15.6), slower otherwise (N=4608, K=5120 23.0 ->
+        // 28.4; N=1280, K=15360 21.7 -> 23.6), so those keep the split-K
+        // pipeline. At 32 rows only the 32 x 32 tiles, with 64 or more.
+        if (!BFP4 && M > 16 && M <= 128 && N % 32 == 0 && K % 512 == 0) {
+            const long cus = cu_count();
+            const long w2 = (long)((M + 31) / 32) * (N / 32);  // 32 x 32 tiles
+            const long w0 = (long)((M + 63) / 64) * (N / 32);  // 64 x 32 tiles
+            int lc = -1;
+            if (M <= 32) lc = w2 >= 64 ? 2 : -1;
+            else lc = w2 <= cus ? 2 : 0;
+            if (M > 64 && lc >= 0 && (K > 8192 || ((lc == 2 ? w2 : w0) > cus && K > 4096)))
+                lc = -1;
+            if (lc >= 0) rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, lc);
+        }
+        if (rc >= 0) return rc;
+        // 4. M > 64: the pipelined split-K kernel (128-row tiles)
         if (M > 64) {
             const int bn = pipe_bn(M, N);
             rc = bn == 256   ? launch_pipe<256, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp)
@@ -1224,7 +1246,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
                              : launch_pipe<64, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp);
         }
         if (rc >= 0) return rc;
-        // 4. 16-column strips (no split-K workspace, or shapes the others
+        // 5. 16-column strips (no split-K workspace, or shapes the others
         // do not stage)
         if (M <= 16) {
             const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
