@@ -536,7 +536,6 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
         h = torch.empty_like(h0)
         aq = torch.empty((M, OD), dtype=torch.uint8, device=dev)
         asc = torch.empty((M, OD // 32), dtype=torch.uint8, device=dev)
-        o = torch.empty((M, DIM), dtype=torch.float32, device=dev)
         logits = torch.empty((M, E), dtype=torch.float32, device=dev)
         idx = torch.empty((layers, M, TOPK), dtype=torch.int32, device=dev)
         wts = torch.empty((layers, M, TOPK), dtype=torch.float32, device=dev)
@@ -557,9 +556,9 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
                 if M == 1:  # emit8 + fp8_gemm + acc_f32 in one launch (same bits)
                     L.fp8_gemv_acc(attn[li], *w["wo"], h, M, DIM, OD, stream=st)
                 else:
+                    # emit8, then fp8_gemm + acc_f32 in one launch (same bits)
                     L.emit8(attn[li], aq, asc, M * OD, stream=st)
-                    L.fp8_gemm(aq, asc, *w["wo"], o, M, DIM, OD, stream=st)
-                    L.acc_f32(o, h, M * DIM, stream=st)
+                    L.fp8_gemm_acc(aq, asc, *w["wo"], h, M, DIM, OD, stream=st)
                 if M == 1:  # gate logits and the shared gate/up + SwiGLU in one launch
                     L.moe_gate_shared_w13(h, w["gate"], logits, *w["shared"][:2], hsf, M, DIM, E,
                                           SI, stream=st)

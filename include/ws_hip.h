@@ -127,6 +127,17 @@ int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream);
  * B e4m3 + sb[ceil(N/32),K/32], C f32 [M,N]. */
 int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                 float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
+/* No single reference counterpart: launch.rs:717-742 fp8_gemm (the
+ * engine's gemm_q8 of wo_b, engine.rs:4008-4017) followed by launch.rs:1175
+ * acc_f32 into the residual, in one launch: c += A.B^T with the add in the
+ * GEMM's epilogue (c[i] + sum). Same operands as ws_fp8_gemm. It runs the
+ * line and column-strip kernels only, never split over K: its bits are
+ * those of ws_fp8_gemm + ws_acc_f32 wherever ws_fp8_gemm runs those too
+ * (m <= 64, or K a multiple of 512 with m <= 128 and one round of tiles;
+ * not where it splits K over a registered workspace or runs the split-K
+ * pipeline's single pass). */
+int ws_fp8_gemm_acc(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                    float *c, int64_t m, int64_t n, int64_t k, ws_stream_t stream);
 /* launch.rs:744-767 fp8_gemm_tile (fp8_gemm_tile.cu:28): same contract. */
 int ws_fp8_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                      float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream);

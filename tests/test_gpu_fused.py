@@ -2,6 +2,7 @@
 replace, bit for bit (both are the same FP8 GEMV sums, in the same order):
 
   ws_fp8_gemv_acc              == emit8 -> fp8_gemm -> acc_f32 (launch.rs:1175)
+  ws_fp8_gemm_acc              == fp8_gemm -> acc_f32
   ws_shared_expert_fp8_w13_acc == ws_shared_expert_fp8_w13 -> acc_f32(ys, yr)
                                   -> acc_f32(yr, h)   (engine.rs:4532)
   ws_moe_gate_shared_w13 + ws_shared_expert_down_acc
@@ -68,7 +69,33 @@ def test_gemv_acc_bit_exact(mode, m, n, k):
     assert torch.equal(got.view(torch.int32), want.view(torch.int32))
 
 
-@pytest.mark.parametrize("m,limit", [(1, 10.0), (1, 0.0), (8, 10.0), (16, 10.0), (20, 10.0)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 4096), (8, 4096, 8192), (20, 512, 1024),
+                                   (64, 4096, 8192), (64, 12288, 4096), (48, 2048, 2304),
+                                   (128, 4096, 4096), (128, 2048, 4096)])
+def test_gemm_acc_bit_exact(mode, m, n, k):
+    """ws_fp8_gemm_acc == emit8 -> fp8_gemm -> acc_f32 on the shapes where
+    both run the same kernel (no split-K workspace registered): column strips
+    (m <= 64), the line kernel (32 x 32 and 64 x 32 tiles)."""
+    announce("fp8_gemm_acc mode=%d m=%d n=%d k=%d" % (mode, m, n, k))
+    gen = torch.Generator(device=DEV).manual_seed(m * 5 + n + k)
+    w, sw = _fp8(gen, n, k)
+    x = _x(gen, m, k)
+    h0 = torch.randn((m, n), device=DEV, generator=gen)
+    xq = torch.empty((m, k), dtype=torch.uint8, device=DEV)
+    xs = torch.empty((m, k // 32), dtype=torch.uint8, device=DEV)
+    L.emit8(x, xq, xs, m * k)
+    o = torch.empty((m, n), device=DEV)
+    want = h0.clone()
+    L.fp8_gemm(xq, xs, w, sw, o, m, n, k)
+    L.acc_f32(o, want, m * n)
+    got = h0.clone()
+    L.fp8_gemm_acc(xq, xs, w, sw, got, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), want.view(torch.int32))
+
+
+@pytest.mark.parametrize("m,limit", [(1, 10.0), (1, 0.0), (8, 10.0), (16, 10.0), (20, 10.0),
+                                     (64, 10.0), (64, 0.0)])
 def test_shared_w13_acc_bit_exact(mode, m, limit):
     dim, inter = 4096, 2048
     announce("shared_expert_fp8_w13_acc mode=%d m=%d limit=%g" % (mode, m, limit))

@@ -64,6 +64,7 @@ SIGNATURES = {
     "ws_gemm_workspace_size": (C.c_size_t, [_i64, _i64, _i64]),
     "ws_set_gemm_workspace": (_i, [_p, C.c_size_t, _p]),
     "ws_fp8_gemm": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "ws_fp8_gemm_acc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_tile": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_bf16": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "ws_fp8_gemm_f32s": (_i, [_p, _p, _p, _p, _p, _i, _i64, _i64, _i64, _p]),

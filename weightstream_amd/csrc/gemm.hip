@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float *__restri
 template <int MF, int NF, int GMH, int GK, bool BFP4, int SMODE, int OMODE, int U>
 static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
                      int m, int n, int k, hipStream_t stream, int S = 1, float *part = nullptr,
-                     int sb_div = 32) {
+                     int sb_div = 32, const float *aux = nullptr) {
     constexpr int rows = 16 * MF * GMH, threads = 64 * GMH * GK;
     if (n % (16 * NF)) return -1;
     const int ksteps = k / 128;
@@ -302,15 +302,16 @@ static int launch_kp(const uint8_t *a, const void *sa, const uint8_t *b, const v
     const size_t lds = kp_head_bytes<MF, NF, GMH, GK, alds>() + (size_t)ksteps * rows * 4;
     if (lds > 160 * 1024) return -1;
     if (S < 1 || (S > 1 && !part)) return -1;
+    if (S > 1 && (OMODE == kOutAcc || OMODE == kOutAcc2)) return -1;  // the reduction writes
     dim3 grid((unsigned)(n / (16 * NF)), (unsigned)((m + rows - 1) / rows), (unsigned)S);
     if (math_mode() == WS_MATH_NATIVE)
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, false, false, alds>),
                            grid, dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
-                           sb_div, nullptr, 0.0f, 16);
+                           sb_div, aux, 0.0f, 16);
     else
         hipLaunchKernelGGL((gemm_kp_kernel<MF, NF, GMH, GK, BFP4, SMODE, OMODE, U, true, false, alds>),
                            grid, dim3(threads), lds, stream, a, sa, b, sb, out, m, n, k, S, part,
-                           sb_div, nullptr, 0.0f, 16);
+                           sb_div, aux, 0.0f, 16);
     int rc = launch_status();
     if (rc || S == 1) return rc;
     const int64_t mn = (int64_t)m * n;
@@ -1136,9 +1137,13 @@ static int forced_cfg() {
 }
 
 template <bool BFP4, int SMODE, int OMODE>
+// OMODE kOutAcc (C += A.B^T) and kOutAcc2 (C = C + (aux + A.B^T)) run on the
+// kernels with those epilogues (line, column strips), never split over K.
 static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb,
                          void *out, int64_t m, int64_t n, int64_t k, hipStream_t stream,
-                         int sb_div = 32) {
+                         int sb_div = 32, const float *aux = nullptr) {
+    constexpr bool kAccOut = OMODE == kOutAcc || OMODE == kOutAcc2;
+    if (OMODE == kOutAcc2 && !aux) return WS_ERR_INVALID_ARG;
     if (!a || !sa || !b || !sb || !out) return WS_ERR_INVALID_ARG;
     if (m <= 0 || n <= 0 || k <= 0) return WS_ERR_INVALID_ARG;
     if (k % 128 || n % 16 || m > (1 << 24) || n > (1 << 24) || k > (1 << 24)) return WS_ERR_SHAPE;
@@ -1151,22 +1156,22 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         // column-strip kernel only
         int rc;
         if (M <= 16) {
-            const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
+            const int S = kAccOut ? 1 : strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
             rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, S,
-                                                               (float *)wsp.ptr, sb_div);
+                                                               (float *)wsp.ptr, sb_div, aux);
         } else if (M <= 32) {
             rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
-                                                               nullptr, sb_div);
+                                                               nullptr, sb_div, aux);
         } else if (M <= 64) {
             rc = launch_kp<4, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
-                                                               nullptr, sb_div);
+                                                               nullptr, sb_div, aux);
         } else {
             rc = launch_kp<4, 1, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1,
-                                                               nullptr, sb_div);
+                                                               nullptr, sb_div, aux);
         }
         return rc < 0 ? WS_ERR_SHAPE : rc;
     }
-    int cfg = forced_cfg();
+    int cfg = kAccOut ? -1 : forced_cfg();
     if (cfg < 0) {
         int rc = -1;
         static const int line_knob = [] {  // measurement knob: force a line-kernel tiling
@@ -1174,7 +1179,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
             return e ? atoi(e) : -1;
         }();
         if (!BFP4 && line_knob >= 0 && M > 16) {
-            rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, line_knob);
+            rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, line_knob, aux);
             if (rc >= 0) return rc;
         }
         // 1. 32-column strips when they give the chip one round of workgroups:
@@ -1192,18 +1197,21 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
                 // 512 K, XCD-paired row blocks) when K allows its stages;
                 // measured at M=128, N=4096, K=4096: 13.8 against 16.6 us
                 if (!BFP4 && K % 512 == 0 && M > 64)
-                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 0);
+                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 0, aux);
                 if (rc < 0)
-                    rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+                    rc = launch_kp<4, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream,
+                                                                       1, nullptr, 32, aux);
             } else if (wg32 * 4 >= cus * 3 && wg32 * 2 <= cus * 3) {
                 // 32-row blocks: the line kernel with 32 x 32 tiles (M=128,
                 // N=2048, K=4096: 9.95 against 10.9 us for the A-resident
                 // kernel), else the A-resident kernel (K <= 4096), else kp
                 if (!BFP4 && K % 512 == 0)
-                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 2);
-                if (!BFP4 && rc < 0) rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
+                    rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 2, aux);
+                if (!BFP4 && !kAccOut && rc < 0)
+                    rc = launch_al<2, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream);
                 if (rc < 0)
-                    rc = launch_kp<2, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+                    rc = launch_kp<2, 2, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream,
+                                                                       1, nullptr, 32, aux);
             }
         }
         if (rc >= 0) return rc;
@@ -1213,7 +1221,7 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         if (!BFP4 && M > 64 && M <= 128 && N % 48 == 0 && K % 256 == 0) {
             const long wg = N / 48, cus = cu_count();
             if (wg * 4 >= cus * 3 && wg * 2 <= cus * 3)
-                rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 4);
+                rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, 4, aux);
         }
         if (rc >= 0) return rc;
         // 3. the line kernel at the other shapes it stages (K a multiple of
@@ -1235,11 +1243,11 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
             else lc = w2 <= cus ? 2 : 0;
             if (M > 64 && lc >= 0 && (K > 8192 || ((lc == 2 ? w2 : w0) > cus && K > 4096)))
                 lc = -1;
-            if (lc >= 0) rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, lc);
+            if (lc >= 0) rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, lc, aux);
         }
         if (rc >= 0) return rc;
         // 4. M > 64: the pipelined split-K kernel (128-row tiles)
-        if (M > 64) {
+        if (M > 64 && !kAccOut) {
             const int bn = pipe_bn(M, N);
             rc = bn == 256   ? launch_pipe<256, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp)
                  : bn == 128 ? launch_pipe<128, BFP4, SMODE, OMODE>(a, sa, b, sb, out, M, N, K, stream, wsp)
@@ -1249,14 +1257,15 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         // 5. 16-column strips (no split-K workspace, or shapes the others
         // do not stage)
         if (M <= 16) {
-            const int S = strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
+            const int S = kAccOut ? 1 : strip_splits(M, N, K, wsp.ptr ? wsp.bytes : 0);
             rc = launch_kp<1, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, S,
-                                                               (float *)wsp.ptr);
+                                                               (float *)wsp.ptr, 32, aux);
         }
-        else if (M <= 32) rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-        else if (M <= 64) rc = launch_kp<4, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
-        else rc = launch_kp<4, 1, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream);
+        else if (M <= 32) rc = launch_kp<2, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1, nullptr, 32, aux);
+        else if (M <= 64) rc = launch_kp<4, 1, 1, 8, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1, nullptr, 32, aux);
+        else rc = launch_kp<4, 1, 2, 4, BFP4, SMODE, OMODE, 1>(a, sa, b, sb, out, M, N, K, stream, 1, nullptr, 32, aux);
         if (rc >= 0) return rc;
+        if (kAccOut) return WS_ERR_SHAPE;
         cfg = (M <= 16) ? 0 : 1;
     }
     switch (cfg) {
@@ -1267,6 +1276,13 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         default:
             return WS_ERR_INVALID_ARG;
     }
+}
+
+// C = C + (aux + A.B^T), UE8M0 32 x 32 weight scales (the engine's
+// acc_f32 pair after a GEMM, in the GEMM's epilogue: the same bits)
+int fp8_gemm_acc2(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                  float *c, const float *aux, int64_t m, int64_t n, int64_t k, hipStream_t stream) {
+    return gemm_dispatch<false, kUe8m0, kOutAcc2>(a, sa, b, sb, c, m, n, k, stream, 32, aux);
 }
 
 }  // namespace ws
@@ -1304,6 +1320,11 @@ int ws_set_gemm_workspace(void *workspace, size_t bytes, ws_stream_t stream) {
 int ws_fp8_gemm(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
                 float *out, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
     return gemm_dispatch<false, kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream);
+}
+
+int ws_fp8_gemm_acc(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                    float *c, int64_t m, int64_t n, int64_t k, ws_stream_t stream) {
+    return gemm_dispatch<false, kUe8m0, kOutAcc>(a, sa, b, sb, c, m, n, k, stream);
 }
 
 int ws_fp8_gemm_tile(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,

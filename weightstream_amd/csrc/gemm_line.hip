@@ -56,7 +56,7 @@ template <int MT, int NT, int WMH, int D, int SMODE, int OMODE, bool EXACT>
 __global__ __launch_bounds__(256) void gemm_line_kernel(const uint8_t *A, const void *SA,
                                                         const uint8_t *B, const void *SB,
                                                         void *__restrict__ C, int M, int N, int K,
-                                                        int nrb, int xcd_map) {
+                                                        int nrb, int xcd_map, const float *aux) {
     using G = LineGeom<MT, NT, WMH>;
     constexpr int KQ = G::KQ, KS = G::KS, MF = G::MF, NJ = G::NJ;
     extern __shared__ __align__(16) uint8_t ln_lds[];
@@ -279,15 +279,18 @@ __global__ __launch_bounds__(256) void gemm_line_kernel(const uint8_t *A, const 
         for (int v = 0; v < 4; v++) {
             const int row = row0 + v;
             if (row >= M) break;
-            if (OMODE == kOutF32) ((float *)C)[(size_t)row * N + col] = o4[v];
-            else ((uint16_t *)C)[(size_t)row * N + col] = f32_to_bf16(o4[v]);
+            const size_t at = (size_t)row * N + col;
+            if (OMODE == kOutF32) ((float *)C)[at] = o4[v];
+            else if (OMODE == kOutBf16) ((uint16_t *)C)[at] = f32_to_bf16(o4[v]);
+            else if (OMODE == kOutAcc) ((float *)C)[at] = ((float *)C)[at] + o4[v];
+            else ((float *)C)[at] = ((float *)C)[at] + (aux[at] + o4[v]);
         }
     }
 }
 
 template <int MT, int NT, int WMH, int D, int SMODE, int OMODE>
 static int launch_line_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb,
-                           void *out, int m, int n, int k, hipStream_t stream) {
+                           void *out, int m, int n, int k, hipStream_t stream, const float *aux) {
     using G = LineGeom<MT, NT, WMH>;
     static_assert(G::lds_bytes(D) <= 160 * 1024, "stages must fit the LDS");
     if (n % NT || k % G::KS) return -1;
@@ -296,10 +299,12 @@ static int launch_line_cfg(const uint8_t *a, const void *sa, const uint8_t *b, c
     const int xcd = (grid % 8 == 0 && (grid / 8) % nrb == 0) ? 1 : 0;
     if (math_mode() == WS_MATH_NATIVE)
         hipLaunchKernelGGL((gemm_line_kernel<MT, NT, WMH, D, SMODE, OMODE, false>), dim3(grid),
-                           dim3(256), G::lds_bytes(D), stream, a, sa, b, sb, out, m, n, k, nrb, xcd);
+                           dim3(256), G::lds_bytes(D), stream, a, sa, b, sb, out, m, n, k, nrb, xcd,
+                           aux);
     else
         hipLaunchKernelGGL((gemm_line_kernel<MT, NT, WMH, D, SMODE, OMODE, true>), dim3(grid),
-                           dim3(256), G::lds_bytes(D), stream, a, sa, b, sb, out, m, n, k, nrb, xcd);
+                           dim3(256), G::lds_bytes(D), stream, a, sa, b, sb, out, m, n, k, nrb, xcd,
+                           aux);
     return launch_status();
 }
 
@@ -308,27 +313,36 @@ static int launch_line_cfg(const uint8_t *a, const void *sa, const uint8_t *b, c
 // -1 (the caller runs another kernel).
 template <int SMODE, int OMODE>
 static int launch_line(const uint8_t *a, const void *sa, const uint8_t *b, const void *sb, void *out,
-                       int m, int n, int k, hipStream_t stream, int cfg) {
+                       int m, int n, int k, hipStream_t stream, int cfg, const float *aux) {
     switch (cfg) {
         // 64 x 32 tiles, 4 waves on the 4 sub-steps of 512-K stages, 3 stages
-        case 0: return launch_line_cfg<64, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
+        case 0: return launch_line_cfg<64, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream, aux);
         // 32 x 32 tiles (four row blocks per column block on one XCD), 3 stages
-        case 2: return launch_line_cfg<32, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
+        case 2: return launch_line_cfg<32, 32, 1, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream, aux);
         // 128 x 48 tiles (two 64-row halves x two K sub-steps of 256-K
         // stages), 3 stages: wide N (M=128, N=12288)
-        case 4: return launch_line_cfg<128, 48, 2, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream);
+        case 4: return launch_line_cfg<128, 48, 2, 3, SMODE, OMODE>(a, sa, b, sb, out, m, n, k, stream, aux);
         default: return -1;
     }
 }
 
 int line_gemm(int smode, int omode, const uint8_t *a, const void *sa, const uint8_t *b,
-              const void *sb, void *out, int m, int n, int k, hipStream_t stream, int cfg) {
+              const void *sb, void *out, int m, int n, int k, hipStream_t stream, int cfg,
+              const float *aux) {
     if (smode == kUe8m0) {
-        return omode == kOutF32 ? launch_line<kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream, cfg)
-                                : launch_line<kUe8m0, kOutBf16>(a, sa, b, sb, out, m, n, k, stream, cfg);
+        switch (omode) {
+            case kOutF32: return launch_line<kUe8m0, kOutF32>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+            case kOutBf16: return launch_line<kUe8m0, kOutBf16>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+            case kOutAcc: return launch_line<kUe8m0, kOutAcc>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+            case kOutAcc2: return launch_line<kUe8m0, kOutAcc2>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+            default: return -1;
+        }
     }
-    return omode == kOutF32 ? launch_line<kF32s, kOutF32>(a, sa, b, sb, out, m, n, k, stream, cfg)
-                            : launch_line<kF32s, kOutBf16>(a, sa, b, sb, out, m, n, k, stream, cfg);
+    switch (omode) {
+        case kOutF32: return launch_line<kF32s, kOutF32>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+        case kOutBf16: return launch_line<kF32s, kOutBf16>(a, sa, b, sb, out, m, n, k, stream, cfg, aux);
+        default: return -1;
+    }
 }
 
 }  // namespace ws

@@ -184,13 +184,29 @@ int ws_shared_expert_fp8_w13_acc(const float *x, const uint8_t *w13, const uint8
         if (rc) return rc;
         return kp_gemv_fused(kGemvAcc2, hf, w2, s2, h, yr, 0.0f, m, dim, inter, stream);
     }
-    float *ys = (float *)(ws + l.y);
-    int rc = ws_shared_expert_fp8_w13(x, w13, s13, w2, s2, ys, m, dim, inter, swiglu_limit,
-                                      workspace, workspace_bytes, stream);
+    // ws_shared_expert_fp8_w13, its down GEMM adding into h in the epilogue
+    // (h = h + (yr + ys): the acc_f32 pair's bits); x may be h (x is
+    // quantised first)
+    uint8_t *xq = ws + l.xq, *xs = ws + l.xs, *hq = ws + l.hq, *hs = ws + l.hs;
+    float *gu = (float *)(ws + l.g);
+    int rc = ws_emit8(x, xq, xs, m * dim, stream);
     if (rc) return rc;
-    const int64_t n = m * dim;
-    hipLaunchKernelGGL(acc2_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                       ys, yr, h, n);
+    rc = ws_fp8_gemm(xq, xs, w13, s13, gu, m, 2 * inter, dim, stream);
+    if (rc) return rc;
+    const int64_t n = m * inter;
+    hipLaunchKernelGGL(swiglu_emit8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       gu, gu + inter, hq, hs, n, (int)inter, (int)(2 * inter), swiglu_limit);
+    rc = launch_status();
+    if (rc) return rc;
+    rc = fp8_gemm_acc2(hq, hs, w2, s2, h, yr, m, dim, inter, stream);
+    if (rc != WS_ERR_SHAPE) return rc;
+    // shapes the accumulating kernels do not take: the GEMM, then the adds
+    float *ys = (float *)(ws + l.y);
+    rc = ws_fp8_gemm(hq, hs, w2, s2, ys, m, dim, inter, stream);
+    if (rc) return rc;
+    const int64_t nd = m * dim;
+    hipLaunchKernelGGL(acc2_f32_kernel, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, stream,
+                       ys, yr, h, nd);
     return launch_status();
 }
 

@@ -44,6 +44,10 @@ int gate_w13_launch(const float *h, const float *gw, float *logits, const uint8_
 // gemm_line.hip: the FP8 GEMM for row blocks of 33-128 rows with whole-K
 // tiles (configuration cfg); -1 when the shape does not fit that tiling.
 int line_gemm(int smode, int omode, const uint8_t *a, const void *sa, const uint8_t *b,
-              const void *sb, void *out, int m, int n, int k, hipStream_t stream, int cfg);
+              const void *sb, void *out, int m, int n, int k, hipStream_t stream, int cfg,
+              const float *aux = nullptr);
+// C = C + (aux + A.B^T) with UE8M0 32 x 32 weight scales (gemm.hip)
+int fp8_gemm_acc2(const uint8_t *a, const uint8_t *sa, const uint8_t *b, const uint8_t *sb,
+                  float *c, const float *aux, int64_t m, int64_t n, int64_t k, hipStream_t stream);
 
 }  // namespace ws

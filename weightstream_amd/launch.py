@@ -178,6 +178,12 @@ def fp8_gemm(a, sa, b, sb, out, m, n, k, stream=None):
     _call("ws_fp8_gemm", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(out), m, n, k, _s(stream))
 
 
+def fp8_gemm_acc(a, sa, b, sb, c, m, n, k, stream=None):
+    """c += a . b^T (fp8_gemm then acc_f32, launch.rs:717-742 and :1175-1179,
+    the add in the GEMM's epilogue: the same bits)."""
+    _call("ws_fp8_gemm_acc", _ptr(a), _ptr(sa), _ptr(b), _ptr(sb), _ptr(c), m, n, k, _s(stream))
+
+
 def fp8_gemm_on(a, sa, b, sb, out, m, n, k, stream):
     fp8_gemm(a, sa, b, sb, out, m, n, k, stream=stream)
 
