@@ -506,7 +506,9 @@ def bench_block(L, torch, dev, packed, gen, Ms=(1, 8, 64), layers=4, reps=8):
     logits' launch (ws_moe_gate_shared_w13) and its down GEMV in the routed
     gate/up launch, the adds at the end of the routed down kernel
     (ws_moe_decode_route_shared): four launches per layer, the unfused
-    chain's bits. Routed layers 2..4 are device copies of layer 1's packed
+    chain's bits. For M > 1 the out-projection's residual add runs in its
+    GEMM's epilogue (ws_fp8_gemm_acc) and the shared expert's adds in its down
+    GEMM's (ws_shared_expert_fp8_w13_acc), the same bits. Routed layers 2..4 are device copies of layer 1's packed
     experts (distinct memory, so no layer reads another's weights from
     cache). Reported per layer; bytes = weights touched once."""
     import numpy as np
