@@ -159,6 +159,58 @@ def test_moe_prefill_matches_oracle(m, E, dim, inter, k, check):
         _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
 
 
+@pytest.mark.parametrize("m,check", [(132, 12), (300, 12), (4500, 8)])
+def test_prefill_all_routes_on_k_experts(m, check):
+    """Every token picks the same k experts (their bias lifts them above the
+    rest; the routing weights still vary per token), so each expert holds m
+    routes: ceil(m / 32) tiles, pairs of full tiles and a ragged last one in
+    the expert-stationary groups (m = 132: 5 tiles per expert, groups of
+    2, 2, 1; m = 300: 10 tiles, five full pairs, the last tile 12 rows). At
+    m = 4500 the tile capacity exceeds what the stationary bodies take and
+    the tile-streaming pair runs 141 tiles per expert."""
+    E, dim, inter, k = 64, 2048, 1024, 8
+    rng = np.random.default_rng(1700 + m)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(1700 + m)
+    announce("moe_prefill all routes on %d experts m=%d" % (k, m))
+    slabs = _slabs(gen, E, dim, inter)
+    hot = rng.choice(E, k, replace=False)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    bias[hot] += 10.0
+    logits = rng.standard_normal((m, E)).astype(np.float32)
+    idx = torch.empty((m, k), dtype=torch.int32, device=DEV)
+    w = torch.empty((m, k), dtype=torch.float32, device=DEV)
+    L.moe_topk(dev(logits), dev(bias), None, idx, w, m, E, k, O.SCORE_SIGMOID, 1.0, True, 1.0)
+    gi = host(idx)
+    assert sorted(set(gi.ravel().tolist())) == sorted(hot.tolist())
+    x = rng.standard_normal((m, dim)).astype(np.float32)
+    ws = torch.empty(L.moe_prefill_workspace_size(m, dim, inter, k, E), dtype=torch.uint8,
+                     device=DEV)
+    y = torch.empty((m, dim), dtype=torch.float32, device=DEV)
+    L.moe_prefill(dev(x), idx, w, *_packed(slabs, E, dim, inter), y, m, dim, inter, E, k, ws)
+    want_choice = _stationary_expected(idx, E, dim, inter)
+    assert want_choice == (1 if m <= 300 else None)
+    if want_choice is not None:
+        got = _stationary_choice(ws, m, dim, k, E)
+        print("[all routes on k experts m=%d] %s bodies" %
+              (m, "expert-stationary" if got else "tile-streaming"), flush=True)
+        assert got == want_choice
+    gw, gy = host(w), host(y)
+    # the first and last rows (first and last tile of every expert) and
+    # rows spread between them
+    rows = np.linspace(0, m - 1, check).astype(int)
+    H = _host_experts(slabs, hot, E, dim, inter)
+    staged = None
+    for r in rows:
+        want = O.moe_routed(*H, dim, inter, x[r], gi[r], gw[r])
+        if rel_err_stats(gy[r], want)[0] <= MOE_TOL:
+            assert_close(gy[r], want, MOE_TOL, "moe_prefill row %d" % r)
+            continue
+        if staged is None:
+            staged = _staged_hidden(x, idx, w, _packed(slabs, E, dim, inter), m, E, dim, inter, k)
+        _check_by_stages(gy[r], x[r], gi[r], gw[r], H, staged, r, k, dim, inter)
+
+
 def _fp4_normal_slab(gen, E, rows, cols, chunk=64):
     """E expert matrices [rows, cols] drawn N(0, 0.02) and encoded e2m1 +
     UE8M0 per 1x32 on the device (the BASELINE weight recipe)."""
