@@ -1156,6 +1156,7 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
 
     // ---- issue side: the unit whose steps are being loaded
     int ri_i = 0, s_i = 0, Ti = 1;
+    int cmask = 1;            // bit j: this wave copies rows of tile j (some hold routes)
     es_rsrc wr[2], sr[2];     // the unit's expert matrices (gate/up: w1, w3; down: w2)
     uint32_t bo[2], so[2];    // this lane's byte offsets of step 0 per band (weights, scales)
     uint32_t ao[kTG];         // this lane's A row offset per tile (rows 4w .. 4w + 3)
@@ -1178,6 +1179,16 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         const int v = __builtin_amdgcn_readfirstlane(es_lds_word(&grp_l[k / NCG]));
         const int cg = k % NCG, t0 = v & 0xFFFF, e = v >> 19;
         Ti = (v >> 16) & 7;
+        // a tile's routes fill its rows from row 0, so rows 4w .. 4w + 3 of
+        // a tile with at most 4w routes are padding: their LDS rows keep
+        // whatever they held, which reaches no output (a padding row's
+        // results are neither stored nor part of a block maximum, and an
+        // MFMA output column depends on its own A row only)
+        const int nri = __builtin_amdgcn_readfirstlane(es_lds_word(&nrl_l[k / NCG]));
+        cmask = 0;
+#pragma unroll
+        for (int j = 0; j < kTG; j++)
+            if (j < Ti && ((nri >> (8 * j)) & 0xFF) > 4 * w) cmask |= 1 << j;
 #pragma unroll
         for (int m = 0; m < 2; m++) {
             wr[m] = es_buf((m == 0 || MODE == 1 ? a.wa : a.wb) + (size_t)e * wmat, wmat);
@@ -1207,9 +1218,9 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         }
         pre_order(ri_i + 1);
     };
-    int nT[kRing];  // tiles of the step in each ring slot: its copies
+    int nT[kRing];  // this wave's copies of the step in each ring slot
     // the loads of the next step of the stream (its unit opened) into
-    // register slot x and ring slot `slot`: 2 + Ti per wave. Past the end
+    // register slot x and ring slot `slot`: 2 + popcount(cmask) per wave. Past the end
     // of the stream (real == false) the last step's loads are repeated and
     // not used, so that every step has the same loads in flight after it.
     auto issue = [&](EsStep &x, int slot, bool real) {
@@ -1222,9 +1233,9 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
         const uint32_t lb = ring + slot * kSlotB + 4 * w * kRowB;
 #pragma unroll
         for (int j = 0; j < kTG; j++)
-            if (j < Ti)  // uniform: the tiles the group has
+            if ((cmask >> j) & 1)  // uniform: tiles the group has, rows with routes
                 es_dma(abuf, ao[j] + (uint32_t)s_i * kRowB, lb + j * kTile * kRowB, 16);
-        nT[slot] = Ti;
+        nT[slot] = __builtin_popcount(cmask);
         if (real && ++s_i == NS) {
             s_i = 0;
             ri_i++;
@@ -1430,11 +1441,11 @@ __device__ __forceinline__ void es_body(const EsArgs &a, uint8_t *g_lds) {
     auto step = [&](EsStep &x, EsStep &next, int u, int q) {
         if ((u & 1) == 0) {
             // steps q and q + 1 have landed: at most the newer loads are in
-            // flight (four steps of 2 + T loads, and two or one scale blocks
-            // of two words)
+            // flight (four steps of 2 loads and 0 .. T copies, and two or one
+            // scale blocks of two words)
             const int n = 8 + nT[(u + 2) % kRing] + nT[(u + 3) % kRing] + nT[(u + 4) % kRing] +
                           nT[(u + 5) % kRing] + ((u & 3) == 0 ? 4 : 2);
-            es_wait_vm<8 + 4 + 2, 8 + 4 * kTG + 4>(n);
+            es_wait_vm<8 + 2, 8 + 4 * kTG + 4>(n);
             raw_barrier();  // every wave's copies of both steps are in LDS
         }
         const bool real = q + kAhead < total;
