@@ -1060,11 +1060,7 @@ static int sk_set(hipStream_t stream, uint8_t *ptr, size_t bytes) {
 static int pipe_splits(int M, int N, int K, int BN, size_t ws_bytes) {
     const int ksteps = K / 128;
     const int tiles = ((M + kPM - 1) / kPM) * ((N + BN - 1) / BN);
-    static const int forced = [] {
-        const char *e = getenv("WS_PIPE_S");
-        return e ? atoi(e) : 0;
-    }();
-    int S = forced > 0 ? forced : cu_count() / tiles;
+    int S = cu_count() / tiles;
     const int smin = (ksteps + kPMaxSteps - 1) / kPMaxSteps;
     if (S < smin) S = smin;
     if (S > ksteps) S = ksteps;
@@ -1074,13 +1070,8 @@ static int pipe_splits(int M, int N, int K, int BN, size_t ws_bytes) {
 }
 
 // Tile width of the pipelined kernel for (M, N): 256 columns when that still
-// gives every eighth CU a tile, else 64; WS_PIPE_BN forces 64, 128 or 256.
+// gives every eighth CU a tile, else 64.
 static int pipe_bn(int M, int N) {
-    static const int forced = [] {
-        const char *e = getenv("WS_PIPE_BN");
-        return e ? atoi(e) : 0;
-    }();
-    if (forced == 64 || forced == 128 || forced == 256) return forced;
     const int mt = (M + kPM - 1) / kPM;
     // measured at M=128, K=4096: 256 wins at N=12288, 64 at N=4096 and 2048
     // (fewer partial bytes per split than 128)
@@ -1127,15 +1118,6 @@ static int launch_cfg(const uint8_t *a, const void *sa, const uint8_t *b, const 
     return launch_status();
 }
 
-// read once per process (a measurement knob, like WS_PIPE_S and WS_PIPE_BN)
-static int forced_cfg() {
-    static const int forced = [] {
-        const char *e = getenv("WS_GEMM_CFG");
-        return e ? atoi(e) : -1;
-    }();
-    return forced;
-}
-
 template <bool BFP4, int SMODE, int OMODE>
 // OMODE kOutAcc (C += A.B^T) and kOutAcc2 (C = C + (aux + A.B^T)) run on the
 // kernels with those epilogues (line, column strips), never split over K.
@@ -1171,17 +1153,9 @@ static int gemm_dispatch(const uint8_t *a, const void *sa, const uint8_t *b, con
         }
         return rc < 0 ? WS_ERR_SHAPE : rc;
     }
-    int cfg = kAccOut ? -1 : forced_cfg();
-    if (cfg < 0) {
+    int cfg = -1;
+    {
         int rc = -1;
-        static const int line_knob = [] {  // measurement knob: force a line-kernel tiling
-            const char *e = getenv("WS_GEMM_LINE");
-            return e ? atoi(e) : -1;
-        }();
-        if (!BFP4 && line_knob >= 0 && M > 16) {
-            rc = line_gemm(SMODE, OMODE, a, sa, b, sb, out, M, N, K, stream, line_knob, aux);
-            if (rc >= 0) return rc;
-        }
         // 1. 32-column strips when they give the chip one round of workgroups:
         // 64-row blocks (M=128, N=4096) or 32-row blocks (M=128, N=2048;
         // M=64, N=4096). Measured at K=4096: 16.4 us (kp) and 10.0 us (A in
